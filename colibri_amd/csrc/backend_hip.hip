@@ -1,0 +1,435 @@
+// backend_hip.hip -- the coli_cuda_* C ABI on gfx950 (libcoli_hip.so).
+//
+// Host side of the drop-in backend: device contexts, resident tensor upload
+// (with the re-layout into MI355X tiles), and the entry points of
+// c/backend_cuda.h. Compute is in gemv.hip (quantized GEMV/GEMM), pipe.hip
+// (router, elementwise) and moe.hip (fused MoE layer).
+#include "coli_hip_internal.h"
+
+#include "coli_backend_abi.h"
+#include "coli_hip_ext.h"
+#include "coli_hip_host.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+DevCtx g_ctx[COLI_CUDA_MAX_DEVICES];
+int g_nctx;
+static std::mutex g_stats_mu;
+static uint64_t g_calls, g_experts, g_rows;
+static double g_h2d_ms, g_kernel_ms, g_d2h_ms;
+
+int hip_ok(hipError_t err, const char *what) {
+    if (err == hipSuccess) return 1;
+    std::fprintf(stderr, "[HIP] %s: %s\n", what, hipGetErrorString(err));
+    (void)hipGetLastError();   // consume the sticky error
+    return 0;
+}
+
+DevCtx *find_ctx(int device) {
+    for (int i = 0; i < g_nctx; i++)
+        if (g_ctx[i].device == device) return &g_ctx[i];
+    return nullptr;
+}
+
+// The current device is per host thread in the HIP runtime; cache it so the
+// expert loop does not pay hipSetDevice per call (c/backend_cuda.cu:139-152).
+static thread_local int g_current_device = -1;
+int select_ctx(DevCtx *ctx) {
+    if (!ctx) return 0;
+    if (g_current_device == ctx->device) return 1;
+    if (!hip_ok(hipSetDevice(ctx->device), "select device")) return 0;
+    g_current_device = ctx->device;
+    return 1;
+}
+
+// Host-forced fault injection (c/backend_cuda.cu:1340-1348).
+static long g_gpu_calls;
+int fault_injected(void) {
+    const char *fa = std::getenv("COLI_GPU_FAIL_AFTER");
+    return fa && g_gpu_calls++ >= std::atol(fa);
+}
+
+// Grow-only device buffer. Growing waits for the stream first, because queued
+// work may still read the old allocation.
+int reserve(DevCtx *ctx, DevBuf *b, size_t bytes, int zero) {
+    if (bytes <= b->cap) return 1;
+    if (b->p) {
+        if (!hip_ok(hipStreamSynchronize(ctx->stream), "reserve sync")) return 0;
+        (void)hipFree(b->p);
+        b->p = nullptr;
+        b->cap = 0;
+    }
+    size_t want = bytes + bytes / 4 + 256;
+    if (!hip_ok(hipMalloc(&b->p, want), "scratch allocation")) return 0;
+    if (zero && !hip_ok(hipMemset(b->p, 0, want), "scratch clear")) return 0;
+    b->cap = want;
+    return 1;
+}
+
+int reserve_pinned(DevCtx *ctx, void **p, size_t *cap, size_t bytes) {
+    if (bytes <= *cap) return 1;
+    if (*p) {
+        if (!hip_ok(hipStreamSynchronize(ctx->stream), "pinned reserve sync")) return 0;
+        (void)hipHostFree(*p);
+        *p = nullptr;
+        *cap = 0;
+    }
+    size_t want = bytes + bytes / 4 + 256;
+    if (!hip_ok(hipHostMalloc(p, want, hipHostMallocDefault), "pinned allocation")) return 0;
+    *cap = want;
+    return 1;
+}
+
+static void free_buf(DevBuf *b) {
+    if (b->p) (void)hipFree(b->p);
+    b->p = nullptr;
+    b->cap = 0;
+}
+
+// ---------------------------------------------------------------------------
+// lifecycle (c/backend_cuda.cu:929-1040)
+// ---------------------------------------------------------------------------
+extern "C" int coli_cuda_init(const int *devices, int count) {
+    int available = 0;
+    if (!devices || count < 1 || count > COLI_CUDA_MAX_DEVICES) return 0;
+    if (!hip_ok(hipGetDeviceCount(&available), "device discovery")) return 0;
+    if (g_nctx) coli_cuda_shutdown();
+    for (int i = 0; i < count; i++) {
+        int device = devices[i];
+        if (device < 0 || device >= available) {
+            std::fprintf(stderr, "[HIP] invalid device %d (available: 0..%d)\n", device, available - 1);
+            g_nctx = 0;
+            return 0;
+        }
+        if (find_ctx(device)) {
+            std::fprintf(stderr, "[HIP] duplicate device %d\n", device);
+            g_nctx = 0;
+            return 0;
+        }
+        DevCtx *ctx = &g_ctx[g_nctx];
+        *ctx = DevCtx();
+        ctx->device = device;
+        g_current_device = -1;
+        if (!select_ctx(ctx)) { g_nctx = 0; return 0; }
+        hipDeviceProp_t prop{};
+        if (!hip_ok(hipGetDeviceProperties(&prop, device), "device properties")) { g_nctx = 0; return 0; }
+        ctx->cu_count = prop.multiProcessorCount;
+        if (!hip_ok(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "stream creation")) {
+            g_nctx = 0;
+            return 0;
+        }
+        if (!reserve(ctx, &ctx->flags, 64 * sizeof(int), 1)) { g_nctx = 0; return 0; }
+        g_nctx++;
+        std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs\n", device, prop.name,
+                     prop.gcnArchName, prop.totalGlobalMem / 1e9, prop.multiProcessorCount);
+    }
+    return 1;
+}
+
+extern "C" void coli_cuda_shutdown(void) {
+    for (int i = 0; i < g_nctx; i++) {
+        DevCtx *ctx = &g_ctx[i];
+        if (!select_ctx(ctx)) continue;
+        (void)hipStreamSynchronize(ctx->stream);
+        DevBuf *bufs[] = {&ctx->x, &ctx->h, &ctx->y, &ctx->g, &ctx->u, &ctx->partial, &ctx->counters,
+                          &ctx->prob, &ctx->iota, &ctx->stage_w, &ctx->stage_s, &ctx->qdq, &ctx->flags,
+                          &ctx->rslot, &ctx->rw, &ctx->tmp_tiles, &ctx->tmp_scales, &ctx->zeros};
+        for (DevBuf *b : bufs) free_buf(b);
+        for (int f = 0; f < 4; f++) {
+            free_buf(&ctx->frag[f].hi);
+            free_buf(&ctx->frag[f].lo);
+            free_buf(&ctx->frag[f].exp);
+        }
+        for (int s = 0; s < COLI_PIPE_SLOTS; s++) free_buf(&ctx->pipe[s]);
+        if (ctx->host_x) (void)hipHostFree(ctx->host_x);
+        if (ctx->host_y) (void)hipHostFree(ctx->host_y);
+        if (ctx->host_prob) (void)hipHostFree(ctx->host_prob);
+        if (ctx->host_small) (void)hipHostFree(ctx->host_small);
+        if (ctx->ev_ok) (void)hipEventDestroy(ctx->ev_done);
+        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+        *ctx = DevCtx();
+    }
+    g_nctx = 0;
+    g_current_device = -1;
+}
+
+extern "C" int coli_cuda_device_count(void) { return g_nctx; }
+extern "C" int coli_cuda_device_at(int index) { return index >= 0 && index < g_nctx ? g_ctx[index].device : -1; }
+
+extern "C" int coli_cuda_mem_info(int device, size_t *free_bytes, size_t *total_bytes) {
+    DevCtx *ctx = find_ctx(device);
+    if (!free_bytes || !total_bytes || !select_ctx(ctx)) return 0;
+    return hip_ok(hipMemGetInfo(free_bytes, total_bytes), "memory info");
+}
+
+extern "C" int coli_cuda_device_integrated(int device) {
+    hipDeviceProp_t prop{};
+    if (!hip_ok(hipGetDeviceProperties(&prop, device), "device properties")) return 0;
+    return prop.integrated ? 1 : 0;
+}
+
+extern "C" void coli_cuda_stats(int device, size_t *tensor_count, size_t *tensor_bytes) {
+    size_t count = 0, bytes = 0;
+    for (int i = 0; i < g_nctx; i++)
+        if (device < 0 || g_ctx[i].device == device) {
+            count += g_ctx[i].tensor_count;
+            bytes += g_ctx[i].tensor_bytes;
+        }
+    if (tensor_count) *tensor_count = count;
+    if (tensor_bytes) *tensor_bytes = bytes;
+}
+
+extern "C" void coli_cuda_group_stats(uint64_t *calls, uint64_t *experts, uint64_t *rows, double *h2d_ms,
+                                      double *kernel_ms, double *d2h_ms) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    if (calls) *calls = g_calls;
+    if (experts) *experts = g_experts;
+    if (rows) *rows = g_rows;
+    if (h2d_ms) *h2d_ms = g_h2d_ms;
+    if (kernel_ms) *kernel_ms = g_kernel_ms;
+    if (d2h_ms) *d2h_ms = g_d2h_ms;
+}
+
+extern "C" void coli_cuda_group_stats_device(int device, uint64_t *calls, uint64_t *experts, uint64_t *rows,
+                                             double *h2d_ms, double *kernel_ms, double *d2h_ms) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    DevCtx *ctx = find_ctx(device);
+    if (calls) *calls = ctx ? ctx->st_calls : 0;
+    if (experts) *experts = ctx ? ctx->st_experts : 0;
+    if (rows) *rows = ctx ? ctx->st_rows : 0;
+    if (h2d_ms) *h2d_ms = ctx ? ctx->st_h2d : 0;
+    if (kernel_ms) *kernel_ms = ctx ? ctx->st_kernel : 0;
+    if (d2h_ms) *d2h_ms = ctx ? ctx->st_d2h : 0;
+}
+
+void note_group(DevCtx *ctx, int count, int total, double h2d, double ker, double d2h) {
+    std::lock_guard<std::mutex> lock(g_stats_mu);
+    g_calls++;
+    g_experts += (uint64_t)count;
+    g_rows += (uint64_t)total;
+    g_h2d_ms += h2d;
+    g_kernel_ms += ker;
+    g_d2h_ms += d2h;
+    ctx->st_calls++;
+    ctx->st_experts += (uint64_t)count;
+    ctx->st_rows += (uint64_t)total;
+    ctx->st_h2d += h2d;
+    ctx->st_kernel += ker;
+    ctx->st_d2h += d2h;
+}
+
+// fmt 6 (E8) and fmt 8 (fp8) are not computed here: the tables are refused
+// so the engine keeps those formats on its CPU path.
+extern "C" int coli_cuda_e8_set_grid(const void *) { return 0; }
+extern "C" int coli_cuda_fp8_set_lut(const float *) { return 0; }
+
+// ---------------------------------------------------------------------------
+// tensors
+// ---------------------------------------------------------------------------
+static int scales_fp16_exact(const float *s, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        float v = s[i];
+        if (!std::isfinite(v)) return 0;
+        _Float16 h = (_Float16)v;
+        if ((float)h != v) return 0;
+    }
+    return 1;
+}
+
+// f32 power-of-two scales -> e8m0 bytes (s with (u32)s << 23 == bits):
+// +0 -> 0, +inf -> 255, 2^(s-127) for s in 1..254; anything else refused.
+static int scales_to_e8(const float *s, size_t n, uint8_t *out) {
+    for (size_t i = 0; i < n; i++) {
+        uint32_t bits;
+        std::memcpy(&bits, &s[i], 4);
+        if (bits & 0x807fffffu) return 0;
+        out[i] = (uint8_t)(bits >> 23);
+    }
+    return 1;
+}
+
+static size_t src_scale_count(int fmt, int I, int O, int gs) {
+    if (fmt == 7) return (size_t)O * ((I + 31) / 32);
+    if (fmt == 4 && gs > 0) return (size_t)O * ((I + gs - 1) / gs);
+    return (size_t)O;
+}
+
+// Copy source bytes to the device and build the tiled layout of t.
+static int fill_tensor(DevCtx *ctx, ColiCudaTensor *t, const void *weights, const void *scales_src,
+                       size_t scale_src_bytes) {
+    size_t rb = (size_t)(t->I + 1) / 2, wsrc = rb * t->O;
+    if (t->kind == COLI_KIND_GENERIC) {
+        if (!hip_ok(hipMemcpy(t->w, weights, wsrc, hipMemcpyHostToDevice), "tensor upload") ||
+            !hip_ok(hipMemcpy(t->sc, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
+            return 0;
+        return 1;
+    }
+    if (!reserve(ctx, &ctx->stage_w, wsrc, 0) || !reserve(ctx, &ctx->stage_s, scale_src_bytes, 0)) return 0;
+    if (!hip_ok(hipStreamSynchronize(ctx->stream), "upload sync") ||
+        !hip_ok(hipMemcpy(ctx->stage_w.p, weights, wsrc, hipMemcpyHostToDevice), "tensor upload") ||
+        !hip_ok(hipMemcpy(ctx->stage_s.p, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
+        return 0;
+    if (!hip_ok(coli_launch_repack(t, (const uint8_t *)ctx->stage_w.p, ctx->stage_s.p, ctx->stream),
+                "tile repack"))
+        return 0;
+    return hip_ok(hipStreamSynchronize(ctx->stream), "tile repack sync");
+}
+
+static ColiCudaTensor *alloc_tensor(DevCtx *ctx, int fmt, int I, int O, int gs, int kind) {
+    ColiCudaTensor *t = (ColiCudaTensor *)std::calloc(1, sizeof(ColiCudaTensor));
+    if (!t) return nullptr;
+    t->fmt = fmt; t->I = I; t->O = O; t->device = ctx->device; t->gs = gs; t->kind = kind;
+    if (kind == COLI_KIND_GENERIC) {
+        t->ng_src = (I + gs - 1) / gs;
+        t->w_bytes = (size_t)(I + 1) / 2 * O;
+        t->sc_bytes = (size_t)O * t->ng_src * sizeof(float);
+    } else {
+        t->Op = (O + 15) / 16 * 16;
+        t->Ip = (I + 127) / 128 * 128;
+        t->nrt = t->Op / 16;
+        t->nq = t->Ip / 128;
+        t->w_bytes = (size_t)t->nrt * t->nq * COLI_TILE_BYTES;
+        size_t per = kind == COLI_KIND_I4_H ? 2 : (kind == COLI_KIND_I4_F ? 4 : 1);
+        t->sc_bytes = (size_t)t->nrt * t->nq * 64 * per;
+    }
+    if (!hip_ok(hipMalloc((void **)&t->w, t->w_bytes), "tensor allocation") ||
+        !hip_ok(hipMalloc(&t->sc, t->sc_bytes), "scale allocation")) {
+        if (t->w) (void)hipFree(t->w);
+        std::free(t);
+        return nullptr;
+    }
+    t->accounted = t->w_bytes + t->sc_bytes;
+    ctx->tensor_count++;
+    ctx->tensor_bytes += t->accounted;
+    return t;
+}
+
+// Upload for fmt 2 / 4 (f32 scales) and fmt 7 (e8 bytes, or f32 powers of two).
+int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scales, const uint8_t *e8,
+                int fmt, int I, int O, int device, int gs) {
+    if (!tensor) return 0;
+    int want_gs = (fmt == 4 && gs > 0) ? gs : (fmt == 7 ? 32 : 0);
+    if (*tensor) {
+        ColiCudaTensor *t = *tensor;
+        return t->fmt == fmt && t->I == I && t->O == O && t->device == device && t->gs == want_gs;
+    }
+    DevCtx *ctx = find_ctx(device);
+    if (!weights || I < 1 || O < 1 || !select_ctx(ctx)) return 0;
+    if (fmt != 2 && fmt != 4 && fmt != 7) return 0;
+    if (fmt == 7) {
+        if (!e8 && !scales) return 0;
+        if (!e8 && gs != 32 && gs != 0) return 0;
+    } else if (!scales) {
+        return 0;
+    }
+    size_t ns = src_scale_count(fmt, I, O, want_gs);
+    std::vector<uint8_t> e8buf;
+    int kind;
+    const void *ssrc;
+    size_t sbytes;
+    if (fmt == 7) {
+        kind = COLI_KIND_FP4;
+        if (!e8) {
+            e8buf.resize(ns);
+            if (!scales_to_e8(scales, ns, e8buf.data())) {
+                std::fprintf(stderr, "[HIP] fmt=7 upload: scales are not exact powers of two\n");
+                return 0;
+            }
+            e8 = e8buf.data();
+        }
+        ssrc = e8;
+        sbytes = ns;
+    } else {
+        if (want_gs > 0 && want_gs % 32) kind = COLI_KIND_GENERIC;
+        else kind = scales_fp16_exact(scales, ns) ? COLI_KIND_I4_H : COLI_KIND_I4_F;
+        ssrc = scales;
+        sbytes = ns * sizeof(float);
+    }
+    ColiCudaTensor *t = alloc_tensor(ctx, fmt, I, O, want_gs, kind);
+    if (!t) return 0;
+    if (!fill_tensor(ctx, t, weights, ssrc, sbytes)) {
+        coli_cuda_tensor_free(t);
+        return 0;
+    }
+    *tensor = t;
+    return 1;
+}
+
+extern "C" int coli_cuda_tensor_upload_g(ColiCudaTensor **tensor, const void *weights, const float *scales,
+                                         int fmt, int I, int O, int device, int gs) {
+    return upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, gs > 0 ? gs : 0);
+}
+
+extern "C" int coli_cuda_tensor_upload(ColiCudaTensor **tensor, const void *weights, const float *scales,
+                                       int fmt, int I, int O, int device) {
+    return upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, fmt == 7 ? 32 : 0);
+}
+
+extern "C" int coli_hip_tensor_upload_mxfp4(ColiCudaTensor **tensor, const unsigned char *q4,
+                                            const unsigned char *e8, int I, int O, int device) {
+    if (!e8) return 0;
+    return upload_impl(tensor, q4, nullptr, e8, 7, I, O, device, 32);
+}
+
+extern "C" int coli_hip_tensor_upload_fp4_rows16(ColiCudaTensor **tensor, const unsigned char *pd,
+                                                 const unsigned char *ps, int I, int O, int device) {
+    if (!tensor || *tensor || !pd || !ps || O < 16 || O % 16 || I < 128 || I % 128) return 0;
+    // Undo the 16-row interleave (c/deepseek_v4.c:10975-10993) on the host,
+    // then take the row-major path.
+    size_t ds = (size_t)I / 2, ss = (size_t)I / 32;
+    std::vector<uint8_t> q4((size_t)O * ds), e8((size_t)O * ss);
+    for (size_t r = 0; r < (size_t)O; r++) {
+        size_t tile = r / 16, lane = r % 16;
+        for (size_t c = 0; c < ds; c++) q4[r * ds + c] = pd[(tile * ds + c) * 16 + lane];
+        for (size_t c = 0; c < ss; c++) e8[r * ss + c] = ps[(tile * ss + c) * 16 + lane];
+    }
+    return upload_impl(tensor, q4.data(), nullptr, e8.data(), 7, I, O, device, 32);
+}
+
+extern "C" void coli_cuda_tensor_free(ColiCudaTensor *t) {
+    if (!t) return;
+    DevCtx *ctx = find_ctx(t->device);
+    if (ctx) {
+        select_ctx(ctx);
+        (void)hipStreamSynchronize(ctx->stream);
+        if (ctx->tensor_count) ctx->tensor_count--;
+        if (ctx->tensor_bytes >= t->accounted) ctx->tensor_bytes -= t->accounted;
+    }
+    if (t->w) (void)hipFree(t->w);
+    if (t->sc) (void)hipFree(t->sc);
+    std::free(t);
+}
+
+extern "C" size_t coli_cuda_tensor_bytes(const ColiCudaTensor *t) { return t ? t->w_bytes + t->sc_bytes : 0; }
+extern "C" int coli_cuda_tensor_device(const ColiCudaTensor *t) { return t ? t->device : -1; }
+extern "C" size_t coli_hip_tensor_stream_bytes(const ColiCudaTensor *t) { return t ? t->w_bytes + t->sc_bytes : 0; }
+extern "C" int coli_hip_tensor_kind(const ColiCudaTensor *t) { return t ? t->kind : -1; }
+
+extern "C" int coli_cuda_tensor_update(ColiCudaTensor *t, const void *weights, const float *scales) {
+    if (!t || !weights || !scales) return 0;
+    DevCtx *ctx = find_ctx(t->device);
+    if (!select_ctx(ctx)) return 0;
+    size_t ns = src_scale_count(t->fmt, t->I, t->O, t->gs);
+    if (t->kind == COLI_KIND_FP4) {
+        std::vector<uint8_t> e8(ns);
+        if (!scales_to_e8(scales, ns, e8.data())) return 0;
+        return fill_tensor(ctx, t, weights, e8.data(), ns);
+    }
+    // The storage kind was fixed at upload: fp16 storage needs fp16-exact scales.
+    if (t->kind == COLI_KIND_I4_H && !scales_fp16_exact(scales, ns)) {
+        std::fprintf(stderr, "[HIP] tensor_update: scales no longer fp16-exact for an fp16-scale tensor\n");
+        return 0;
+    }
+    return fill_tensor(ctx, t, weights, scales, ns * sizeof(float));
+}
+
+extern "C" void *coli_hip_stream(int device) {
+    DevCtx *ctx = find_ctx(device);
+    return ctx ? (void *)ctx->stream : nullptr;
+}

@@ -1,0 +1,86 @@
+// coli_hip_host.h -- host-side state of the gfx950 backend (not part of the ABI).
+#pragma once
+
+#include "coli_hip_internal.h"
+
+#include <stdint.h>
+
+#define COLI_PIPE_SLOTS 27
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+// Activation fragments of one kind of input (see coli_prep_frag in gemv.hip).
+struct FragSet {
+    DevBuf hi, lo, exp;
+};
+
+struct DevCtx {
+    int device = -1;
+    int cu_count = 0;
+    hipStream_t stream = nullptr;
+    size_t tensor_count = 0, tensor_bytes = 0;
+    // grow-only scratch
+    DevBuf x, h, y, g, u, partial, counters, prob, iota, zeros, stage_w, stage_s, qdq, flags;
+    DevBuf rslot, rw, tmp_tiles, tmp_scales;
+    FragSet frag[4];                   // 0/1: inputs (int4 / fp4 order), 2/3: hidden rows
+    DevBuf pipe[COLI_PIPE_SLOTS];
+    // pinned staging
+    void *host_x = nullptr, *host_y = nullptr, *host_prob = nullptr, *host_small = nullptr;
+    size_t host_x_cap = 0, host_y_cap = 0, host_prob_cap = 0, host_small_cap = 0;
+    int group_pending = 0;
+    hipEvent_t ev_done = nullptr;
+    int ev_ok = 0;
+    // statistics
+    uint64_t st_calls = 0, st_experts = 0, st_rows = 0;
+    double st_h2d = 0, st_kernel = 0, st_d2h = 0;
+};
+
+extern DevCtx g_ctx[];
+extern int g_nctx;
+
+int hip_ok(hipError_t err, const char *what);
+DevCtx *find_ctx(int device);
+int select_ctx(DevCtx *ctx);
+int fault_injected(void);
+int reserve(DevCtx *ctx, DevBuf *b, size_t bytes, int zero);
+int reserve_pinned(DevCtx *ctx, void **p, size_t *cap, size_t bytes);
+void note_group(DevCtx *ctx, int count, int total, double h2d, double ker, double d2h);
+int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scales, const uint8_t *e8,
+                int fmt, int I, int O, int device, int gs);
+
+// kernels (gemv.hip / pipe.hip)
+extern "C" {
+hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, int max_rows, hipStream_t st);
+hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, const int *nrows_dev,
+                                 int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
+                                 int *exp2out, int *haslo, hipStream_t st);
+hipError_t coli_launch_repack(const ColiCudaTensor *t, const uint8_t *src_w, const void *src_s,
+                              hipStream_t st);
+hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const float *x, int ldx, float *y, int ldy,
+                                  int S, hipStream_t st);
+hipError_t coli_launch_qdq_e4m3(const float *x, float *y, int S, int K, hipStream_t st);
+hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E, float *logits,
+                                     hipStream_t st);
+hipError_t coli_launch_router_select(const float *logits, const float *bias, int S, int E, int K, int mode,
+                                     float topp, int norm_topk, float routed_scale, int *idx, float *w,
+                                     int *keff, hipStream_t st);
+hipError_t coli_launch_zero_i32(int *p, int n, hipStream_t st);
+hipError_t coli_launch_silu_mul(float *gate, const float *up, size_t n, hipStream_t st);
+hipError_t coli_launch_silu_mul_to(float *h, const float *gate, const float *up, size_t n, hipStream_t st);
+hipError_t coli_launch_add_n(float *x, const float *t, size_t n, hipStream_t st);
+hipError_t coli_launch_rows_add(float *x, const float *partial, const int *rows, int nrows, int D,
+                                hipStream_t st);
+hipError_t coli_launch_weighted_sum_rows(float *out, const float *y, const float *w, int count, int D,
+                                         hipStream_t st);
+hipError_t coli_launch_sum_slots(float *dst, const float *slots, int n, int D, hipStream_t st);
+}
+
+// Expert path runner (expert.hip): one shared routine behind expert_group,
+// issue, expert_mlp, resident_issue and the MoE layer.
+struct GemvLaunchPlan {
+    int R, rbpp, splits, qps;
+};
+GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual);

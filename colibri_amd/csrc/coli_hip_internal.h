@@ -1,0 +1,78 @@
+// coli_hip_internal.h -- shared types of the gfx950 backend (libcoli_hip.so).
+//
+// Device data layout ("MI355X tiles"), chosen at upload time:
+//   A quantized matrix W[O, I] (int4 offset-binary or e2m1 nibbles) is padded
+//   to Op = ceil16(O) rows and Ip = ceil128(I) columns and cut into tiles of
+//   16 rows x 128 columns (4 groups of 32). A tile is 1 KiB; within it, lane l
+//   of a wave owns the 16 bytes at l*16: dword j holds the 8 nibbles of row
+//   (l % 16), columns [32*(4q+j) + 8*(l/16), +8) in the source byte order.
+//   One global_load_dwordx4 per lane therefore streams a whole tile with
+//   perfect coalescing, and every nibble lands in the lane that feeds it to
+//   the MFMA B operand. Tiles are ordered [row_tile][quad] so a wave walking K
+//   for one row tile reads contiguous memory.
+//   Group scales are stored tile-ordered as well: [row_tile][quad][16][4] of
+//   fp16 (int4 whose f32 scales are exactly fp16), f32 (other int4), or e8m0
+//   bytes (MXFP4). Padding carries value 0 (nibble 8 / code 0, scale 0).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define COLI_TILE_ROWS 16
+#define COLI_TILE_COLS 128
+#define COLI_TILE_BYTES 1024
+#define COLI_GROUP 32
+
+// Tensor storage kinds.
+enum ColiKind {
+    COLI_KIND_I4_H = 0,     // int4, fp16 group scales (tiled)
+    COLI_KIND_I4_F = 1,     // int4, f32 group scales (tiled)
+    COLI_KIND_FP4 = 2,      // MXFP4 e2m1 + e8m0 (tiled)
+    COLI_KIND_GENERIC = 3,  // int4 with a group size that is not a multiple of 32:
+                            // source layout kept, scalar kernel
+};
+
+struct ColiCudaTensor {
+    int fmt, I, O, device, gs;   // ABI view (fmt as passed, gs 0 = per-row)
+    int kind;
+    int Op, Ip, nrt, nq;         // tiled geometry
+    uint8_t *w;                  // tiles (or raw rows for GENERIC)
+    void *sc;                    // scale tiles (or raw f32 [O, ng] for GENERIC)
+    size_t w_bytes, sc_bytes;
+    int ng_src;                  // scale groups per source row (GENERIC)
+    size_t accounted;            // bytes charged to the device statistics
+};
+
+// One GEMV problem: a matrix (or a gate/up pair) applied to a set of batch rows.
+struct ColiProb {
+    const uint8_t *w0;  const void *s0;   // matrix (plain) or gate (dual)
+    const uint8_t *w1;  const void *s1;   // up (dual)
+    int nrows;                            // batch rows of this problem
+    int xrow_off;                         // -> xrows[]: fragment row per batch row
+    int out_row0;                         // first output row (rows are consecutive)
+    int pad;
+};
+
+struct ColiGemvArgs {
+    const ColiProb *prob;
+    const int *nprob_dev;     // if non-null, number of live problems (device)
+    int nprob;                // upper bound (grid sizing)
+    int nrt, nq, O;           // tiles, real output rows
+    int n_bt;                 // 16-row batch tiles per problem
+    int rb_per_prob;          // row blocks per problem
+    int splits, qps;          // K split
+    const int *xrows;
+    const _Float16 *xhi, *xlo;
+    int xstride;              // halves per fragment row (= ngp * 32)
+    const int *xexp;          // per fragment row
+    const int *haslo;
+    float *out;
+    int ldo;
+    float *partial;
+    unsigned *counters;
+};
+
+
+// Numeric helpers shared by host and device.
+static inline int coli_ceil_div(int a, int b) { return (a + b - 1) / b; }

@@ -1,0 +1,553 @@
+// gemv.hip -- dequant-fused quantized expert GEMV/GEMM for gfx950 (CDNA4).
+//
+// y[b, o] = sum_g scale[o, g] * sum_{k in g} x[b, k] * w[o, k]
+//
+// int4-g32 (fmt=4/2; w = nibble - 8, c/quant.h:168-202) and MXFP4 (fmt=7;
+// w = e2m1, scale = e8m0 via (u32)s << 23, c/quant.h:1391-1440) share one
+// kernel skeleton, built for the HBM roofline of batch 1..16 decode:
+//
+//  * Weights stream once from HBM as 1 KiB tiles (16 rows x 128 columns), one
+//    global_load_dwordx4 per lane per tile (see coli_hip_internal.h).
+//  * Each 32-column group is one v_mfma_f32_16x16x32_f16: A = activations
+//    (batch rows in M, zero-padded to 16), B = the weight group unpacked in
+//    registers to exact fp16 values, so the per-group scale is applied once
+//    per (row, batch) output instead of once per weight.
+//      int4: v_perm_b32 drops each nibble into the mantissa of 1024.0 (low
+//            nibbles) or at 16x (high nibbles), one v_pk_add_f16 removes the
+//            1032 / 1152 bias -> exact (u-8) and 16(u-8); the activation of the
+//            high-nibble columns is pre-scaled by 1/16 (exact).
+//      fp4:  v_cvt_scalef32_pk_f16_fp4 (scale 1.0) decodes two codes per op.
+//  * Activations arrive as fp16 hi + lo fragments of x * 2^-E (E = per-row
+//    exponent, exact), i.e. ~22 significant bits; the lo MFMA is skipped when
+//    every lo part is zero (bf16-exact inputs).
+//  * Split-K across waves with a deterministic fixed-order reduction by the
+//    last-arriving wave (self-resetting counters, no memset, no atomics on the
+//    data), then fused epilogues: plain store, or SwiGLU (silu(g)*u, the
+//    expression of c/backend_cuda.cu:618-624) for gate/up pairs.
+#include "coli_hip_internal.h"
+
+#include <math.h>
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Upload-time repack kernels
+// ---------------------------------------------------------------------------
+
+// One thread per destination dword. Source: row-major [O][ceil(I/2)] nibbles.
+__global__ void coli_repack_nibbles(const uint8_t *__restrict__ src, int O, int I,
+                                   uint32_t *__restrict__ dst, int nrt, int nq,
+                                   uint32_t pad_nib) {
+    size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t total = (size_t)nrt * nq * 256;
+    if (d >= total) return;
+    int j = (int)(d & 3), lane = (int)((d >> 2) & 63);
+    size_t tile = d >> 8;
+    int q = (int)(tile % nq), rt = (int)(tile / nq);
+    int row = rt * 16 + (lane & 15);
+    int k0 = (4 * q + j) * 32 + 8 * (lane >> 4);
+    size_t rb = (size_t)(I + 1) / 2;
+    uint32_t v = 0;
+    if (row < O && k0 + 8 <= I) {
+        const uint8_t *p = src + (size_t)row * rb + (k0 >> 1);
+        v = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+    } else {
+        for (int t = 0; t < 8; t++) {
+            int k = k0 + t;
+            uint32_t n = pad_nib;
+            if (row < O && k < I) {
+                uint8_t b = src[(size_t)row * rb + (k >> 1)];
+                n = (k & 1) ? (b >> 4) : (b & 15);
+            }
+            v |= n << (4 * t);
+        }
+    }
+    dst[d] = v;
+}
+
+// int4 scales: source f32 [O][ng_src] with group size gs (0 = one per row);
+// gs is a multiple of 32 here, so every 32-column group lies in one source group.
+// Destination tile-ordered [rt][q][16][4] as fp16 (as_half) or f32.
+__global__ void coli_repack_scales_i4(const float *__restrict__ src, int O, int I, int gs,
+                                     void *__restrict__ dst, int nrt, int nq, int as_half) {
+    size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t total = (size_t)nrt * nq * 64;
+    if (d >= total) return;
+    int j = (int)(d & 3), r = (int)((d >> 2) & 15);
+    size_t tile = d >> 6;
+    int q = (int)(tile % nq), rt = (int)(tile / nq);
+    int row = rt * 16 + r, g = 4 * q + j;
+    float v = 0.0f;
+    if (row < O && g * 32 < I) {
+        if (gs <= 0) v = src[row];
+        else {
+            int ng = (I + gs - 1) / gs;
+            v = src[(size_t)row * ng + (g * 32) / gs];
+        }
+    }
+    if (as_half) ((_Float16 *)dst)[d] = (_Float16)v;
+    else ((float *)dst)[d] = v;
+}
+
+// MXFP4 scales: source e8m0 [O][ceil(I/32)], destination [rt][q][16][4] bytes.
+__global__ void coli_repack_scales_e8(const uint8_t *__restrict__ src, int O, int I,
+                                     uint8_t *__restrict__ dst, int nrt, int nq) {
+    size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t total = (size_t)nrt * nq * 64;
+    if (d >= total) return;
+    int j = (int)(d & 3), r = (int)((d >> 2) & 15);
+    size_t tile = d >> 6;
+    int q = (int)(tile % nq), rt = (int)(tile / nq);
+    int row = rt * 16 + r, g = 4 * q + j, ng = (I + 31) / 32;
+    dst[d] = (row < O && g < ng) ? src[(size_t)row * ng + g] : (uint8_t)0;
+}
+
+// ---------------------------------------------------------------------------
+// Activation fragments
+// ---------------------------------------------------------------------------
+// For fragment row r (source row src_row[r] of x, f32 [.., ldx]):
+//   E = exponent with max|x| * 2^-E in [0.5, 1) (0 for an all-zero row),
+//   hi = fp16(x * 2^-E * m), lo = fp16(x * 2^-E * m - hi), m = 1/16 on the
+//   high-nibble columns of the int4 order, else 1.
+// Layout per row: [ngp groups][4 kslices][8 halves]; slot t of kslice s of
+// group g holds column 32g + 8s + perm[t], perm = {0,2,4,6,1,3,5,7} (int4)
+// or identity (fp4), matching the B-operand order built in the GEMV.
+// One 256-thread block per fragment row.
+__global__ void coli_prep_frag(const float *__restrict__ x, int ldx, const int *__restrict__ src_row,
+                               const int *__restrict__ nrows_dev, int nrows_host, int K, int ngp,
+                               int int4_order, _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
+                               int *__restrict__ exp2out, int *__restrict__ haslo) {
+    int r = blockIdx.x;
+    int nrows = nrows_dev ? *nrows_dev : nrows_host;
+    if (r >= nrows) return;
+    int srow = src_row ? src_row[r] : r;
+    if (srow < 0) return;   // unused slot of a padded row set
+    const float *xr = x + (size_t)srow * ldx;
+    __shared__ float red[256];
+    float m = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+    red[threadIdx.x] = m;
+    __syncthreads();
+    for (int s = 128; s; s >>= 1) {
+        if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    m = red[0];
+    int E = 0;
+    if (m > 0.0f && isfinite(m)) frexpf(m, &E);
+    if (threadIdx.x == 0) exp2out[r] = E;
+    size_t base = (size_t)r * ngp * 32;
+    int any_lo = 0;
+    for (int e = threadIdx.x; e < ngp * 32; e += 256) {
+        int g = e >> 5, s = (e >> 3) & 3, t = e & 7;
+        int off = int4_order ? ((t < 4) ? 2 * t : 2 * (t - 4) + 1) : t;
+        int k = g * 32 + 8 * s + off;
+        float v = k < K ? ldexpf(xr[k], -E) : 0.0f;
+        if (int4_order && (off & 1)) v *= 0.0625f;
+        _Float16 h = (_Float16)v;
+        _Float16 l = (_Float16)(v - (float)h);
+        hi[base + e] = h;
+        lo[base + e] = l;
+        any_lo |= (l != (_Float16)0.0f);
+    }
+    if (any_lo) atomicOr(haslo, 1);
+}
+
+// ---------------------------------------------------------------------------
+// GEMV problems
+// ---------------------------------------------------------------------------
+enum { EPI_STORE = 0, EPI_SWIGLU = 1 };
+
+template <int KIND>
+__device__ __forceinline__ half8v unpack_b(uint32_t w) {
+    if constexpr (KIND == COLI_KIND_FP4) {
+        half2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0);
+        half2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1);
+        half2v c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2);
+        half2v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3);
+        return (half8v){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+    } else {
+        uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
+        uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+        uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+        uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+        uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+        const half2v blo = {(_Float16)1032.0f, (_Float16)1032.0f};
+        const half2v bhi = {(_Float16)1152.0f, (_Float16)1152.0f};
+        half2v a = __builtin_bit_cast(half2v, p0) - blo;
+        half2v b = __builtin_bit_cast(half2v, p1) - blo;
+        half2v c = __builtin_bit_cast(half2v, p2) - bhi;
+        half2v d = __builtin_bit_cast(half2v, p3) - bhi;
+        return (half8v){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+    }
+}
+
+// Scale of group j (0..3) of the lane's row, from the per-tile-quad scale word(s).
+template <int KIND> struct ScaleRegs;
+template <> struct ScaleRegs<COLI_KIND_I4_H> {
+    u32x2 v;
+    __device__ void load(const void *base, size_t tq, int r16) {
+        v = *(const u32x2 *)((const uint8_t *)base + (tq * 16 + r16) * 8);
+    }
+    __device__ float get(int j) const {
+        uint32_t wd = v[j >> 1];
+        _Float16 h = __builtin_bit_cast(half2v, wd)[j & 1];
+        return (float)h;
+    }
+    __device__ void zero() { v = (u32x2){0u, 0u}; }
+};
+template <> struct ScaleRegs<COLI_KIND_I4_F> {
+    floatx4 v;
+    __device__ void load(const void *base, size_t tq, int r16) {
+        v = *(const floatx4 *)((const uint8_t *)base + (tq * 16 + r16) * 16);
+    }
+    __device__ float get(int j) const { return v[j]; }
+    __device__ void zero() { v = (floatx4){0.f, 0.f, 0.f, 0.f}; }
+};
+template <> struct ScaleRegs<COLI_KIND_FP4> {
+    uint32_t v;
+    __device__ void load(const void *base, size_t tq, int r16) {
+        v = *(const uint32_t *)((const uint8_t *)base + (tq * 16 + r16) * 4);
+    }
+    __device__ float get(int j) const {
+        return __builtin_bit_cast(float, ((v >> (8 * j)) & 0xFFu) << 23);
+    }
+    __device__ void zero() { v = 0u; }
+};
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return (g / (1.0f + expf(-g))) * u;
+}
+
+// One workgroup (4 waves) = one work item: (problem, batch tile, row block,
+// K split). The 4 waves interleave over the item's quads (wave w takes quads
+// Q0+w, Q0+w+4, ...) so the group streams contiguous tile memory together,
+// then reduce through LDS in fixed wave order. R = row tiles accumulated per
+// wave; DUAL: tiles [0, R/2) come from w0 (gate) and [R/2, R) from w1 (up) over
+// the same rows. NB4 = accumulator rows per lane that can hold real batch rows
+// (1, 2 or 4): the MFMA result row of lane l, register i is batch row
+// 4*(l/16)+i, its column is output row 16*tile + (l%16).
+template <int KIND, int R, bool DUAL, int NB4>
+__global__ __launch_bounds__(256) void coli_gemv_tiles(ColiGemvArgs a) {
+    constexpr int RT = DUAL ? R / 2 : R;
+    __shared__ float red[4][R * 4][64];
+    __shared__ unsigned last_flag;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int item = blockIdx.x;
+    const int items_per_bt = a.rb_per_prob * a.splits;
+    const int items_per_p = a.n_bt * items_per_bt;
+    const int p = item / items_per_p;
+    if (p >= a.nprob) return;
+    if (a.nprob_dev && p >= *a.nprob_dev) return;
+    int rem = item - p * items_per_p;
+    const int bt = rem / items_per_bt;
+    rem -= bt * items_per_bt;
+    const int rb = rem / a.splits;
+    const int s = rem - rb * a.splits;
+    const ColiProb pr = a.prob[p];
+    const int nb = min(16, pr.nrows - 16 * bt);
+    if (nb <= 0) return;
+
+    const int b = lane & 15, ks = lane >> 4;
+    const int Q0 = s * a.qps, Q1 = min(a.nq, Q0 + a.qps);
+    const bool use_lo = *a.haslo != 0;
+
+    const _Float16 *xh = nullptr, *xl = nullptr;
+    if (b < nb) {
+        int fr = a.xrows[pr.xrow_off + 16 * bt + b];
+        xh = a.xhi + (size_t)fr * a.xstride + ks * 8;
+        xl = a.xlo + (size_t)fr * a.xstride + ks * 8;
+    }
+
+    int rt[R];
+    bool live[R];
+    const uint8_t *wb[R];
+    const void *sb[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int rr = DUAL ? (r % RT) : r;
+        rt[r] = rb * RT + rr;
+        live[r] = rt[r] < a.nrt;
+        bool second = DUAL && r >= RT;
+        wb[r] = second ? pr.w1 : pr.w0;
+        sb[r] = second ? pr.s1 : pr.s0;
+    }
+
+    floatx4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+
+    u32x4 wv[R];
+    ScaleRegs<KIND> sc[R];
+    auto load_q = [&](int q) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (live[r]) {
+                size_t tq = (size_t)rt[r] * a.nq + q;
+                wv[r] = __builtin_nontemporal_load((const u32x4 *)(wb[r] + tq * COLI_TILE_BYTES) + lane);
+                sc[r].load(sb[r], tq, lane & 15);
+            } else {
+                wv[r] = (u32x4){0u, 0u, 0u, 0u};
+                sc[r].zero();
+            }
+        }
+    };
+
+    int q = Q0 + wave;
+    if (q < Q1) load_q(q);
+    for (; q < Q1; q += 4) {
+        u32x4 cw[R];
+        ScaleRegs<KIND> cs[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) { cw[r] = wv[r]; cs[r] = sc[r]; }
+        if (q + 4 < Q1) load_q(q + 4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int g = 4 * q + j;
+            half8v ah = (half8v){0, 0, 0, 0, 0, 0, 0, 0}, al = ah;
+            if (xh) {
+                ah = *(const half8v *)(xh + (size_t)g * 32);
+                if (use_lo) al = *(const half8v *)(xl + (size_t)g * 32);
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                half8v bw = unpack_b<KIND>(cw[r][j]);
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if (use_lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, d, 0, 0, 0);
+                float scl = cs[r].get(j);
+#pragma unroll
+                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
+            }
+        }
+    }
+
+    // ---- intra-group reduction, fixed wave order; wave w finishes register i = w ----
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < NB4; i++) red[wave][r * 4 + i][lane] = acc[r][i];
+    __syncthreads();
+    const int i = wave;
+    float v[R];
+    if (i < NB4) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            v[r] = ((red[0][r * 4 + i][lane] + red[1][r * 4 + i][lane]) + red[2][r * 4 + i][lane]) +
+                   red[3][r * 4 + i][lane];
+    }
+
+    // ---- cross-group split-K: deterministic fixed-order sum by the last group ----
+    if (a.splits > 1) {
+        const size_t inst = ((size_t)p * a.n_bt + bt) * a.rb_per_prob + rb;
+        if (i < NB4) {
+            float *mine = a.partial + ((inst * a.splits + s) * R * 4) * 64;
+#pragma unroll
+            for (int r = 0; r < R; r++) mine[(r * 4 + i) * 64 + lane] = v[r];
+        }
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) last_flag = atomicAdd(&a.counters[inst], 1u) == (unsigned)(a.splits - 1);
+        __syncthreads();
+        if (!last_flag) return;
+        __threadfence();
+        if (threadIdx.x == 0) a.counters[inst] = 0u;   // self-reset for the next launch
+        if (i < NB4) {
+            const float *base = a.partial + (inst * a.splits * R * 4) * 64;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float t = 0.0f;
+                for (int ss = 0; ss < a.splits; ss++)
+                    t += __builtin_nontemporal_load(base + ((size_t)ss * R * 4 + r * 4 + i) * 64 + lane);
+                v[r] = t;
+            }
+        }
+    }
+
+    // ---- epilogue ----
+    if (i >= NB4) return;
+    const int brow = 4 * ks + i;
+    if (brow >= nb) return;
+    const int fr = a.xrows[pr.xrow_off + 16 * bt + brow];
+    const int E = a.xexp[fr];
+    float *orow = a.out + (size_t)(pr.out_row0 + 16 * bt + brow) * a.ldo;
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const int o = rt[r] * 16 + (lane & 15);
+        if (!live[r] || o >= a.O) continue;
+        if constexpr (DUAL) {
+            float gv = ldexpf(v[r], E), uv = ldexpf(v[r + RT], E);
+            orow[o] = silu_mul(gv, uv);
+        } else {
+            orow[o] = ldexpf(v[r], E);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic int4 kernel: any group size (incl. ones that are not a multiple of
+// 32), source layout, reference group semantics (c/quant.h:168-202). One
+// 256-thread block per (output row, batch row).
+// ---------------------------------------------------------------------------
+__global__ void coli_gemv_generic_i4(const uint8_t *__restrict__ w, const float *__restrict__ sc,
+                                     int I, int O, int gs, const float *__restrict__ x, int ldx,
+                                     float *__restrict__ y, int ldy) {
+    int o = blockIdx.x, s = blockIdx.y;
+    int rb = (I + 1) / 2, egs = gs > 0 ? gs : I, ng = (I + egs - 1) / egs;
+    const uint8_t *row = w + (size_t)o * rb;
+    const float *scl = sc + (size_t)o * ng;
+    const float *xs = x + (size_t)s * ldx;
+    float sum = 0.0f;
+    for (int g = threadIdx.x; g < ng; g += blockDim.x) {
+        int base = g * egs, end = min(I, base + egs);
+        float part = 0.0f;
+        for (int k = base; k < end; k++) {
+            uint8_t v = row[k >> 1];
+            int n = (k & 1) ? (v >> 4) : (v & 15);
+            part = fmaf(xs[k], (float)(n - 8), part);
+        }
+        sum = fmaf(part, scl[g], sum);
+    }
+    __shared__ float red[256];
+    red[threadIdx.x] = sum;
+    __syncthreads();
+    for (int st = 128; st; st >>= 1) {
+        if (threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
+        __syncthreads();
+    }
+    if (!threadIdx.x) y[(size_t)s * ldy + o] = red[0];
+}
+
+
+// ---------------------------------------------------------------------------
+// e4m3 activation quantize-dequantize, one e8m0 scale per 128-column block
+// (the native_quant contract, c/deepseek_v4.c:10495-10520), bit-exact: the
+// block max, the power-of-two scale, the division by it and the
+// round-to-nearest-even e4m3 encode are all exact operations.
+// ---------------------------------------------------------------------------
+__device__ float e4m3_qdq_value(float v) {
+    // v already clamped to [-448, 448]; returns decode(encode(v)).
+    if (v != v) return v;
+    float mag = fabsf(v);
+    float out;
+    if (mag == 0.0f) {
+        out = 0.0f;
+    } else if (mag < 0.015625f) {
+        float scaled = mag * 512.0f;
+        uint32_t whole = (uint32_t)scaled;
+        float frac = scaled - (float)whole;
+        if (frac > 0.5f || (frac == 0.5f && (whole & 1u))) whole++;
+        out = (float)whole * (1.0f / 512.0f);
+    } else {
+        uint32_t bits = __builtin_bit_cast(uint32_t, mag);
+        int e = (int)((bits >> 23) & 0xff) - 127;
+        uint32_t sig = 0x800000u | (bits & 0x7fffffu);
+        uint32_t keep = sig >> 20, rest = sig & 0xfffffu;
+        if (rest > 0x80000u || (rest == 0x80000u && (keep & 1u))) keep++;
+        out = ldexpf((float)keep, e - 3);
+        if (out > 448.0f) out = 448.0f;   // 0x7e saturation
+    }
+    return signbit(v) ? -out : out;
+}
+
+__global__ __launch_bounds__(128) void coli_qdq_e4m3(const float *__restrict__ x, float *__restrict__ y, int K) {
+    int blk = blockIdx.x, s = blockIdx.y, k = blk * 128 + threadIdx.x;
+    const float *xr = x + (size_t)s * K;
+    float v = k < K ? xr[k] : 0.0f;
+    __shared__ float red[128];
+    red[threadIdx.x] = k < K ? fabsf(v) : 0.0f;
+    __syncthreads();
+    for (int st = 64; st; st >>= 1) {
+        if (threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
+        __syncthreads();
+    }
+    float mx = fmaxf(red[0], 1e-4f);
+    int e;
+    float f = frexpf(mx / 448.0f, &e);
+    int se = f == 0.5f ? e - 1 : e;
+    se = se < -127 ? -127 : (se > 127 ? 127 : se);
+    float sc = ldexpf(1.0f, se);
+    if (k < K) {
+        float q = fmaxf(-448.0f, fminf(448.0f, v / sc));
+        y[(size_t)s * K + k] = e4m3_qdq_value(q) * sc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launchers (called from backend_hip.hip)
+// ---------------------------------------------------------------------------
+struct ColiGemvPlan {
+    int R, dual, nb4;
+};
+
+template <int KIND, int R, bool DUAL>
+static hipError_t launch_nb(const ColiGemvArgs &a, int nb4, int blocks, hipStream_t st) {
+    if (nb4 == 1) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, 1>), dim3(blocks), dim3(256), 0, st, a);
+    else if (nb4 == 2) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, 2>), dim3(blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, 4>), dim3(blocks), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+template <int KIND>
+static hipError_t launch_kind(const ColiGemvArgs &a, int R, bool dual, int nb4, int blocks, hipStream_t st) {
+    if (dual) return launch_nb<KIND, 4, true>(a, nb4, blocks, st);
+    if (R == 4) return launch_nb<KIND, 4, false>(a, nb4, blocks, st);
+    if (R == 2) return launch_nb<KIND, 2, false>(a, nb4, blocks, st);
+    return launch_nb<KIND, 1, false>(a, nb4, blocks, st);
+}
+
+extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual,
+                                       int max_rows, hipStream_t st) {
+    int nb4 = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
+    long items = (long)a->nprob * a->n_bt * a->rb_per_prob * a->splits;
+    int blocks = (int)items;
+    if (blocks <= 0) return hipSuccess;
+    switch (kind) {
+    case COLI_KIND_I4_H: return launch_kind<COLI_KIND_I4_H>(*a, R, dual, nb4, blocks, st);
+    case COLI_KIND_I4_F: return launch_kind<COLI_KIND_I4_F>(*a, R, dual, nb4, blocks, st);
+    case COLI_KIND_FP4: return launch_kind<COLI_KIND_FP4>(*a, R, dual, nb4, blocks, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row,
+                                            const int *nrows_dev, int nrows, int K, int ngp,
+                                            int int4_order, _Float16 *hi, _Float16 *lo,
+                                            int *exp2out, int *haslo, hipStream_t st) {
+    if (nrows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(coli_prep_frag, dim3(nrows), dim3(256), 0, st, x, ldx, src_row, nrows_dev,
+                       nrows, K, ngp, int4_order, hi, lo, exp2out, haslo);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t coli_launch_repack(const ColiCudaTensor *t, const uint8_t *src_w,
+                                         const void *src_s, hipStream_t st) {
+    size_t nd = (size_t)t->nrt * t->nq * 256;
+    hipLaunchKernelGGL(coli_repack_nibbles, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, st,
+                       src_w, t->O, t->I, (uint32_t *)t->w, t->nrt, t->nq,
+                       t->kind == COLI_KIND_FP4 ? 0u : 8u);
+    size_t ns = (size_t)t->nrt * t->nq * 64;
+    if (t->kind == COLI_KIND_FP4)
+        hipLaunchKernelGGL(coli_repack_scales_e8, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, st,
+                           (const uint8_t *)src_s, t->O, t->I, (uint8_t *)t->sc, t->nrt, t->nq);
+    else
+        hipLaunchKernelGGL(coli_repack_scales_i4, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, st,
+                           (const float *)src_s, t->O, t->I, t->gs, t->sc, t->nrt, t->nq,
+                           t->kind == COLI_KIND_I4_H ? 1 : 0);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const float *x, int ldx,
+                                             float *y, int ldy, int S, hipStream_t st) {
+    hipLaunchKernelGGL(coli_gemv_generic_i4, dim3(t->O, S), dim3(256), 0, st, t->w,
+                       (const float *)t->sc, t->I, t->O, t->gs, x, ldx, y, ldy);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t coli_launch_qdq_e4m3(const float *x, float *y, int S, int K, hipStream_t st) {
+    hipLaunchKernelGGL(coli_qdq_e4m3, dim3((K + 127) / 128, S), dim3(128), 0, st, x, y, K);
+    return hipGetLastError();
+}

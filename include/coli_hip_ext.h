@@ -1,0 +1,89 @@
+/* coli_hip_ext.h -- entry points libcoli_hip.so adds beyond the reference ABI.
+ *
+ * None of these has a counterpart in c/backend_cuda.h; each states the
+ * reference code whose behaviour it provides on the device.
+ */
+#ifndef COLI_HIP_EXT_H
+#define COLI_HIP_EXT_H
+
+#include "coli_backend_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Resident MXFP4 (fmt=7) tensor from its native bytes: q4 [O, ceil(I/2)]
+ * e2m1 nibbles, e8 [O, ceil(I/32)] ue8m0 exponents (the layout of
+ * c/quant.h:1375-1390). The CUDA backend has no resident fmt=7 group path
+ * (c/backend_cuda.cu:1636-1643); this is new capability. */
+int coli_hip_tensor_upload_mxfp4(ColiCudaTensor **tensor, const unsigned char *q4,
+                                 const unsigned char *e8, int I, int O, int device);
+
+/* Resident MXFP4 tensor from the 16-row interleaved layout of
+ * coli_fp4_pack_rows16_v10 (c/deepseek_v4.c:10975-10993): O % 16 == 0,
+ * I % 128 == 0. */
+int coli_hip_tensor_upload_fp4_rows16(ColiCudaTensor **tensor, const unsigned char *packed_data,
+                                      const unsigned char *packed_scales, int I, int O,
+                                      int device);
+
+/* native_quant contract on the device: every activation row is first
+ * quantize-dequantized to e4m3 in blocks of 128 with an e8m0 scale
+ * (c/deepseek_v4.c:10495-10520), then multiplied with the resident MXFP4
+ * tensor (coli_fp4_matmul_batch_ref, c/deepseek_v4.c:10906-10933; batch 1 is
+ * coli_fp4_matvec_ref, 10571-10605). Host pointers; returns 1 / 0. */
+int coli_hip_fp4_matmul_qdq(ColiCudaTensor *tensor, float *y, const float *x, int S);
+
+/* Same, device pointers, asynchronous on the backend stream. */
+int coli_hip_fp4_matmul_qdq_dev(ColiCudaTensor *tensor, float *y_dev, const float *x_dev, int S);
+
+/* ---- fused MoE layer (router -> union -> experts -> SwiGLU -> scatter) ---- */
+typedef struct ColiHipMoe ColiHipMoe;
+
+typedef struct {
+    int D, I, E, K;        /* hidden, expert intermediate, routed experts, top-k */
+    int route_mode;        /* 0 softmax then top-k (c/olmoe.c:666-681)
+                              1 sigmoid, choice = sigmoid + bias (c/colibri.c:3978-4126)
+                              2 sigmoid + bias select, weights renormalized over the
+                                selection (c/kimi_k3.c:1337-1356) */
+    int norm_topk;
+    float topp;            /* 0 disables */
+    float routed_scale;    /* 1.0 for none */
+    int has_shared;        /* one always-on expert, added after the routed sum */
+} ColiHipMoeConfig;
+
+/* Router weights f32 [E, D] (+ bias [E] or NULL) are copied to the device;
+ * expert tensors are resident handles of one device (gate/up [I, D], down
+ * [D, I]). All experts must share one storage kind. */
+int coli_hip_moe_create(ColiHipMoe **moe, int device, const ColiHipMoeConfig *cfg,
+                        const float *router_w, const float *router_bias,
+                        ColiCudaTensor *const *gates, ColiCudaTensor *const *ups,
+                        ColiCudaTensor *const *downs, ColiCudaTensor *shared_gate,
+                        ColiCudaTensor *shared_up, ColiCudaTensor *shared_down);
+void coli_hip_moe_free(ColiHipMoe *moe);
+
+/* Device-resident forward of S <= 16 decode rows: x_dev [S, D] f32 ->
+ * out_dev [S, D] f32, asynchronous on the backend stream (no host sync, no
+ * allocation after the first call at a given S). */
+int coli_hip_moe_forward_dev(ColiHipMoe *moe, const float *x_dev, float *out_dev, int S);
+
+/* Host forward with routing read back: idx/w [S, K], keff [S] (may be NULL). */
+int coli_hip_moe_forward(ColiHipMoe *moe, const float *x, float *out, int S, int *idx,
+                         float *w, int *keff);
+
+/* Union of the last forward: nu and the unique expert ids in first-seen order
+ * (c/colibri.c:4146-4152). Synchronizes. */
+int coli_hip_moe_last_union(ColiHipMoe *moe, int *nu, int *uniq);
+
+/* ---- plumbing for benchmarks and tests ----------------------------------- */
+/* The hipStream_t every asynchronous entry point of `device` runs on. */
+void *coli_hip_stream(int device);
+/* Bytes the tensor streams per full GEMV (weights + scales, tiled storage). */
+size_t coli_hip_tensor_stream_bytes(const ColiCudaTensor *tensor);
+/* Storage kind: 0 int4+fp16 scales, 1 int4+f32 scales, 2 MXFP4, 3 generic int4. */
+int coli_hip_tensor_kind(const ColiCudaTensor *tensor);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

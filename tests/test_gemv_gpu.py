@@ -1,0 +1,202 @@
+"""GPU parity of the quantized GEMV through the C ABI (coli_cuda_matmul and
+friends) against the CPU oracle (bit-exact restatement of c/quant.h)."""
+import numpy as np
+import pytest
+
+from oracle_lib import Cref
+from quant_util import (deq_i4, deq_mxfp4, magnitude, rand_i4, rand_mxfp4, rand_x, rel_err)
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+cref = Cref()
+
+
+def check(got, ref, mag, tol=TOL):
+    e = rel_err(got, ref, mag)
+    assert np.isfinite(got).all()
+    assert e.max() <= tol, f"max rel err {e.max():.3e}"
+    return e.max()
+
+
+@pytest.mark.parametrize("O,I", [(64, 256), (1024, 2048), (48, 200), (17, 96), (2048, 1024)])
+@pytest.mark.parametrize("S", [1, 2, 3, 4, 8, 16, 21])
+def test_int4_g32_fp16_scales(session, O, I, S):
+    rng = np.random.default_rng(O * 131 + I * 7 + S)
+    q4, sc = rand_i4(rng, O, I, 32)
+    x = rand_x(rng, S, I)
+    h = session.upload(q4, sc, 4, I, O, 32)
+    try:
+        assert session.b.hip_tensor_kind(h) == 0
+        y = session.matmul(h, x, 4, I, O, 32)
+    finally:
+        session.free(h)
+    ref = cref.matmul_i4_grouped(x, q4, sc, O, I, 32)
+    check(y, ref, magnitude(x, deq_i4(q4, sc, I, 32)))
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("S", [1, 5])
+def test_int4_f32_scales_and_group_sizes(session, gs, S):
+    rng = np.random.default_rng(gs + S)
+    O, I = 96, 640
+    q4, sc = rand_i4(rng, O, I, gs, fp16_scales=False)
+    x = rng.standard_normal((S, I)).astype(np.float32)   # not bf16-exact: exercises the lo MFMA
+    h = session.upload(q4, sc, 4, I, O, gs)
+    try:
+        assert session.b.hip_tensor_kind(h) == 1
+        y = session.matmul(h, x, 4, I, O, gs)
+    finally:
+        session.free(h)
+    ref = cref.matmul_i4_grouped(x, q4, sc, O, I, gs)
+    check(y, ref, magnitude(x, deq_i4(q4, sc, I, gs)))
+
+
+def test_int4_per_row_fmt2(session):
+    rng = np.random.default_rng(3)
+    O, I, S = 80, 333, 3
+    q4, sc = rand_i4(rng, O, I, 0)
+    x = rand_x(rng, S, I)
+    h = session.upload(q4, sc, 2, I, O, 0)
+    try:
+        y = session.matmul(h, x, 2, I, O, 0)
+    finally:
+        session.free(h)
+    ref = cref.matmul_i4(x, q4, sc, O, I)
+    check(y, ref, magnitude(x, deq_i4(q4, sc, I, 0)))
+
+
+def test_int4_generic_group16(session):
+    rng = np.random.default_rng(4)
+    O, I, S = 40, 200, 2
+    q4, sc = rand_i4(rng, O, I, 16)
+    x = rand_x(rng, S, I)
+    h = session.upload(q4, sc, 4, I, O, 16)
+    try:
+        assert session.b.hip_tensor_kind(h) == 3
+        y = session.matmul(h, x, 4, I, O, 16)
+    finally:
+        session.free(h)
+    ref = cref.matmul_i4_grouped(x, q4, sc, O, I, 16)
+    check(y, ref, magnitude(x, deq_i4(q4, sc, I, 16)))
+
+
+def test_int4_nibble_edges_closed_form(session):
+    """Unit scales and x = e_i return the nibble value - 8 exactly (0x00 -> -8, 0xF -> +7)."""
+    O, I = 16, 128
+    q4 = np.zeros((O, I // 2), np.uint8)
+    q4[:, 0] = 0xF0        # column 0 -> nibble 0 (-8), column 1 -> nibble 15 (+7)
+    sc = np.ones((O, I // 32), np.float32)
+    x = np.zeros((2, I), np.float32)
+    x[0, 0] = 1.0
+    x[1, 1] = 1.0
+    h = session.upload(q4, sc, 4, I, O, 32)
+    try:
+        y = session.matmul(h, x, 4, I, O, 32)
+    finally:
+        session.free(h)
+    assert (y[0] == -8.0).all() and (y[1] == 7.0).all()
+
+
+@pytest.mark.parametrize("O,I", [(64, 256), (2048, 7168), (7168, 2048), (40, 96)])
+@pytest.mark.parametrize("S", [1, 4, 16])
+def test_mxfp4(session, O, I, S):
+    rng = np.random.default_rng(O + I + S)
+    q4, e8 = rand_mxfp4(rng, O, I)
+    x = rand_x(rng, S, I)
+    h = session.upload_mxfp4(q4, e8, I, O)
+    try:
+        assert session.b.hip_tensor_kind(h) == 2
+        y = session.matmul(h, x, 7, I, O, 32)
+    finally:
+        session.free(h)
+    ref = cref.matmul_mxfp4(x, q4, e8, O, I)
+    check(y, ref, magnitude(x, deq_mxfp4(q4, e8, I)))
+
+
+def test_mxfp4_all_codes_exact(session):
+    """One column set to code c, x = 1: the result is the decoded value
+    (c/tests/test_mxfp4_cuda.cu:106-132)."""
+    want = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6], np.float32)
+    I, O = 32, 16
+    q4 = np.zeros((O, I // 2), np.uint8)
+    q4[:, 0] = np.arange(16, dtype=np.uint8)
+    e8 = np.full((O, 1), 127, np.uint8)
+    x = np.zeros((1, I), np.float32)
+    x[0, 0] = 1.0
+    y = np.zeros((1, O), np.float32)
+    from colibri_amd.backend import f32p, u8p
+    assert session.b.cuda_matmul_mxfp4(f32p(y), f32p(x), u8p(q4), u8p(e8), 1, I, O)
+    assert np.array_equal(y[0], want)
+
+
+@pytest.mark.parametrize("e", [0, 127, 255])
+def test_mxfp4_scale_edges(session, e):
+    """e8m0 0 -> +0 and 255 -> +inf follow quant.h's bit trick (c/quant.h:1375-1390)."""
+    rng = np.random.default_rng(e)
+    O, I = 16, 64
+    q4 = rng.integers(0, 256, (O, I // 2), dtype=np.uint8)
+    e8 = np.full((O, 2), e, np.uint8)
+    x = rng.standard_normal((1, I)).astype(np.float32)
+    y = np.zeros((1, O), np.float32)
+    from colibri_amd.backend import f32p, u8p
+    assert session.b.cuda_matmul_mxfp4(f32p(y), f32p(x), u8p(q4), u8p(e8), 1, I, O)
+    ref = cref.matmul_mxfp4(x, q4, e8, O, I)
+    if e == 0:
+        assert np.array_equal(y, ref) and (y == 0).all()
+    elif e == 255:
+        # +inf scales: every output is non-finite on both sides; which ones end
+        # as inf and which as NaN depends on how partial sums of opposite sign
+        # meet (the reference's 8-lane accumulator mixes them into NaN), the
+        # same latitude c/tests/test_mxfp4_cuda.cu:84-92 gives the CUDA kernel.
+        assert not np.isfinite(y).any() and not np.isfinite(ref).any()
+    else:
+        check(y, ref, magnitude(x, deq_mxfp4(q4, e8, I)))
+
+
+@pytest.mark.parametrize("S,I,O", [(1, 80, 8), (4, 128, 64), (1, 2048, 16), (3, 96, 8)])
+def test_matmul_mxfp4_stateless(session, S, I, O):
+    rng = np.random.default_rng(S * I + O)
+    q4, e8 = rand_mxfp4(rng, O, I, 110, 139)
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    y = np.zeros((S, O), np.float32)
+    from colibri_amd.backend import f32p, u8p
+    assert session.b.cuda_matmul_mxfp4(f32p(y), f32p(x), u8p(q4), u8p(e8), S, I, O)
+    ref = cref.matmul_mxfp4(x, q4, e8, O, I)
+    check(y, ref, magnitude(x, deq_mxfp4(q4, e8, I)))
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_fp4_native_quant_contract(session, S):
+    """coli_hip_fp4_matmul_qdq == e4m3 QDQ (block 128) + fmt=7 GEMV
+    (coli_fp4_matmul_batch_ref, c/deepseek_v4.c:10906-10933)."""
+    rng = np.random.default_rng(10 + S)
+    O, I = 256, 1024
+    q4, e8 = rand_mxfp4(rng, O, I)
+    x = (rng.standard_normal((S, I)) * 3).astype(np.float32)
+    h = session.upload_mxfp4(q4, e8, I, O)
+    y = np.zeros((S, O), np.float32)
+    from colibri_amd.backend import f32p
+    try:
+        assert session.b.hip_fp4_matmul_qdq(h, f32p(y), f32p(x), S)
+    finally:
+        session.free(h)
+    ref = cref.fp4_matmul_batch(x, q4, e8, O, I)
+    xq = np.stack([cref.qdq(x[s])[0] for s in range(S)])
+    check(y, ref, magnitude(xq, deq_mxfp4(q4, e8, I)))
+
+
+def test_fp4_matvec_kat(session):
+    """weights 0x44 (+2.0, +2.0), scale 0x7e (0.5), x = 1 over 128 columns gives
+    exactly 128.0 (c/tests/test_native_quant.c:76-88)."""
+    q4 = np.full((1, 64), 0x44, np.uint8)
+    e8 = np.full((1, 4), 0x7E, np.uint8)
+    x = np.ones((1, 128), np.float32)
+    h = session.upload_mxfp4(q4, e8, 128, 1)
+    y = np.zeros((1, 1), np.float32)
+    from colibri_amd.backend import f32p
+    try:
+        assert session.b.hip_fp4_matmul_qdq(h, f32p(y), f32p(x), 1)
+    finally:
+        session.free(h)
+    assert y[0, 0] == 128.0
