@@ -304,6 +304,18 @@ static ColiCudaTensor *alloc_tensor(DevCtx *ctx, int fmt, int I, int O, int gs, 
         std::free(t);
         return nullptr;
     }
+    if (kind != COLI_KIND_GENERIC) {
+        ColiProb d[COLI_DESC_ROWS];
+        for (int r = 0; r < COLI_DESC_ROWS; r++) d[r] = {t->w, t->sc, nullptr, nullptr, r + 1, 0, 0, 0};
+        if (!hip_ok(hipMalloc((void **)&t->desc, sizeof(d)), "descriptor allocation") ||
+            !hip_ok(hipMemcpy(t->desc, d, sizeof(d), hipMemcpyHostToDevice), "descriptor upload")) {
+            (void)hipFree(t->w);
+            (void)hipFree(t->sc);
+            if (t->desc) (void)hipFree(t->desc);
+            std::free(t);
+            return nullptr;
+        }
+    }
     t->accounted = t->w_bytes + t->sc_bytes;
     ctx->tensor_count++;
     ctx->tensor_bytes += t->accounted;
@@ -403,6 +415,7 @@ extern "C" void coli_cuda_tensor_free(ColiCudaTensor *t) {
     }
     if (t->w) (void)hipFree(t->w);
     if (t->sc) (void)hipFree(t->sc);
+    if (t->desc) (void)hipFree(t->desc);
     std::free(t);
 }
 

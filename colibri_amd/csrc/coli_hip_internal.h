@@ -23,6 +23,7 @@
 #define COLI_TILE_COLS 128
 #define COLI_TILE_BYTES 1024
 #define COLI_GROUP 32
+#define COLI_DESC_ROWS 64
 
 // Tensor storage kinds.
 enum ColiKind {
@@ -42,6 +43,7 @@ struct ColiCudaTensor {
     size_t w_bytes, sc_bytes;
     int ng_src;                  // scale groups per source row (GENERIC)
     size_t accounted;            // bytes charged to the device statistics
+    struct ColiProb *desc;       // device: 64 descriptors, entry s-1 = this matrix on s rows
 };
 
 // One GEMV problem: a matrix (or a gate/up pair) applied to a set of batch rows.

@@ -381,23 +381,52 @@ extern "C" int coli_cuda_shared_mlp_w4a16(ColiCudaTensor *gate, ColiCudaTensor *
 // ---------------------------------------------------------------------------
 // single-matrix GEMV / GEMM
 // ---------------------------------------------------------------------------
+// Fragments of x_dev[S, I] for tensor t (input set of t's kind).
+static int gemm_prep(DevCtx *ctx, ColiCudaTensor *t, const float *x_dev, int S) {
+    if (!ensure_iota(ctx, S)) return 0;
+    return make_frags(ctx, frag_set_of(t->kind, false), x_dev, t->I, S, t->I, t->kind != COLI_KIND_FP4);
+}
+
+// GEMV of t over the prepared fragments of S rows -> y_dev[S, O]. Uses the
+// tensor's cached descriptor for S <= 64 (no host synchronization).
+static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S) {
+    const ColiProb *pd;
+    if (t->desc && S <= COLI_DESC_ROWS) {
+        pd = t->desc + (S - 1);
+    } else {
+        ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
+        if (!reserve_pinned(ctx, &ctx->host_prob, &ctx->host_prob_cap, sizeof(p)) ||
+            !reserve(ctx, &ctx->prob, sizeof(p), 0) || !hip_ok(hipStreamSynchronize(ctx->stream), "gemm staging"))
+            return 0;
+        std::memcpy(ctx->host_prob, &p, sizeof(p));
+        if (!hip_ok(hipMemcpyAsync(ctx->prob.p, ctx->host_prob, sizeof(p), hipMemcpyHostToDevice, ctx->stream),
+                    "gemm descriptor"))
+            return 0;
+        pd = (const ColiProb *)ctx->prob.p;
+    }
+    return run_gemv(ctx, t->kind, false, pd, 1, nullptr, t->nrt, t->nq, t->O, S, frag_set_of(t->kind, false),
+                    (const int *)ctx->iota.p, y_dev, t->O);
+}
+
 // y_dev[S, O] = x_dev[S, I] W^T on the stream (tensor already resident).
 static int gemm_dev(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
     if (t->kind == COLI_KIND_GENERIC)
         return hip_ok(coli_launch_generic_i4(t, x_dev, t->I, y_dev, t->O, S, ctx->stream), "generic gemv");
-    if (!ensure_iota(ctx, S)) return 0;
-    int set = frag_set_of(t->kind, false);
-    if (!make_frags(ctx, set, x_dev, t->I, S, t->I, t->kind != COLI_KIND_FP4)) return 0;
-    ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
-    if (!reserve_pinned(ctx, &ctx->host_prob, &ctx->host_prob_cap, sizeof(p)) ||
-        !reserve(ctx, &ctx->prob, sizeof(p), 0) || !hip_ok(hipStreamSynchronize(ctx->stream), "gemm staging"))
-        return 0;
-    std::memcpy(ctx->host_prob, &p, sizeof(p));
-    if (!hip_ok(hipMemcpyAsync(ctx->prob.p, ctx->host_prob, sizeof(p), hipMemcpyHostToDevice, ctx->stream),
-                "gemm descriptor"))
-        return 0;
-    return run_gemv(ctx, t->kind, false, (const ColiProb *)ctx->prob.p, 1, nullptr, t->nrt, t->nq, t->O, S, set,
-                    (const int *)ctx->iota.p, y_dev, t->O);
+    return gemm_prep(ctx, t, x_dev, S) && gemm_run(ctx, t, y_dev, S);
+}
+
+extern "C" int coli_hip_gemm_prep_dev(ColiCudaTensor *t, const float *x_dev, int S) {
+    if (!t || !x_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
+    DevCtx *ctx = find_ctx(t->device);
+    if (!select_ctx(ctx)) return 0;
+    return gemm_prep(ctx, t, x_dev, S);
+}
+
+extern "C" int coli_hip_gemm_run_dev(ColiCudaTensor *t, float *y_dev, int S) {
+    if (!t || !y_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
+    DevCtx *ctx = find_ctx(t->device);
+    if (!select_ctx(ctx)) return 0;
+    return gemm_run(ctx, t, y_dev, S);
 }
 
 static int gemm_host(DevCtx *ctx, ColiCudaTensor *t, float *y, const float *x, int S, int qdq) {

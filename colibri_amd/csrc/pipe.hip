@@ -112,8 +112,13 @@ __global__ __launch_bounds__(256) void coli_router_logits(const float *__restric
 
 extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E,
                                                 float *logits, hipStream_t st) {
-    if (S <= 4) hipLaunchKernelGGL(coli_router_logits<4>, dim3(E), dim3(256), 0, st, x, S, W, D, E, logits);
-    else hipLaunchKernelGGL(coli_router_logits<16>, dim3(E), dim3(256), 0, st, x, S, W, D, E, logits);
+    for (int s0 = 0; s0 < S; s0 += 16) {   // 16 rows of accumulators per pass
+        int n = S - s0 < 16 ? S - s0 : 16;
+        const float *xs = x + (size_t)s0 * D;
+        float *ls = logits + (size_t)s0 * E;
+        if (n <= 4) hipLaunchKernelGGL(coli_router_logits<4>, dim3(E), dim3(256), 0, st, xs, n, W, D, E, ls);
+        else hipLaunchKernelGGL(coli_router_logits<16>, dim3(E), dim3(256), 0, st, xs, n, W, D, E, ls);
+    }
     return hipGetLastError();
 }
 

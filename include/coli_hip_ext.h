@@ -75,6 +75,12 @@ int coli_hip_moe_forward(ColiHipMoe *moe, const float *x, float *out, int S, int
 int coli_hip_moe_last_union(ColiHipMoe *moe, int *nu, int *uniq);
 
 /* ---- plumbing for benchmarks and tests ----------------------------------- */
+/* coli_cuda_pipe_gemm in two halves, so a timer can bracket the GEMV kernel
+ * alone: prep builds the activation fragments of x_dev[S, I] for the
+ * tensor's storage kind; run launches the GEMV y_dev[S, O] on them. A run
+ * must follow the prep of the same kind of tensor and the same S. */
+int coli_hip_gemm_prep_dev(ColiCudaTensor *tensor, const float *x_dev, int S);
+int coli_hip_gemm_run_dev(ColiCudaTensor *tensor, float *y_dev, int S);
 /* The hipStream_t every asynchronous entry point of `device` runs on. */
 void *coli_hip_stream(int device);
 /* Bytes the tensor streams per full GEMV (weights + scales, tiled storage). */

@@ -1,0 +1,205 @@
+"""GPU parity of the expert path: ABI group calls (sync, issue/take, mlp,
+resident) and the fused device MoE layer (router -> union -> experts ->
+SwiGLU -> scatter) against the oracle composition."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from colibri_amd.backend import ColiHipMoeConfig, f32p, i32p, tensor_array
+from moe_ref import Layer, cref, make_router_inputs, moe_reference
+from quant_util import rand_x, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def group_reference(layer, x, members, rows):
+    out, off = [], 0
+    for e, r in zip(members, rows):
+        for s in range(r):
+            out.append(layer.expert_forward(e, x[off + s:off + s + 1])[1][0])
+        off += r
+    return np.stack(out)
+
+
+def group_mag(layer, x, members, rows):
+    mags, off = [], 0
+    for e, r in zip(members, rows):
+        for s in range(r):
+            h, _ = layer.expert_forward(e, x[off + s:off + s + 1])
+            mags.append(np.abs(h[0]).astype(np.float64) @ np.abs(layer.deq(layer.experts[e][2], layer.I)).T)
+        off += r
+    return np.stack(mags)
+
+
+@pytest.mark.parametrize("fmt", [4, 7])
+def test_expert_group_sync_async_bitwise(session, fmt):
+    """Group call vs oracle; issue/take result bitwise equal to the sync call
+    (c/tests/test_grouped_g4_cuda.cu:115-171)."""
+    rng = np.random.default_rng(fmt)
+    D, I = 384, 256
+    layer = Layer(rng, fmt, D, I, 3)
+    hs = layer.upload(session)
+    rows = [1, 2, 1]
+    x = rand_x(rng, sum(rows), D)
+    try:
+        y = session.expert_group([h[0] for h in hs], [h[1] for h in hs], [h[2] for h in hs], rows, x)
+        ref = group_reference(layer, x, [0, 1, 2], rows)
+        assert rel_err(y, ref, group_mag(layer, x, [0, 1, 2], rows)).max() <= TOL
+        g, ga = tensor_array([h[0] for h in hs])
+        u, ua = tensor_array([h[1] for h in hs])
+        d, da = tensor_array([h[2] for h in hs])
+        r = np.array(rows, np.int32)
+        assert session.b.cuda_expert_group_issue(g, u, d, i32p(r), 3, f32p(x))
+        yp = session.b.cuda_expert_group_take(0)
+        assert yp
+        ya = np.ctypeslib.as_array(yp, shape=(sum(rows) * D,)).reshape(sum(rows), D).copy()
+        assert np.array_equal(ya.view(np.uint32), y.view(np.uint32))
+        # a second take without an issue returns NULL
+        assert not session.b.cuda_expert_group_take(0)
+    finally:
+        for h in hs:
+            for t in h:
+                session.free(t)
+
+
+def test_expert_mlp_many_rows(session):
+    """expert_mlp over S = 40 rows (three 16-row batch tiles)."""
+    rng = np.random.default_rng(5)
+    D, I = 256, 384
+    layer = Layer(rng, 4, D, I, 1)
+    hs = layer.upload(session)
+    x = rand_x(rng, 40, D)
+    y = np.zeros_like(x)
+    try:
+        assert session.b.cuda_expert_mlp(hs[0][0], hs[0][1], hs[0][2], f32p(y), f32p(x), 40)
+    finally:
+        for t in hs[0]:
+            session.free(t)
+    ref = group_reference(layer, x, [0], [40])
+    assert rel_err(y, ref, group_mag(layer, x, [0], [40])).max() <= TOL
+
+
+def test_resident_issue_take(session):
+    """Resident decode group: sum_c w_c * expert_c(x) lands in the slot; take
+    sums slots in issue order (c/backend_cuda.cu:2246-2316)."""
+    rng = np.random.default_rng(6)
+    D, I = 256, 128
+    layer = Layer(rng, 4, D, I, 4)
+    hs = layer.upload(session)
+    x = rand_x(rng, 1, D)
+    w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    b = session.b
+    xd = b.cuda_pipe_alloc(0, D * 4)
+    slots = b.cuda_pipe_alloc(0, 2 * D * 4)
+    acc = b.cuda_pipe_alloc(0, D * 4)
+    try:
+        assert b.cuda_pipe_upload(0, xd, x.ctypes.data_as(C.c_void_p), D * 4)
+        g, ga = tensor_array([h[0] for h in hs[:2]])
+        u, ua = tensor_array([h[1] for h in hs[:2]])
+        d, da = tensor_array([h[2] for h in hs[:2]])
+        assert b.cuda_expert_group_resident_issue(g, u, d, f32p(w[:2].copy()), 2, 0, xd, slots)
+        g2, ga2 = tensor_array([h[0] for h in hs[2:]])
+        u2, ua2 = tensor_array([h[1] for h in hs[2:]])
+        d2, da2 = tensor_array([h[2] for h in hs[2:]])
+        assert b.cuda_expert_group_resident_issue(g2, u2, d2, f32p(w[2:].copy()), 2, 0, xd,
+                                                  C.c_void_p(slots + D * 4))
+        devs = np.zeros(2, np.int32)
+        assert b.cuda_expert_group_resident_take(0, i32p(devs), 2, slots, acc, D)
+        out = np.zeros(D, np.float32)
+        assert b.cuda_pipe_download(0, acc, out.ctypes.data_as(C.c_void_p), D * 4)
+    finally:
+        for p in (xd, slots, acc):
+            b.cuda_pipe_free(0, p)
+        for h in hs:
+            for t in h:
+                session.free(t)
+    ref = np.zeros(D)
+    mag = np.zeros(D)
+    for e in range(4):
+        h, y = layer.expert_forward(e, x)
+        ref += w[e] * y[0]
+        mag += w[e] * (np.abs(h[0]).astype(np.float64) @ np.abs(layer.deq(layer.experts[e][2], I)).T)
+    assert rel_err(out, ref, mag).max() <= TOL
+
+
+def test_pipe_router_bitexact(session):
+    """coli_cuda_pipe_router: indices bit-exact, weights to 1e-5, vs the CPU
+    clone of c/backend_cuda.cu:2169-2194 (sigmoid + bias, norm, scale)."""
+    rng = np.random.default_rng(7)
+    D, E, K = 2048, 256, 8
+    b = session.b
+    for trial in range(8):
+        x, W, bias = make_router_inputs(rng, 1, D, E, K, 1, bias=True)
+        xd = b.cuda_pipe_alloc(0, D * 4)
+        wd = b.cuda_pipe_alloc(0, E * D * 4)
+        bd = b.cuda_pipe_alloc(0, E * 4)
+        try:
+            assert b.cuda_pipe_upload(0, xd, x.ctypes.data_as(C.c_void_p), D * 4)
+            assert b.cuda_pipe_upload(0, wd, W.ctypes.data_as(C.c_void_p), E * D * 4)
+            assert b.cuda_pipe_upload(0, bd, bias.ctypes.data_as(C.c_void_p), E * 4)
+            idx = np.zeros(K, np.int32)
+            w = np.zeros(K, np.float32)
+            keff = np.zeros(1, np.int32)
+            topp = 0.9 if trial % 2 else 0.0
+            assert b.cuda_pipe_router(0, xd, wd, bd, D, E, K, topp, 1, 2.5, i32p(idx), f32p(w), i32p(keff))
+        finally:
+            for p in (xd, wd, bd):
+                b.cuda_pipe_free(0, p)
+        ri, rw, rk = cref.route(cref.matmul_f32(x, W), K, 1, bias=bias, topp=topp, norm_topk=1,
+                                routed_scale=2.5)
+        assert keff[0] == rk[0]
+        assert np.array_equal(idx[:keff[0]], ri[0, :rk[0]])
+        assert np.allclose(w[:keff[0]], rw[0, :rk[0]], rtol=1e-5, atol=0)
+
+
+def make_moe(session, layer, W, b, K, mode, norm_topk=0, topp=0.0, routed_scale=1.0):
+    hs = layer.upload(session)
+    E = layer.E
+    routed, shared = hs[:E], (hs[E] if layer.shared else (None, None, None))
+    g, ga = tensor_array([h[0] for h in routed])
+    u, ua = tensor_array([h[1] for h in routed])
+    d, da = tensor_array([h[2] for h in routed])
+    cfg = ColiHipMoeConfig(layer.D, layer.I, E, K, mode, norm_topk, topp, routed_scale,
+                           1 if layer.shared else 0)
+    m = C.c_void_p()
+    Wc = np.ascontiguousarray(W)
+    bc = np.ascontiguousarray(b) if b is not None else None
+    ok = session.b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(Wc), f32p(bc) if bc is not None else None,
+                                  g, u, d, shared[0], shared[1], shared[2])
+    assert ok
+    return m, hs
+
+
+@pytest.mark.parametrize("fmt,mode,S,shared", [(4, 0, 1, False), (4, 0, 5, False), (7, 2, 1, True),
+                                               (7, 2, 16, True), (4, 1, 21, False), (7, 1, 3, False)])
+def test_moe_layer(session, fmt, mode, S, shared):
+    rng = np.random.default_rng(100 + fmt * 10 + mode + S)
+    D, I, E, K = 512, 256, 32, 4
+    layer = Layer(rng, fmt, D, I, E, shared=shared)
+    x, W, b = make_router_inputs(rng, S, D, E, K, mode, bias=(mode != 0))
+    norm = 1 if mode == 1 else 0
+    scale = 2.5 if mode == 1 else 1.0
+    m, hs = make_moe(session, layer, W, b, K, mode, norm_topk=norm, routed_scale=scale)
+    out = np.zeros((S, D), np.float32)
+    idx = np.zeros((S, K), np.int32)
+    w = np.zeros((S, K), np.float32)
+    keff = np.zeros(S, np.int32)
+    try:
+        assert session.b.hip_moe_forward(m, f32p(x), f32p(out), S, i32p(idx), f32p(w), i32p(keff))
+        nu = C.c_int()
+        uq = np.zeros(E, np.int32)
+        assert session.b.hip_moe_last_union(m, C.byref(nu), i32p(uq))
+    finally:
+        session.b.hip_moe_free(m)
+        for h in hs:
+            for t in h:
+                session.free(t)
+    ri, rw, rk, ref, mag = moe_reference(layer, x, W, b, K, mode, norm_topk=norm, routed_scale=scale)
+    assert np.array_equal(keff, rk)
+    assert np.array_equal(idx, ri), "router top-K indices must be bit-exact"
+    assert np.allclose(w, rw, rtol=1e-5, atol=1e-7)
+    nu_r, uq_r = cref.expert_union(ri, rw, rk, E)[:2]
+    assert nu.value == nu_r and np.array_equal(uq[:nu_r], uq_r)
+    assert rel_err(out, ref, mag).max() <= TOL
