@@ -1,0 +1,364 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized MoE expert hot path on one MI355X.
+
+Headline (BASELINE.json metric "expert GEMV HBM GB/s (% of 8 TB/s peak) +
+MoE-layer tokens/s, 1 GPU"):
+
+  value      = algorithmic GB/s of the dense int4-g32 GEMV workload of
+               W_up 14336x4096 then W_down 4096x14336 (Llama-8B
+               FFN shape), at batch 1, 4, 8 and 16. One step = the up and
+               down GEMV at each of the four batch sizes (8 GEMVs), inputs
+               resident in HBM. Weight copies rotate through >= 2 GB of
+               distinct memory so the 256 MB MALL cannot serve them.
+  roofline   = the GEMV kernel alone (coli_gemv_tiles), bracketed by HIP
+               events on the backend stream, against 8 TB/s.
+  moe_layer  = tokens/s of one fused MoE layer (router -> union -> experts
+               -> SwiGLU -> scatter) for configs[0] (OLMoE-shaped, int4) and
+               configs[2] (DeepSeek-V3-shaped, MXFP4, + shared expert).
+  cpu_baseline = the reference's own OpenMP CPU kernel (c/quant.h
+               matmul_i4_grouped, compiled from its sources into
+               oracle/_ref) on this host's cores, bounded sample.
+
+Algorithmic bytes per GEMV = O*I/2 nibble bytes + O*I/32 scales (2 bytes
+fp16 for int4, 1 byte e8m0 for MXFP4) + bf16 activations in and out; each
+weight byte counted once per call. Synthetic data, seeded.
+"""
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBS = 8000.0
+BATCHES = (1, 4, 8, 16)
+UP = (14336, 4096)      # (O, I)
+DOWN = (4096, 14336)
+METRIC = "expert GEMV HBM GB/s (% of 8 TB/s peak) + MoE-layer tokens/s, 1 GPU"
+
+
+def bytes_i4(O, I, B):
+    return O * I // 2 + O * (I // 32) * 2 + B * I * 2 + B * O * 2
+
+
+def bytes_fp4(O, I, B):
+    return O * I // 2 + O * (I // 32) + B * I * 2 + B * O * 2
+
+
+def bf16_exact(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def fp16_scales(rng, O, ng):
+    return np.abs(rng.standard_normal((O, ng)) * 0.01).astype(np.float16).astype(np.float32)
+
+
+class Bench:
+    def __init__(self, args):
+        from colibri_amd.backend import Session
+        from colibri_amd import hiprt
+        self.args = args
+        self.hiprt = hiprt
+        self.s = Session(0)
+        self.b = self.s.b
+        self.stream = self.b.hip_stream(0)
+        self.rng = np.random.default_rng(1234)
+        self.allocs = []
+
+    def alloc(self, nbytes):
+        p = self.b.cuda_pipe_alloc(0, nbytes)
+        if not p:
+            raise RuntimeError("device allocation failed")
+        self.allocs.append(p)
+        return p
+
+    def put(self, arr):
+        arr = np.ascontiguousarray(arr)
+        p = self.alloc(arr.nbytes)
+        if not self.b.cuda_pipe_upload(0, p, arr.ctypes.data_as(C.c_void_p), arr.nbytes):
+            raise RuntimeError("upload failed")
+        return p
+
+    # -- tensors with device-generated weights ------------------------------
+    def tensor_i4(self, stage, O, I, scales, seed):
+        nb = O * ((I + 1) // 2)
+        assert self.b.hip_fill_random_u8(0, stage, nb, seed)
+        h = C.c_void_p()
+        from colibri_amd.backend import f32p
+        sc = np.ascontiguousarray(scales, np.float32)
+        if not self.b.hip_tensor_upload_from_device(C.byref(h), stage, f32p(sc), None, 4, I, O, 0, 32):
+            raise RuntimeError("upload_from_device (int4) failed")
+        return h
+
+    def tensor_fp4(self, stage, O, I, e8, seed):
+        nb = O * ((I + 1) // 2)
+        assert self.b.hip_fill_random_u8(0, stage, nb, seed)
+        h = C.c_void_p()
+        from colibri_amd.backend import u8p
+        e8 = np.ascontiguousarray(e8, np.uint8)
+        if not self.b.hip_tensor_upload_from_device(C.byref(h), stage, None, u8p(e8), 7, I, O, 0, 32):
+            raise RuntimeError("upload_from_device (mxfp4) failed")
+        return h
+
+    # -- dense GEMV ---------------------------------------------
+    def dense(self):
+        b, hrt = self.b, self.hiprt
+        pair = bytes_i4(*UP, 0) + bytes_i4(*DOWN, 0)
+        copies = max(2, math.ceil(self.args.anticache_gb * 1e9 / pair))
+        stage = self.alloc(UP[0] * UP[1] // 2)
+        sc_up = fp16_scales(self.rng, UP[0], UP[1] // 32)
+        sc_dn = fp16_scales(self.rng, DOWN[0], DOWN[1] // 32)
+        ups, downs = [], []
+        for c in range(copies):
+            ups.append(self.tensor_i4(stage, *UP, np.roll(sc_up, 7 * c, axis=0), 2 * c + 1))
+            downs.append(self.tensor_i4(stage, *DOWN, np.roll(sc_dn, 7 * c, axis=0), 2 * c + 2))
+        x = bf16_exact(self.rng.standard_normal((16, UP[1])).astype(np.float32))
+        xd = self.put(x)
+        hd = self.alloc(16 * UP[0] * 4)
+        yd = self.alloc(16 * DOWN[0] * 4)
+        K, W = self.args.steps, self.args.warmup
+        nev = K * len(BATCHES) * 2
+        ev = [(hrt.Event(), hrt.Event()) for _ in range(nev)]
+        state = {"c": 0}
+
+        def step(record):
+            k = 0
+            for B in BATCHES:
+                c = state["c"] % copies
+                state["c"] += 1
+                ok = b.hip_gemm_prep_dev(ups[c], xd, B)
+                if record: record[k][0].record(self.stream)
+                ok &= b.hip_gemm_run_dev(ups[c], hd, B)
+                if record: record[k][1].record(self.stream)
+                ok &= b.hip_gemm_prep_dev(downs[c], hd, B)
+                if record: record[k + 1][0].record(self.stream)
+                ok &= b.hip_gemm_run_dev(downs[c], yd, B)
+                if record: record[k + 1][1].record(self.stream)
+                k += 2
+                if not ok:
+                    raise RuntimeError("GEMV launch failed")
+
+        for _ in range(W):
+            step(None)
+        hrt.device_sync()
+        t0 = time.perf_counter()
+        for k in range(K):
+            step(ev[k * len(BATCHES) * 2:(k + 1) * len(BATCHES) * 2])
+        hrt.device_sync()
+        wall = time.perf_counter() - t0
+        durs = np.array([a.elapsed_ms(z) for a, z in ev]).reshape(K, len(BATCHES), 2)
+        step_bytes = sum(bytes_i4(*UP, B) + bytes_i4(*DOWN, B) for B in BATCHES)
+        by_batch = {}
+        kern_bytes, kern_ms = 0.0, 0.0
+        for j, B in enumerate(BATCHES):
+            bu, bd = bytes_i4(*UP, B), bytes_i4(*DOWN, B)
+            mu, md = durs[:, j, 0].mean(), durs[:, j, 1].mean()
+            by_batch[str(B)] = {
+                "up_us": round(mu * 1e3, 2), "down_us": round(md * 1e3, 2),
+                "up_GBs": round(bu / mu / 1e6, 1), "down_GBs": round(bd / md / 1e6, 1),
+                "frac_of_peak": round((bu + bd) / (mu + md) / 1e6 / PEAK_GBS, 3),
+            }
+            kern_bytes += K * (bu + bd)
+            kern_ms += durs[:, j, :].sum()
+        kern_gbs = kern_bytes / kern_ms / 1e6
+        value = K * step_bytes / wall / 1e9
+        self.dense_result = dict(value=value, wall=wall, K=K, W=W, by_batch=by_batch, copies=copies,
+                                 kern_gbs=kern_gbs, kern_avg_us=kern_ms / (K * len(BATCHES) * 2) * 1e3,
+                                 kern_avg_bytes=kern_bytes / (K * len(BATCHES) * 2), pair=pair)
+        # host copy of copy 0 for the CPU baseline
+        if not self.args.skip_cpu:
+            self.cpu_inputs = {}
+            for name, (O, I), sc, seed in (("up", UP, sc_up, 1), ("down", DOWN, sc_dn, 2)):
+                nb = O * I // 2
+                assert b.hip_fill_random_u8(0, stage, nb, seed)
+                q = np.empty(nb, np.uint8)
+                assert b.cuda_pipe_download(0, stage, q.ctypes.data_as(C.c_void_p), nb)
+                self.cpu_inputs[name] = (q.reshape(O, I // 2), sc)
+            self.cpu_x = x
+        for t in ups + downs:
+            b.cuda_tensor_free(t)
+
+    # -- CPU baseline: the reference's own kernel ------------------------------
+    def cpu_baseline(self):
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        from oracle_lib import REF_PATH, Ref, Cref
+        kind = "reference" if os.path.exists(REF_PATH) else "port"
+        lib = Ref() if kind == "reference" else Cref()
+        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        (qu, su), (qd, sd) = self.cpu_inputs["up"], self.cpu_inputs["down"]
+        h = np.empty((16, UP[0]), np.float32)
+
+        def one_pass():
+            nbytes = 0
+            for B in BATCHES:
+                xb = np.ascontiguousarray(self.cpu_x[:B])
+                h[:B] = lib.matmul_i4_grouped(xb, qu, su, UP[0], UP[1], 32)
+                lib.matmul_i4_grouped(np.ascontiguousarray(h[:B]), qd, sd, DOWN[0], DOWN[1], 32)
+                nbytes += bytes_i4(*UP, B) + bytes_i4(*DOWN, B)
+            return nbytes
+
+        one_pass()                       # warm the page cache / thread pool
+        t0 = time.perf_counter()
+        nbytes, reps = 0, 0
+        while time.perf_counter() - t0 < self.args.cpu_seconds:
+            nbytes += one_pass()
+            reps += 1
+        dt = time.perf_counter() - t0
+        return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+                "sample": f"{reps} passes of the bench step (up+down GEMV at batch 1/4/8/16) over one "
+                          f"weight copy, {dt:.1f} s, c/quant.h matmul_i4_grouped (AVX2+FMA, OpenMP)",
+                "ms_per_step": round(dt / reps * 1e3, 2)}
+
+    # -- fused MoE layer ------------------------------
+    def moe(self, name, fmt, D, I, E, K, mode, shared, batches, layers_for_anticache, bias, zipf=None):
+        from colibri_amd.backend import ColiHipMoeConfig, f32p, tensor_array
+        b, hrt = self.b, self.hiprt
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        from oracle_lib import Cref
+        cref = Cref()
+        per_expert = 2 * (bytes_i4(I, D, 0) if fmt == 4 else bytes_fp4(I, D, 0)) + \
+            (bytes_i4(D, I, 0) if fmt == 4 else bytes_fp4(D, I, 0))
+        n_layers = layers_for_anticache
+        stage = self.alloc(max(I * D // 2, D * I // 2))
+        layers = []
+        seed = 1000
+        for L in range(n_layers):
+            hs = []
+            for e in range(E + (1 if shared else 0)):
+                trip = []
+                for (O, II) in ((I, D), (I, D), (D, I)):
+                    seed += 1
+                    if fmt == 4:
+                        trip.append(self.tensor_i4(stage, O, II, fp16_scales(self.rng, O, II // 32), seed))
+                    else:
+                        e8 = self.rng.integers(119, 124, (O, II // 32), dtype=np.uint8)
+                        trip.append(self.tensor_fp4(stage, O, II, e8, seed))
+                hs.append(trip)
+            W = (self.rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+            bvec = (self.rng.standard_normal(E) * 0.01).astype(np.float32) if bias else None
+            routed = hs[:E]
+            sh = hs[E] if shared else [None, None, None]
+            g, ga = tensor_array([t[0] for t in routed])
+            u, ua = tensor_array([t[1] for t in routed])
+            d, da = tensor_array([t[2] for t in routed])
+            cfg = ColiHipMoeConfig(D, I, E, K, mode, 0, 0.0, 1.0, 1 if shared else 0)
+            m = C.c_void_p()
+            if not b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(W), f32p(bvec) if bias else None,
+                                    g, u, d, sh[0], sh[1], sh[2]):
+                raise RuntimeError("moe_create failed")
+            layers.append((m, hs, W, bvec))
+        npool = 64
+        xpool = bf16_exact(self.rng.standard_normal((npool, D)).astype(np.float32))
+        xd = self.put(xpool)
+        od = self.alloc(64 * D * 4)
+        result = {}
+        for B in batches:
+            steps = self.args.moe_steps
+            # unique experts per call, from the reference router on the same inputs
+            nus = []
+            for k in range(steps):
+                L = k % n_layers
+                rows = [(k * B + r) % npool for r in range(B)]
+                xb = np.ascontiguousarray(xpool[rows])
+                W, bvec = layers[L][2], layers[L][3]
+                idx, _, keff = cref.route(cref.matmul_f32(xb, W), K, mode, bias=bvec)
+                nus.append(len({int(e) for s in range(B) for e in idx[s, :keff[s]]}) + (1 if shared else 0))
+            ev = [(hrt.Event(), hrt.Event()) for _ in range(steps)]
+
+            def call(k, rec=None):
+                L = k % n_layers
+                r0 = (k * B) % npool
+                if r0 + B > npool:
+                    r0 = 0
+                if rec: rec[0].record(self.stream)
+                ok = b.hip_moe_forward_dev(layers[L][0], C.c_void_p(xd + r0 * D * 4), od, B)
+                if rec: rec[1].record(self.stream)
+                if not ok:
+                    raise RuntimeError("moe forward failed")
+
+            for k in range(self.args.warmup):
+                call(k)
+            hrt.device_sync()
+            t0 = time.perf_counter()
+            for k in range(steps):
+                call(k, ev[k])
+            hrt.device_sync()
+            wall = time.perf_counter() - t0
+            ms = np.array([a.elapsed_ms(z) for a, z in ev])
+            router = E * D * 4
+            byts = np.array([nu * per_expert + router + 2 * B * D * 2 for nu in nus], np.float64)
+            result[f"B{B}"] = {"tokens_per_s": round(B * steps / wall, 1),
+                               "layer_us": round(ms.mean() * 1e3, 2),
+                               "layer_us_wall": round(wall / steps * 1e6, 2),
+                               "avg_unique_experts": round(float(np.mean(nus)), 2),
+                               "GBs": round(byts.sum() / ms.sum() / 1e6, 1),
+                               "frac_of_peak": round(byts.sum() / ms.sum() / 1e6 / PEAK_GBS, 3)}
+        for (m, hs, W, bvec) in layers:
+            b.hip_moe_free(m)
+            for trip in hs:
+                for t in trip:
+                    b.cuda_tensor_free(t)
+        result["layers_cycled"] = n_layers
+        result["weights_GB"] = round(n_layers * (E + (1 if shared else 0)) * per_expert / 1e9, 2)
+        return result
+
+    def close(self):
+        for p in self.allocs:
+            self.b.cuda_pipe_free(0, p)
+        self.s.close()
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--anticache-gb", type=float, default=2.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-moe", action="store_true")
+    ap.add_argument("--moe-steps", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the expert path has no collectives; "
+                                   "run with --gpus 1 (see DESIGN.md for how it would shard)"}))
+        sys.exit(2)
+    bench = Bench(args)
+    bench.dense()
+    r = bench.dense_result
+    out = {
+        "metric": METRIC, "value": round(r["value"], 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(r["wall"] / r["K"] * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int4", "data": "synthetic",
+        "config": {"workload": "configs[1]: dense int4-g32 GEMV, W_up 14336x4096 then W_down 4096x14336, "
+                               "batch 1/4/8/16 per step, fp16 group scales, bf16 activations, f32 accumulate",
+                   "weight_copies": r["copies"], "distinct_weight_GB": round(r["copies"] * r["pair"] / 1e9, 2)},
+        "frac_of_peak": round(r["value"] / PEAK_GBS, 3),
+        "roofline": {"bound": "hbm", "achieved": round(r["kern_gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r["kern_gbs"] / PEAK_GBS, 3), "traffic": None,
+                     "kernel": "coli_gemv_tiles", "avg_launch_us": round(r["kern_avg_us"], 2),
+                     "avg_launch_bytes": int(r["kern_avg_bytes"])},
+        "gemv_by_batch": r["by_batch"],
+    }
+    if not args.skip_moe:
+        out["moe_layer"] = {
+            "configs[0]_olmoe_int4": bench.moe("olmoe", 4, 2048, 1024, 64, 8, 0, False, (1,), 10, False),
+            "configs[2]_dsv3_mxfp4": bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 16), 1, True),
+        }
+    if not args.skip_cpu:
+        out["cpu_baseline"] = bench.cpu_baseline()
+    bench.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

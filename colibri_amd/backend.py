@@ -101,6 +101,8 @@ _SIGS = {
     "coli_hip_moe_forward": ([_vp, _f, _f, _i, _i32, _f, _i32], _i),
     "coli_hip_moe_last_union": ([_vp, _i32, _i32], _i),
     "coli_hip_stream": ([_i], _vp),
+    "coli_hip_tensor_upload_from_device": ([_tpp, _vp, _f, _u8, _i, _i, _i, _i, _i], _i),
+    "coli_hip_fill_random_u8": ([_i, _vp, _sz, C.c_ulonglong], _i),
     "coli_hip_gemm_prep_dev": ([_tp, _vp, _i], _i),
     "coli_hip_gemm_run_dev": ([_tp, _vp, _i], _i),
     "coli_hip_tensor_stream_bytes": ([_tp], _sz),

@@ -124,7 +124,10 @@ extern "C" int coli_cuda_init(const int *devices, int count) {
             g_nctx = 0;
             return 0;
         }
-        if (!reserve(ctx, &ctx->flags, 64 * sizeof(int), 1)) { g_nctx = 0; return 0; }
+        if (!reserve(ctx, &ctx->flags, 64 * sizeof(int), 1) || !reserve(ctx, &ctx->zeros, COLI_ZERO_BYTES, 1)) {
+            g_nctx = 0;
+            return 0;
+        }
         g_nctx++;
         std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs\n", device, prop.name,
                      prop.gcnArchName, prop.totalGlobalMem / 1e9, prop.multiProcessorCount);
@@ -262,20 +265,23 @@ static size_t src_scale_count(int fmt, int I, int O, int gs) {
 
 // Copy source bytes to the device and build the tiled layout of t.
 static int fill_tensor(DevCtx *ctx, ColiCudaTensor *t, const void *weights, const void *scales_src,
-                       size_t scale_src_bytes) {
+                       size_t scale_src_bytes, int w_on_device = 0) {
     size_t rb = (size_t)(t->I + 1) / 2, wsrc = rb * t->O;
+    hipMemcpyKind wkind = w_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
     if (t->kind == COLI_KIND_GENERIC) {
-        if (!hip_ok(hipMemcpy(t->w, weights, wsrc, hipMemcpyHostToDevice), "tensor upload") ||
+        if (!hip_ok(hipMemcpy(t->w, weights, wsrc, wkind), "tensor upload") ||
             !hip_ok(hipMemcpy(t->sc, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
             return 0;
         return 1;
     }
-    if (!reserve(ctx, &ctx->stage_w, wsrc, 0) || !reserve(ctx, &ctx->stage_s, scale_src_bytes, 0)) return 0;
+    if ((!w_on_device && !reserve(ctx, &ctx->stage_w, wsrc, 0)) || !reserve(ctx, &ctx->stage_s, scale_src_bytes, 0))
+        return 0;
     if (!hip_ok(hipStreamSynchronize(ctx->stream), "upload sync") ||
-        !hip_ok(hipMemcpy(ctx->stage_w.p, weights, wsrc, hipMemcpyHostToDevice), "tensor upload") ||
+        (!w_on_device && !hip_ok(hipMemcpy(ctx->stage_w.p, weights, wsrc, hipMemcpyHostToDevice), "tensor upload")) ||
         !hip_ok(hipMemcpy(ctx->stage_s.p, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
         return 0;
-    if (!hip_ok(coli_launch_repack(t, (const uint8_t *)ctx->stage_w.p, ctx->stage_s.p, ctx->stream),
+    const uint8_t *wsrc_dev = w_on_device ? (const uint8_t *)weights : (const uint8_t *)ctx->stage_w.p;
+    if (!hip_ok(coli_launch_repack(t, wsrc_dev, ctx->stage_s.p, ctx->stream),
                 "tile repack"))
         return 0;
     return hip_ok(hipStreamSynchronize(ctx->stream), "tile repack sync");
@@ -324,7 +330,7 @@ static ColiCudaTensor *alloc_tensor(DevCtx *ctx, int fmt, int I, int O, int gs, 
 
 // Upload for fmt 2 / 4 (f32 scales) and fmt 7 (e8 bytes, or f32 powers of two).
 int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scales, const uint8_t *e8,
-                int fmt, int I, int O, int device, int gs) {
+                int fmt, int I, int O, int device, int gs, int w_on_device) {
     if (!tensor) return 0;
     int want_gs = (fmt == 4 && gs > 0) ? gs : (fmt == 7 ? 32 : 0);
     if (*tensor) {
@@ -365,7 +371,7 @@ int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scale
     }
     ColiCudaTensor *t = alloc_tensor(ctx, fmt, I, O, want_gs, kind);
     if (!t) return 0;
-    if (!fill_tensor(ctx, t, weights, ssrc, sbytes)) {
+    if (!fill_tensor(ctx, t, weights, ssrc, sbytes, w_on_device)) {
         coli_cuda_tensor_free(t);
         return 0;
     }
@@ -375,18 +381,18 @@ int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scale
 
 extern "C" int coli_cuda_tensor_upload_g(ColiCudaTensor **tensor, const void *weights, const float *scales,
                                          int fmt, int I, int O, int device, int gs) {
-    return upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, gs > 0 ? gs : 0);
+    return upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, gs > 0 ? gs : 0, 0);
 }
 
 extern "C" int coli_cuda_tensor_upload(ColiCudaTensor **tensor, const void *weights, const float *scales,
                                        int fmt, int I, int O, int device) {
-    return upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, fmt == 7 ? 32 : 0);
+    return upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, fmt == 7 ? 32 : 0, 0);
 }
 
 extern "C" int coli_hip_tensor_upload_mxfp4(ColiCudaTensor **tensor, const unsigned char *q4,
                                             const unsigned char *e8, int I, int O, int device) {
     if (!e8) return 0;
-    return upload_impl(tensor, q4, nullptr, e8, 7, I, O, device, 32);
+    return upload_impl(tensor, q4, nullptr, e8, 7, I, O, device, 32, 0);
 }
 
 extern "C" int coli_hip_tensor_upload_fp4_rows16(ColiCudaTensor **tensor, const unsigned char *pd,
@@ -401,7 +407,16 @@ extern "C" int coli_hip_tensor_upload_fp4_rows16(ColiCudaTensor **tensor, const 
         for (size_t c = 0; c < ds; c++) q4[r * ds + c] = pd[(tile * ds + c) * 16 + lane];
         for (size_t c = 0; c < ss; c++) e8[r * ss + c] = ps[(tile * ss + c) * 16 + lane];
     }
-    return upload_impl(tensor, q4.data(), nullptr, e8.data(), 7, I, O, device, 32);
+    return upload_impl(tensor, q4.data(), nullptr, e8.data(), 7, I, O, device, 32, 0);
+}
+
+extern "C" int coli_hip_tensor_upload_from_device(ColiCudaTensor **tensor, const void *weights_dev,
+                                                  const float *scales, const unsigned char *e8, int fmt, int I,
+                                                  int O, int device, int gs) {
+    if (!tensor || *tensor) return 0;   // a fresh tensor only: no cached-handle reuse here
+    if (fmt == 7 && !e8) return 0;
+    return upload_impl(tensor, weights_dev, fmt == 7 ? nullptr : scales, fmt == 7 ? e8 : nullptr, fmt, I, O, device,
+                       fmt == 7 ? 32 : (gs > 0 ? gs : 0), 1);
 }
 
 extern "C" void coli_cuda_tensor_free(ColiCudaTensor *t) {
@@ -440,6 +455,13 @@ extern "C" int coli_cuda_tensor_update(ColiCudaTensor *t, const void *weights, c
         return 0;
     }
     return fill_tensor(ctx, t, weights, scales, ns * sizeof(float));
+}
+
+extern "C" int coli_hip_fill_random_u8(int device, void *dev, size_t n, unsigned long long seed) {
+    DevCtx *ctx = find_ctx(device);
+    if (!dev || !select_ctx(ctx)) return 0;
+    return hip_ok(coli_launch_fill_random(dev, n, seed, ctx->stream), "random fill") &&
+           hip_ok(hipStreamSynchronize(ctx->stream), "random fill sync");
 }
 
 extern "C" void *coli_hip_stream(int device) {

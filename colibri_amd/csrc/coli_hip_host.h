@@ -49,11 +49,12 @@ int reserve(DevCtx *ctx, DevBuf *b, size_t bytes, int zero);
 int reserve_pinned(DevCtx *ctx, void **p, size_t *cap, size_t bytes);
 void note_group(DevCtx *ctx, int count, int total, double h2d, double ker, double d2h);
 int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scales, const uint8_t *e8,
-                int fmt, int I, int O, int device, int gs);
+                int fmt, int I, int O, int device, int gs, int w_on_device);
 
 // kernels (gemv.hip / pipe.hip)
 extern "C" {
-hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, int max_rows, hipStream_t st);
+hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, int W, int max_rows,
+                            hipStream_t st);
 hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, const int *nrows_dev,
                                  int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
                                  int *exp2out, int *haslo, hipStream_t st);
@@ -68,6 +69,7 @@ hipError_t coli_launch_router_select(const float *logits, const float *bias, int
                                      float topp, int norm_topk, float routed_scale, int *idx, float *w,
                                      int *keff, hipStream_t st);
 hipError_t coli_launch_zero_i32(int *p, int n, hipStream_t st);
+hipError_t coli_launch_fill_random(void *dev, size_t n, unsigned long long seed, hipStream_t st);
 hipError_t coli_launch_silu_mul(float *gate, const float *up, size_t n, hipStream_t st);
 hipError_t coli_launch_silu_mul_to(float *h, const float *gate, const float *up, size_t n, hipStream_t st);
 hipError_t coli_launch_add_n(float *x, const float *t, size_t n, hipStream_t st);
@@ -81,6 +83,6 @@ hipError_t coli_launch_sum_slots(float *dst, const float *slots, int n, int D, h
 // Expert path runner (expert.hip): one shared routine behind expert_group,
 // issue, expert_mlp, resident_issue and the MoE layer.
 struct GemvLaunchPlan {
-    int R, rbpp, splits, qps;
+    int R, W, rbpp, splits, qps;
 };
-GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual);
+GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual, int max_rows);

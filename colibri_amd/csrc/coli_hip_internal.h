@@ -24,6 +24,7 @@
 #define COLI_TILE_BYTES 1024
 #define COLI_GROUP 32
 #define COLI_DESC_ROWS 64
+#define COLI_ZERO_BYTES (1u << 20)   // covers one fragment row of I <= 512K and a tile + its scales
 
 // Tensor storage kinds.
 enum ColiKind {
@@ -69,6 +70,7 @@ struct ColiGemvArgs {
     int xstride;              // halves per fragment row (= ngp * 32)
     const int *xexp;          // per fragment row
     const int *haslo;
+    const _Float16 *zero;     // >= COLI_ZERO_BYTES of zeros: inactive batch lanes, dead tiles
     float *out;
     int ldo;
     float *partial;

@@ -21,23 +21,36 @@
 // ---------------------------------------------------------------------------
 // planning and launch helpers
 // ---------------------------------------------------------------------------
-GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual) {
+// Work decomposition of one GEMV launch. K is split across the W waves of a
+// group (LDS reduction, no device-scope sync); rows are split across groups.
+//  * R (row tiles per wave) trades activation-fragment re-reads for group
+//    count: with many batch rows the fragments are as large as the weights,
+//    so R = 4 shares each fragment load over four tiles; at B <= 4 R = 2.
+//  * W grows until the launch has about 12 waves per CU, as long as every
+//    wave still gets >= 2 quads.
+//  * Cross-group splits only when even W = 16 leaves the chip mostly idle.
+GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual, int max_rows) {
     GemvLaunchPlan p;
-    int RT;
-    if (dual) {
-        p.R = 4;
-        RT = 2;
-    } else {
-        p.R = nrt >= 4 ? 4 : (nrt >= 2 ? 2 : 1);
+    const long cus = ctx && ctx->cu_count ? ctx->cu_count : 256;
+    const long target_waves = 12 * cus;
+    p.R = max_rows > 4 ? 4 : 2;
+    int RT = dual ? p.R / 2 : p.R;
+    if (!dual && nrt < p.R) {
+        p.R = nrt >= 2 ? 2 : 1;
         RT = p.R;
     }
     p.rbpp = (nrt + RT - 1) / RT;
-    long base = (long)nprob * n_bt * p.rbpp;
-    long target = 4L * (ctx && ctx->cu_count ? ctx->cu_count : 256);
-    int sp = (int)std::max(1L, (target + base - 1) / base);
-    int maxsp = std::max(1, nq / 8);   // keep >= 8 quads (2 per wave) per group
-    sp = std::min(sp, maxsp);
-    p.qps = (nq + sp - 1) / sp;
+    long groups = (long)nprob * n_bt * p.rbpp;
+    p.W = 4;
+    const int wmax = p.R == 4 ? 8 : 16;   // 1024-thread groups only within the 128-VGPR budget
+    while (p.W < wmax && groups * p.W < target_waves && nq >= 2 * (2 * p.W)) p.W *= 2;
+    p.splits = 1;
+    if (groups * p.W < target_waves / 4 && nq >= 4 * p.W) {
+        long want = (target_waves / 4 + groups * p.W - 1) / (groups * p.W);
+        p.splits = (int)std::min<long>(want, nq / (2 * p.W));
+        if (p.splits < 1) p.splits = 1;
+    }
+    p.qps = (nq + p.splits - 1) / p.splits;
     p.splits = (nq + p.qps - 1) / p.qps;
     return p;
 }
@@ -76,7 +89,7 @@ static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
                     const int *xrows_dev, float *out, int ldo) {
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
-    GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual);
+    GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
     size_t inst = (size_t)nprob * n_bt * pl.rbpp;
     if (pl.splits > 1) {
         if (!reserve(ctx, &ctx->partial, inst * pl.splits * pl.R * 4 * 64 * sizeof(float), 0) ||
@@ -101,11 +114,12 @@ static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
     a.xstride = nq * 4 * 32;
     a.xexp = (const int *)f.exp.p;
     a.haslo = (const int *)ctx->flags.p + set;
+    a.zero = (const _Float16 *)ctx->zeros.p;
     a.out = out;
     a.ldo = ldo;
     a.partial = (float *)ctx->partial.p;
     a.counters = (unsigned *)ctx->counters.p;
-    return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, max_rows, ctx->stream), "gemv launch");
+    return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
 }
 
 static int frag_set_of(int kind, bool hidden) {
@@ -459,7 +473,7 @@ extern "C" int coli_cuda_matmul(ColiCudaTensor **tensor, float *y, const float *
     if (fault_injected()) return 0;
     if (fmt == 4 && gs <= 0) return 0;
     if (S < 1 || !y || !x || !tensor) return 0;
-    if (!upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, gs > 0 ? gs : (fmt == 7 ? 32 : 0)))
+    if (!upload_impl(tensor, weights, scales, nullptr, fmt, I, O, device, gs > 0 ? gs : (fmt == 7 ? 32 : 0), 0))
         return 0;
     ColiCudaTensor *t = *tensor;
     if (!tensor_computable(t)) return 0;

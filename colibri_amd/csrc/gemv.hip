@@ -34,6 +34,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Loads through address-space-1 pointers: pointers read from descriptors are
+// generic to the compiler, and generic (FLAT) loads may complete out of order,
+// which forces a full vmcnt(0) drain before every use. Global loads keep the
+// in-order counter the software pipeline relies on.
+#define GPTR(T, p) ((const __attribute__((address_space(1))) T *)(const void *)(p))
+
 // ---------------------------------------------------------------------------
 // Upload-time repack kernels
 // ---------------------------------------------------------------------------
@@ -191,7 +197,7 @@ template <int KIND> struct ScaleRegs;
 template <> struct ScaleRegs<COLI_KIND_I4_H> {
     u32x2 v;
     __device__ void load(const void *base, size_t tq, int r16) {
-        v = *(const u32x2 *)((const uint8_t *)base + (tq * 16 + r16) * 8);
+        v = *GPTR(u32x2, (const uint8_t *)base + (tq * 16 + r16) * 8);
     }
     __device__ float get(int j) const {
         uint32_t wd = v[j >> 1];
@@ -203,7 +209,7 @@ template <> struct ScaleRegs<COLI_KIND_I4_H> {
 template <> struct ScaleRegs<COLI_KIND_I4_F> {
     floatx4 v;
     __device__ void load(const void *base, size_t tq, int r16) {
-        v = *(const floatx4 *)((const uint8_t *)base + (tq * 16 + r16) * 16);
+        v = *GPTR(floatx4, (const uint8_t *)base + (tq * 16 + r16) * 16);
     }
     __device__ float get(int j) const { return v[j]; }
     __device__ void zero() { v = (floatx4){0.f, 0.f, 0.f, 0.f}; }
@@ -211,7 +217,7 @@ template <> struct ScaleRegs<COLI_KIND_I4_F> {
 template <> struct ScaleRegs<COLI_KIND_FP4> {
     uint32_t v;
     __device__ void load(const void *base, size_t tq, int r16) {
-        v = *(const uint32_t *)((const uint8_t *)base + (tq * 16 + r16) * 4);
+        v = *GPTR(uint32_t, (const uint8_t *)base + (tq * 16 + r16) * 4);
     }
     __device__ float get(int j) const {
         return __builtin_bit_cast(float, ((v >> (8 * j)) & 0xFFu) << 23);
@@ -223,18 +229,90 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
-// One workgroup (4 waves) = one work item: (problem, batch tile, row block,
-// K split). The 4 waves interleave over the item's quads (wave w takes quads
-// Q0+w, Q0+w+4, ...) so the group streams contiguous tile memory together,
-// then reduce through LDS in fixed wave order. R = row tiles accumulated per
-// wave; DUAL: tiles [0, R/2) come from w0 (gate) and [R/2, R) from w1 (up) over
-// the same rows. NB4 = accumulator rows per lane that can hold real batch rows
-// (1, 2 or 4): the MFMA result row of lane l, register i is batch row
-// 4*(l/16)+i, its column is output row 16*tile + (l%16).
-template <int KIND, int R, bool DUAL, int NB4>
-__global__ __launch_bounds__(256) void coli_gemv_tiles(ColiGemvArgs a) {
+// One pipeline stage: everything one quad (4 groups x R tiles) of one wave
+// reads from memory.
+template <int KIND, int R, bool LO>
+struct Stage {
+    u32x4 w[R];
+    ScaleRegs<KIND> sc[R];
+    half8v xh[4];
+    half8v xl[LO ? 4 : 1];
+};
+
+// Main loop of one wave over quads q = q_first, q_first+4, ... < Q1.
+// Loads of quad q+4 are issued before the math of quad q, as one branch-free
+// batch (dead tiles read a valid tile and get a zero scale), so the wave
+// keeps a full stage in flight while it computes and the waits before the
+// math only cover the current stage.
+template <int KIND, int R, int NB4, int W, bool LO>
+__device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], int q_first, int Q1, const size_t (&tbase)[R],
+                                           const int (&tstep)[R], const uint8_t *const (&wb)[R],
+                                           const void *const (&sb)[R], const _Float16 *xh, const _Float16 *xl,
+                                           int lane) {
+    Stage<KIND, R, LO> cur, nxt;
+    auto load = [&](Stage<KIND, R, LO> &st, int q) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            size_t tq = tbase[r] + (size_t)q * tstep[r];
+            st.w[r] = __builtin_nontemporal_load(GPTR(u32x4, wb[r] + tq * COLI_TILE_BYTES) + lane);
+            st.sc[r].load(sb[r], tq, lane & 15);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            st.xh[j] = *GPTR(half8v, xh + (size_t)(4 * q + j) * 32);
+            if constexpr (LO) st.xl[j] = *GPTR(half8v, xl + (size_t)(4 * q + j) * 32);
+        }
+    };
+    auto compute = [&](const Stage<KIND, R, LO> &st) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                half8v bw = unpack_b<KIND>(st.w[r][j]);
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.xl[j], bw, d, 0, 0, 0);
+                float scl = st.sc[r].get(j);
+#pragma unroll
+                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
+            }
+        }
+    };
+    // Ping-pong between two stages (no register copies, which would wait on
+    // the prefetch): stage A holds quad q, stage B quad q+W.
+    if (q_first >= Q1) return;
+    load(cur, q_first);
+    int q = q_first;
+    for (; q + 2 * W < Q1; q += 2 * W) {
+        load(nxt, q + W);
+        compute(cur);
+        load(cur, q + 2 * W);
+        compute(nxt);
+    }
+    if (q + W < Q1) {
+        load(nxt, q + W);
+        compute(cur);
+        compute(nxt);
+    } else {
+        compute(cur);
+    }
+}
+
+// One workgroup (W waves) = one work item: (problem, batch tile, row block,
+// K split). The W waves interleave over the item's quads (wave w takes quads
+// Q0+w, Q0+w+W, ...) so the group streams contiguous tile memory together,
+// then reduce through LDS in fixed wave order: K is split inside the group,
+// which needs no device-scope synchronization. A cross-group split (splits
+// > 1) exists only for shapes too small to fill the chip otherwise; it uses a
+// fixed-order reduction by the last-arriving group.
+// R = row tiles accumulated per wave; DUAL: tiles [0, R/2) come from w0
+// (gate) and [R/2, R) from w1 (up) over the same rows. NB4 = accumulator rows
+// per lane that can hold real batch rows (1, 2 or 4): the MFMA result row of
+// lane l, register i is batch row 4*(l/16)+i, its column is output row
+// 16*tile + (l%16).
+template <int KIND, int R, bool DUAL, int NB4, int W>
+__global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     constexpr int RT = DUAL ? R / 2 : R;
-    __shared__ float red[4][R * 4][64];
+    __shared__ float red[W][R * NB4][64];
     __shared__ unsigned last_flag;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int item = blockIdx.x;
@@ -256,91 +334,58 @@ __global__ __launch_bounds__(256) void coli_gemv_tiles(ColiGemvArgs a) {
     const int Q0 = s * a.qps, Q1 = min(a.nq, Q0 + a.qps);
     const bool use_lo = *a.haslo != 0;
 
-    const _Float16 *xh = nullptr, *xl = nullptr;
+    // Lanes past the problem's rows read the zero fragment row.
+    const _Float16 *xh = a.zero, *xl = a.zero;
     if (b < nb) {
-        int fr = a.xrows[pr.xrow_off + 16 * bt + b];
+        const int fr = a.xrows[pr.xrow_off + 16 * bt + b];
         xh = a.xhi + (size_t)fr * a.xstride + ks * 8;
         xl = a.xlo + (size_t)fr * a.xstride + ks * 8;
     }
 
+    // Row tiles past the matrix read the zero buffer (zero scale: no contribution).
     int rt[R];
     bool live[R];
     const uint8_t *wb[R];
     const void *sb[R];
+    size_t tbase[R];
+    int tstep[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         int rr = DUAL ? (r % RT) : r;
         rt[r] = rb * RT + rr;
         live[r] = rt[r] < a.nrt;
         bool second = DUAL && r >= RT;
-        wb[r] = second ? pr.w1 : pr.w0;
-        sb[r] = second ? pr.s1 : pr.s0;
+        wb[r] = live[r] ? (second ? pr.w1 : pr.w0) : (const uint8_t *)a.zero;
+        sb[r] = live[r] ? (second ? pr.s1 : pr.s0) : (const void *)a.zero;
+        tbase[r] = live[r] ? (size_t)rt[r] * a.nq : 0;
+        tstep[r] = live[r] ? 1 : 0;
     }
 
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, lane);
+    else gemv_quads<KIND, R, NB4, W, false>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, lane);
 
-    u32x4 wv[R];
-    ScaleRegs<KIND> sc[R];
-    auto load_q = [&](int q) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (live[r]) {
-                size_t tq = (size_t)rt[r] * a.nq + q;
-                wv[r] = __builtin_nontemporal_load((const u32x4 *)(wb[r] + tq * COLI_TILE_BYTES) + lane);
-                sc[r].load(sb[r], tq, lane & 15);
-            } else {
-                wv[r] = (u32x4){0u, 0u, 0u, 0u};
-                sc[r].zero();
-            }
-        }
-    };
-
-    int q = Q0 + wave;
-    if (q < Q1) load_q(q);
-    for (; q < Q1; q += 4) {
-        u32x4 cw[R];
-        ScaleRegs<KIND> cs[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) { cw[r] = wv[r]; cs[r] = sc[r]; }
-        if (q + 4 < Q1) load_q(q + 4);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int g = 4 * q + j;
-            half8v ah = (half8v){0, 0, 0, 0, 0, 0, 0, 0}, al = ah;
-            if (xh) {
-                ah = *(const half8v *)(xh + (size_t)g * 32);
-                if (use_lo) al = *(const half8v *)(xl + (size_t)g * 32);
-            }
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                half8v bw = unpack_b<KIND>(cw[r][j]);
-                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                if (use_lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw, d, 0, 0, 0);
-                float scl = cs[r].get(j);
-#pragma unroll
-                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
-            }
-        }
-    }
-
-    // ---- intra-group reduction, fixed wave order; wave w finishes register i = w ----
+    // ---- intra-group reduction in fixed wave order; wave i finishes register i ----
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
-        for (int i = 0; i < NB4; i++) red[wave][r * 4 + i][lane] = acc[r][i];
+        for (int i = 0; i < NB4; i++) red[wave][r * NB4 + i][lane] = acc[r][i];
     __syncthreads();
     const int i = wave;
     float v[R];
     if (i < NB4) {
 #pragma unroll
-        for (int r = 0; r < R; r++)
-            v[r] = ((red[0][r * 4 + i][lane] + red[1][r * 4 + i][lane]) + red[2][r * 4 + i][lane]) +
-                   red[3][r * 4 + i][lane];
+        for (int r = 0; r < R; r++) {
+            float t = red[0][r * NB4 + i][lane];
+#pragma unroll
+            for (int w = 1; w < W; w++) t += red[w][r * NB4 + i][lane];
+            v[r] = t;
+        }
     }
 
-    // ---- cross-group split-K: deterministic fixed-order sum by the last group ----
+    // ---- cross-group split-K (small shapes only): fixed-order sum by the last group ----
     if (a.splits > 1) {
         const size_t inst = ((size_t)p * a.n_bt + bt) * a.rb_per_prob + rb;
         if (i < NB4) {
@@ -371,13 +416,13 @@ __global__ __launch_bounds__(256) void coli_gemv_tiles(ColiGemvArgs a) {
     if (i >= NB4) return;
     const int brow = 4 * ks + i;
     if (brow >= nb) return;
-    const int fr = a.xrows[pr.xrow_off + 16 * bt + brow];
-    const int E = a.xexp[fr];
+    const int E = a.xexp[a.xrows[pr.xrow_off + 16 * bt + brow]];
     float *orow = a.out + (size_t)(pr.out_row0 + 16 * bt + brow) * a.ldo;
 #pragma unroll
     for (int r = 0; r < RT; r++) {
+        if (!live[r]) continue;
         const int o = rt[r] * 16 + (lane & 15);
-        if (!live[r] || o >= a.O) continue;
+        if (o >= a.O) continue;
         if constexpr (DUAL) {
             float gv = ldexpf(v[r], E), uv = ldexpf(v[r + RT], E);
             orow[o] = silu_mul(gv, uv);
@@ -483,32 +528,49 @@ struct ColiGemvPlan {
     int R, dual, nb4;
 };
 
-template <int KIND, int R, bool DUAL>
-static hipError_t launch_nb(const ColiGemvArgs &a, int nb4, int blocks, hipStream_t st) {
-    if (nb4 == 1) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, 1>), dim3(blocks), dim3(256), 0, st, a);
-    else if (nb4 == 2) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, 2>), dim3(blocks), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, 4>), dim3(blocks), dim3(256), 0, st, a);
+// 16-wave groups only for R <= 2: at R = 4 the 128-VGPR budget of a
+// 1024-thread group would spill.
+template <int KIND, int R, bool DUAL, int NB4>
+static hipError_t launch_w(const ColiGemvArgs &a, int W, int blocks, hipStream_t st) {
+    if constexpr (R <= 2) {
+        if (W == 16) {
+            hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 16>), dim3(blocks), dim3(1024), 0, st, a);
+            return hipGetLastError();
+        }
+    }
+    if (W >= 8) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 8>), dim3(blocks), dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 4>), dim3(blocks), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
-template <int KIND>
-static hipError_t launch_kind(const ColiGemvArgs &a, int R, bool dual, int nb4, int blocks, hipStream_t st) {
-    if (dual) return launch_nb<KIND, 4, true>(a, nb4, blocks, st);
-    if (R == 4) return launch_nb<KIND, 4, false>(a, nb4, blocks, st);
-    if (R == 2) return launch_nb<KIND, 2, false>(a, nb4, blocks, st);
-    return launch_nb<KIND, 1, false>(a, nb4, blocks, st);
+template <int KIND, int R, bool DUAL>
+static hipError_t launch_nb(const ColiGemvArgs &a, int nb4, int W, int blocks, hipStream_t st) {
+    if (nb4 == 1) return launch_w<KIND, R, DUAL, 1>(a, W, blocks, st);
+    if (nb4 == 2) return launch_w<KIND, R, DUAL, 2>(a, W, blocks, st);
+    return launch_w<KIND, R, DUAL, 4>(a, W, blocks, st);
 }
 
-extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual,
-                                       int max_rows, hipStream_t st) {
+template <int KIND>
+static hipError_t launch_kind(const ColiGemvArgs &a, int R, bool dual, int nb4, int W, int blocks, hipStream_t st) {
+    if (dual) {
+        if (R == 4) return launch_nb<KIND, 4, true>(a, nb4, W, blocks, st);
+        return launch_nb<KIND, 2, true>(a, nb4, W, blocks, st);
+    }
+    if (R == 4) return launch_nb<KIND, 4, false>(a, nb4, W, blocks, st);
+    if (R == 2) return launch_nb<KIND, 2, false>(a, nb4, W, blocks, st);
+    return launch_nb<KIND, 1, false>(a, nb4, W, blocks, st);
+}
+
+extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, int W, int max_rows,
+                                       hipStream_t st) {
     int nb4 = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
     long items = (long)a->nprob * a->n_bt * a->rb_per_prob * a->splits;
     int blocks = (int)items;
     if (blocks <= 0) return hipSuccess;
     switch (kind) {
-    case COLI_KIND_I4_H: return launch_kind<COLI_KIND_I4_H>(*a, R, dual, nb4, blocks, st);
-    case COLI_KIND_I4_F: return launch_kind<COLI_KIND_I4_F>(*a, R, dual, nb4, blocks, st);
-    case COLI_KIND_FP4: return launch_kind<COLI_KIND_FP4>(*a, R, dual, nb4, blocks, st);
+    case COLI_KIND_I4_H: return launch_kind<COLI_KIND_I4_H>(*a, R, dual, nb4, W, blocks, st);
+    case COLI_KIND_I4_F: return launch_kind<COLI_KIND_I4_F>(*a, R, dual, nb4, W, blocks, st);
+    case COLI_KIND_FP4: return launch_kind<COLI_KIND_FP4>(*a, R, dual, nb4, W, blocks, st);
     default: return hipErrorInvalidValue;
     }
 }

@@ -208,8 +208,8 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     // make sure every scratch the kernels touch exists before the first launch
     size_t inst_max = 0;
     {
-        GemvLaunchPlan a = plan_gemv(ctx, P, (S + 15) / 16, (c.I + 15) / 16, nq_d, true);
-        GemvLaunchPlan b = plan_gemv(ctx, P, (S + 15) / 16, (c.D + 15) / 16, nq_i, false);
+        GemvLaunchPlan a = plan_gemv(ctx, P, (S + 15) / 16, (c.I + 15) / 16, nq_d, true, S);
+        GemvLaunchPlan b = plan_gemv(ctx, P, (S + 15) / 16, (c.D + 15) / 16, nq_i, false, S);
         size_t ia = (size_t)P * ((S + 15) / 16) * a.rbpp, ib = (size_t)P * ((S + 15) / 16) * b.rbpp;
         inst_max = std::max(ia, ib);
         size_t pa = a.splits > 1 ? ia * a.splits * a.R * 4 * 64 * 4 : 0;
@@ -242,7 +242,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     if (!hip_ok(hipGetLastError(), "moe union")) return 0;
     // 5. gate/up + SwiGLU over the union
     ColiGemvArgs a;
-    GemvLaunchPlan pl = plan_gemv(ctx, P, (S + 15) / 16, (c.I + 15) / 16, nq_d, true);
+    GemvLaunchPlan pl = plan_gemv(ctx, P, (S + 15) / 16, (c.I + 15) / 16, nq_d, true, S);
     a.prob = m->pdual;
     a.nprob_dev = m->state;
     a.nprob = P;
@@ -259,11 +259,12 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     a.xstride = nq_d * 128;
     a.xexp = (const int *)fx.exp.p;
     a.haslo = flags + ord;
+    a.zero = (const _Float16 *)ctx->zeros.p;
     a.out = m->h;
     a.ldo = c.I;
     a.partial = (float *)ctx->partial.p;
     a.counters = (unsigned *)ctx->counters.p;
-    if (!hip_ok(coli_launch_gemv(m->kind, &a, pl.R, 1, S, st), "moe dual")) return 0;
+    if (!hip_ok(coli_launch_gemv(m->kind, &a, pl.R, 1, pl.W, S, st), "moe dual")) return 0;
     // 6. hidden fragments (valid slots only)
     if (!hip_ok(coli_launch_zero_i32(flags + 2 + ord, 1, st), "moe flag") ||
         !hip_ok(coli_launch_prep_frag(m->h, c.I, m->hrows, m->state + 1, P * RS, c.I, nq_i * 4, !ord,
@@ -271,7 +272,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
                 "moe hidden fragments"))
         return 0;
     // 7. down
-    pl = plan_gemv(ctx, P, (S + 15) / 16, (c.D + 15) / 16, nq_i, false);
+    pl = plan_gemv(ctx, P, (S + 15) / 16, (c.D + 15) / 16, nq_i, false, S);
     a.prob = m->pdown;
     a.nrt = (c.D + 15) / 16;
     a.nq = nq_i;
@@ -287,7 +288,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     a.haslo = flags + 2 + ord;
     a.out = m->y;
     a.ldo = c.D;
-    if (!hip_ok(coli_launch_gemv(m->kind, &a, pl.R, 0, S, st), "moe down")) return 0;
+    if (!hip_ok(coli_launch_gemv(m->kind, &a, pl.R, 0, pl.W, S, st), "moe down")) return 0;
     // 8. combine
     hipLaunchKernelGGL(coli_moe_combine, dim3((c.D + 255) / 256, S), dim3(256), 0, st, m->y, c.D, m->wsel, m->keff,
                        m->slotrow, c.K, m->state, c.has_shared, RS, out_dev);

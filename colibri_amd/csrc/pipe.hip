@@ -329,3 +329,27 @@ extern "C" hipError_t coli_launch_sum_slots(float *dst, const float *slots, int 
     hipLaunchKernelGGL(coli_sum_slots, dim3(48), dim3(256), 0, st, dst, slots, n, D);
     return hipGetLastError();
 }
+
+// Uniform pseudo-random bytes: splitmix64 of (seed, 8-byte word index).
+__global__ void coli_fill_random(uint8_t *dst, size_t n, unsigned long long seed) {
+    size_t w = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; w * 8 < n; w += stride) {
+        unsigned long long z = seed + 0x9E3779B97F4A7C15ull * (w + 1);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        size_t base = w * 8;
+        if (base + 8 <= n) {
+            *(unsigned long long *)(dst + base) = z;   // n-aligned callers: 8-byte stores
+        } else {
+            for (int b = 0; base + b < n; b++) dst[base + b] = (uint8_t)(z >> (8 * b));
+        }
+    }
+}
+
+extern "C" hipError_t coli_launch_fill_random(void *dev, size_t n, unsigned long long seed, hipStream_t st) {
+    if (((uintptr_t)dev & 7) != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(coli_fill_random, dim3(4096), dim3(256), 0, st, (uint8_t *)dev, n, seed);
+    return hipGetLastError();
+}

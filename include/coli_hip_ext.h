@@ -26,6 +26,14 @@ int coli_hip_tensor_upload_fp4_rows16(ColiCudaTensor **tensor, const unsigned ch
                                       const unsigned char *packed_scales, int I, int O,
                                       int device);
 
+/* Upload whose weight source is already in device memory (row-major source
+ * layout, e.g. landed there by a GPU-side loader); scales come from the host:
+ * f32 (fmt 2/4) or ue8m0 bytes (fmt 7, e8 != NULL). Same semantics otherwise
+ * as coli_cuda_tensor_upload_g. */
+int coli_hip_tensor_upload_from_device(ColiCudaTensor **tensor, const void *weights_dev,
+                                       const float *scales, const unsigned char *e8, int fmt,
+                                       int I, int O, int device, int gs);
+
 /* native_quant contract on the device: every activation row is first
  * quantize-dequantized to e4m3 in blocks of 128 with an e8m0 scale
  * (c/deepseek_v4.c:10495-10520), then multiplied with the resident MXFP4
@@ -81,6 +89,9 @@ int coli_hip_moe_last_union(ColiHipMoe *moe, int *nu, int *uniq);
  * must follow the prep of the same kind of tensor and the same S. */
 int coli_hip_gemm_prep_dev(ColiCudaTensor *tensor, const float *x_dev, int S);
 int coli_hip_gemm_run_dev(ColiCudaTensor *tensor, float *y_dev, int S);
+/* Fill n bytes of device memory with uniform pseudo-random bytes (seeded,
+ * deterministic): synthetic weights for benchmarks without a host round trip. */
+int coli_hip_fill_random_u8(int device, void *dev, size_t n, unsigned long long seed);
 /* The hipStream_t every asynchronous entry point of `device` runs on. */
 void *coli_hip_stream(int device);
 /* Bytes the tensor streams per full GEMV (weights + scales, tiled storage). */
