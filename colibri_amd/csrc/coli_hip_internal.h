@@ -69,12 +69,12 @@ struct ColiGemvArgs {
     const _Float16 *xhi, *xlo;
     int xstride;              // halves per fragment row (= ngp * 32)
     const int *xexp;          // per fragment row
-    const int *haslo;
+    const int *haslo;         // == lo_gen when some lo part of this fragment set is non-zero
+    int lo_gen;
     const _Float16 *zero;     // >= COLI_ZERO_BYTES of zeros: inactive batch lanes, dead tiles
     float *out;
     int ldo;
-    float *partial;
-    unsigned *counters;
+    float *partial;           // split-K partials: [instance][split][R][NB4][64]
 };
 
 

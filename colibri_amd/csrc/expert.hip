@@ -21,34 +21,49 @@
 // ---------------------------------------------------------------------------
 // planning and launch helpers
 // ---------------------------------------------------------------------------
-// Work decomposition of one GEMV launch. K is split across the W waves of a
-// group (LDS reduction, no device-scope sync); rows are split across groups.
-//  * R (row tiles per wave) trades activation-fragment re-reads for group
-//    count: with many batch rows the fragments are as large as the weights,
-//    so R = 4 shares each fragment load over four tiles; at B <= 4 R = 2.
-//  * W grows until the launch has about 12 waves per CU, as long as every
-//    wave still gets >= 2 quads.
-//  * Cross-group splits only when even W = 16 leaves the chip mostly idle.
+// Work decomposition of one GEMV launch.
+//  * R = 4 row tiles per wave: four 1 KiB weight loads per stage keep ~8 KiB
+//    in flight per wave with the two-stage pipeline, and one activation
+//    fragment load feeds four tiles. Narrow matrices fall back to 2 or 1.
+//  * K is split across the W waves of a group (LDS reduction) and, when the
+//    rows alone cannot fill the chip with ~12 waves per CU, across groups
+//    (partials reduced in split order by a second kernel).
+//  * Every wave keeps at least 2 quads.
 GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual, int max_rows) {
+    (void)max_rows;
     GemvLaunchPlan p;
     const long cus = ctx && ctx->cu_count ? ctx->cu_count : 256;
     const long target_waves = 12 * cus;
-    p.R = max_rows > 4 ? 4 : 2;
-    int RT = dual ? p.R / 2 : p.R;
-    if (!dual && nrt < p.R) {
+    p.R = 4;
+    int RT = dual ? 2 : 4;
+    if (!dual && nrt < 4) {
         p.R = nrt >= 2 ? 2 : 1;
         RT = p.R;
     }
     p.rbpp = (nrt + RT - 1) / RT;
     long groups = (long)nprob * n_bt * p.rbpp;
     p.W = 4;
-    const int wmax = p.R == 4 ? 8 : 16;   // 1024-thread groups only within the 128-VGPR budget
-    while (p.W < wmax && groups * p.W < target_waves && nq >= 2 * (2 * p.W)) p.W *= 2;
+    if (groups * 4 < target_waves && nq >= 16) p.W = 8;
+    // K splits cost a partial round trip and a second launch: only worth it
+    // when the row tiles alone leave the chip under 4 waves per CU (long-K,
+    // narrow-O shapes such as a dense down projection).
     p.splits = 1;
-    if (groups * p.W < target_waves / 4 && nq >= 4 * p.W) {
-        long want = (target_waves / 4 + groups * p.W - 1) / (groups * p.W);
-        p.splits = (int)std::min<long>(want, nq / (2 * p.W));
-        if (p.splits < 1) p.splits = 1;
+    if (groups * p.W < 4 * cus) {
+        long want = (8 * cus + groups * p.W - 1) / (groups * p.W);
+        long cap = std::max(1, nq / (2 * p.W));
+        p.splits = (int)std::min(want, cap);
+    }
+    // COLI_HIP_PLAN="R,W,splits" overrides the decomposition (tuning only).
+    if (const char *ov = std::getenv("COLI_HIP_PLAN")) {
+        int r = 0, w = 0, sp = 0;
+        if (std::sscanf(ov, "%d,%d,%d", &r, &w, &sp) == 3 && (r == 1 || r == 2 || r == 4) &&
+            (w == 4 || w == 8 || w == 16) && sp >= 1 && !(dual && r == 1) && !(r == 4 && w == 16)) {
+            p.R = r;
+            RT = dual ? r / 2 : r;
+            p.rbpp = (nrt + RT - 1) / RT;
+            p.W = w;
+            p.splits = sp;
+        }
     }
     p.qps = (nq + p.splits - 1) / p.splits;
     p.splits = (nq + p.qps - 1) / p.qps;
@@ -76,9 +91,10 @@ static int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, i
         !reserve(ctx, &f.exp, (size_t)nrows * sizeof(int), 0))
         return 0;
     int *flag = (int *)ctx->flags.p + set;
-    if (!hip_ok(coli_launch_zero_i32(flag, 1, ctx->stream), "fragment flag")) return 0;
+    f.gen = f.gen == 0x7fffffff ? 1 : f.gen + 1;
+    if (f.gen == 1 && !hip_ok(coli_launch_zero_i32(flag, 1, ctx->stream), "fragment flag")) return 0;
     return hip_ok(coli_launch_prep_frag(x, ld, src_rows, nrows_dev, nrows, K, ngp, int4_order,
-                                        (_Float16 *)f.hi.p, (_Float16 *)f.lo.p, (int *)f.exp.p, flag,
+                                        (_Float16 *)f.hi.p, (_Float16 *)f.lo.p, (int *)f.exp.p, flag, f.gen,
                                         ctx->stream),
                   "fragment prep");
 }
@@ -91,11 +107,8 @@ static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
     int n_bt = (max_rows + 15) / 16;
     GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
     size_t inst = (size_t)nprob * n_bt * pl.rbpp;
-    if (pl.splits > 1) {
-        if (!reserve(ctx, &ctx->partial, inst * pl.splits * pl.R * 4 * 64 * sizeof(float), 0) ||
-            !reserve(ctx, &ctx->counters, inst * sizeof(unsigned), 1))
-            return 0;
-    }
+    if (pl.splits > 1 && !reserve(ctx, &ctx->partial, inst * pl.splits * pl.R * 4 * 64 * sizeof(float), 0))
+        return 0;
     FragSet &f = ctx->frag[set];
     ColiGemvArgs a;
     a.prob = probs_dev;
@@ -114,11 +127,11 @@ static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
     a.xstride = nq * 4 * 32;
     a.xexp = (const int *)f.exp.p;
     a.haslo = (const int *)ctx->flags.p + set;
+    a.lo_gen = f.gen;
     a.zero = (const _Float16 *)ctx->zeros.p;
     a.out = out;
     a.ldo = ldo;
     a.partial = (float *)ctx->partial.p;
-    a.counters = (unsigned *)ctx->counters.p;
     return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
 }
 

@@ -20,10 +20,13 @@
 //  * Activations arrive as fp16 hi + lo fragments of x * 2^-E (E = per-row
 //    exponent, exact), i.e. ~22 significant bits; the lo MFMA is skipped when
 //    every lo part is zero (bf16-exact inputs).
-//  * Split-K across waves with a deterministic fixed-order reduction by the
-//    last-arriving wave (self-resetting counters, no memset, no atomics on the
-//    data), then fused epilogues: plain store, or SwiGLU (silu(g)*u, the
-//    expression of c/backend_cuda.cu:618-624) for gate/up pairs.
+//  * K is split across the waves of a workgroup (LDS reduction in fixed wave
+//    order) and, for shapes whose rows cannot fill the chip, across
+//    workgroups (partials summed in split order by a second kernel; no
+//    device-scope fences, no atomics on the data), then fused epilogues:
+//    plain store, or SwiGLU (silu(g)*u, the expression of
+//    c/backend_cuda.cu:618-624) for gate/up pairs. Results are bitwise
+//    reproducible run to run.
 #include "coli_hip_internal.h"
 
 #include <math.h>
@@ -115,27 +118,41 @@ __global__ void coli_repack_scales_e8(const uint8_t *__restrict__ src, int O, in
 // ---------------------------------------------------------------------------
 // Activation fragments
 // ---------------------------------------------------------------------------
-// For fragment row r (source row src_row[r] of x, f32 [.., ldx]):
+// For fragment row r (source row src_row[r] of x, f32 [.., ldx]; src_row[r]
+// < 0 marks an unused slot):
 //   E = exponent with max|x| * 2^-E in [0.5, 1) (0 for an all-zero row),
 //   hi = fp16(x * 2^-E * m), lo = fp16(x * 2^-E * m - hi), m = 1/16 on the
 //   high-nibble columns of the int4 order, else 1.
 // Layout per row: [ngp groups][4 kslices][8 halves]; slot t of kslice s of
 // group g holds column 32g + 8s + perm[t], perm = {0,2,4,6,1,3,5,7} (int4)
 // or identity (fp4), matching the B-operand order built in the GEMV.
-// One 256-thread block per fragment row.
-__global__ void coli_prep_frag(const float *__restrict__ x, int ldx, const int *__restrict__ src_row,
-                               const int *__restrict__ nrows_dev, int nrows_host, int K, int ngp,
-                               int int4_order, _Float16 *__restrict__ hi, _Float16 *__restrict__ lo,
-                               int *__restrict__ exp2out, int *__restrict__ haslo) {
-    int r = blockIdx.x;
-    int nrows = nrows_dev ? *nrows_dev : nrows_host;
-    if (r >= nrows) return;
-    int srow = src_row ? src_row[r] : r;
-    if (srow < 0) return;   // unused slot of a padded row set
+// Grid (chunks of 2048 fragment elements, rows); every block of a row derives
+// the row maximum itself (the row is L2-resident), so one launch does it all.
+// Whether any lo part is non-zero is published as `gen` into *haslo with an
+// atomic max: the GEMV of the same generation compares against `gen`, so the
+// flag never needs clearing; the GEMV treats any flag >= its generation as
+// "lo present", which stays correct when a captured graph replays an old gen.
+__global__ __launch_bounds__(256) void coli_prep_frag(const float *__restrict__ x, int ldx,
+                                                      const int *__restrict__ src_row,
+                                                      const int *__restrict__ nrows_dev, int K, int ngp,
+                                                      int int4_order, _Float16 *__restrict__ hi,
+                                                      _Float16 *__restrict__ lo, int *__restrict__ exp2out,
+                                                      int *__restrict__ haslo, int gen) {
+    const int r = blockIdx.y;
+    if (nrows_dev && r >= *nrows_dev) return;
+    const int srow = src_row ? src_row[r] : r;
+    if (srow < 0) return;
     const float *xr = x + (size_t)srow * ldx;
     __shared__ float red[256];
     float m = 0.0f;
-    for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+    if ((K & 3) == 0 && ((ldx & 3) == 0)) {
+        for (int k = threadIdx.x * 4; k < K; k += 1024) {
+            float4 v = *(const float4 *)(xr + k);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+    }
     red[threadIdx.x] = m;
     __syncthreads();
     for (int s = 128; s; s >>= 1) {
@@ -145,22 +162,29 @@ __global__ void coli_prep_frag(const float *__restrict__ x, int ldx, const int *
     m = red[0];
     int E = 0;
     if (m > 0.0f && isfinite(m)) frexpf(m, &E);
-    if (threadIdx.x == 0) exp2out[r] = E;
-    size_t base = (size_t)r * ngp * 32;
-    int any_lo = 0;
-    for (int e = threadIdx.x; e < ngp * 32; e += 256) {
-        int g = e >> 5, s = (e >> 3) & 3, t = e & 7;
+    if (blockIdx.x == 0 && threadIdx.x == 0) exp2out[r] = E;
+    // one thread = one 8-half slot (kslice s of group g): source columns 32g+8s .. +7
+    const int slot = blockIdx.x * 256 + threadIdx.x;
+    if (slot >= ngp * 4) return;
+    const int k0 = slot * 8;
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) v[t] = k0 + t < K ? xr[k0 + t] : 0.0f;
+    _Float16 h[8], l[8];
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
         int off = int4_order ? ((t < 4) ? 2 * t : 2 * (t - 4) + 1) : t;
-        int k = g * 32 + 8 * s + off;
-        float v = k < K ? ldexpf(xr[k], -E) : 0.0f;
-        if (int4_order && (off & 1)) v *= 0.0625f;
-        _Float16 h = (_Float16)v;
-        _Float16 l = (_Float16)(v - (float)h);
-        hi[base + e] = h;
-        lo[base + e] = l;
-        any_lo |= (l != (_Float16)0.0f);
+        float y = ldexpf(v[off], -E);
+        if (int4_order && (off & 1)) y *= 0.0625f;
+        h[t] = (_Float16)y;
+        l[t] = (_Float16)(y - (float)h[t]);
+        any |= (l[t] != (_Float16)0.0f);
     }
-    if (any_lo) atomicOr(haslo, 1);
+    size_t base = (size_t)r * ngp * 32 + (size_t)k0;
+    *(half8v *)(hi + base) = (half8v){h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+    *(half8v *)(lo + base) = (half8v){l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
+    if (any) atomicMax(haslo, gen);
 }
 
 // ---------------------------------------------------------------------------
@@ -239,61 +263,93 @@ struct Stage {
     half8v xl[LO ? 4 : 1];
 };
 
-// Main loop of one wave over quads q = q_first, q_first+4, ... < Q1.
-// Loads of quad q+4 are issued before the math of quad q, as one branch-free
-// batch (dead tiles read a valid tile and get a zero scale), so the wave
-// keeps a full stage in flight while it computes and the waits before the
-// math only cover the current stage.
+#ifndef COLI_PD
+#define COLI_PD 2
+#endif
+
+// Main loop of one wave over its quads q = q_first + it*W, it < nit.
+// A ring of PD stages: the loads of iteration it+PD-1 are issued (as one
+// branch-free batch) before the math of iteration it, so up to PD-1 stages
+// stay in flight while the wave computes. Iterations past the end read the
+// zero buffer instead (their math is skipped), which keeps every load
+// unconditional and the in-order vmcnt accounting exact.
 template <int KIND, int R, int NB4, int W, bool LO>
 __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], int q_first, int Q1, const size_t (&tbase)[R],
                                            const int (&tstep)[R], const uint8_t *const (&wb)[R],
                                            const void *const (&sb)[R], const _Float16 *xh, const _Float16 *xl,
-                                           int lane) {
-    Stage<KIND, R, LO> cur, nxt;
-    auto load = [&](Stage<KIND, R, LO> &st, int q) {
+                                           const _Float16 *zero, int lane) {
+    constexpr int PD = COLI_PD;
+    if (q_first >= Q1) return;
+    const int nit = (Q1 - q_first + W - 1) / W;
+    Stage<KIND, R, LO> st[PD];
+    auto load = [&](Stage<KIND, R, LO> &sg, int it) {
+        const bool valid = it < nit;
+        const int q = q_first + it * W;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            size_t tq = tbase[r] + (size_t)q * tstep[r];
-            st.w[r] = __builtin_nontemporal_load(GPTR(u32x4, wb[r] + tq * COLI_TILE_BYTES) + lane);
-            st.sc[r].load(sb[r], tq, lane & 15);
+            size_t tq = valid ? tbase[r] + (size_t)q * tstep[r] : 0;
+            const uint8_t *w = valid ? wb[r] : (const uint8_t *)zero;
+            const void *sp = valid ? sb[r] : (const void *)zero;
+            sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + tq * COLI_TILE_BYTES) + lane);
+            sg.sc[r].load(sp, tq, lane & 15);
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            st.xh[j] = *GPTR(half8v, xh + (size_t)(4 * q + j) * 32);
-            if constexpr (LO) st.xl[j] = *GPTR(half8v, xl + (size_t)(4 * q + j) * 32);
+            const _Float16 *ph = valid ? xh + (size_t)(4 * q + j) * 32 : zero;
+            sg.xh[j] = *GPTR(half8v, ph);
+            if constexpr (LO) {
+                const _Float16 *pl = valid ? xl + (size_t)(4 * q + j) * 32 : zero;
+                sg.xl[j] = *GPTR(half8v, pl);
+            }
         }
     };
-    auto compute = [&](const Stage<KIND, R, LO> &st) {
+    auto compute = [&](const Stage<KIND, R, LO> &sg) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                half8v bw = unpack_b<KIND>(st.w[r][j]);
-                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.xl[j], bw, d, 0, 0, 0);
-                float scl = st.sc[r].get(j);
+                half8v bw = unpack_b<KIND>(sg.w[r][j]);
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg.xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg.xl[j], bw, d, 0, 0, 0);
+                float scl = sg.sc[r].get(j);
 #pragma unroll
                 for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
             }
         }
     };
-    // Ping-pong between two stages (no register copies, which would wait on
-    // the prefetch): stage A holds quad q, stage B quad q+W.
-    if (q_first >= Q1) return;
-    load(cur, q_first);
-    int q = q_first;
-    for (; q + 2 * W < Q1; q += 2 * W) {
-        load(nxt, q + W);
-        compute(cur);
-        load(cur, q + 2 * W);
-        compute(nxt);
+#pragma unroll
+    for (int p = 0; p < PD - 1; p++) load(st[p], p);
+    for (int it0 = 0; it0 < nit; it0 += PD) {
+#pragma unroll
+        for (int u = 0; u < PD; u++) {
+            load(st[(u + PD - 1) % PD], it0 + u + PD - 1);
+            if (it0 + u < nit) compute(st[u]);
+        }
     }
-    if (q + W < Q1) {
-        load(nxt, q + W);
-        compute(cur);
-        compute(nxt);
-    } else {
-        compute(cur);
+}
+
+// Output of one lane for batch row `brow` of the problem: output row
+// rt*16 + (lane & 15) of every live tile, scaled back by the row's 2^E; for
+// DUAL, silu(gate) * up of the paired tiles.
+template <int R, bool DUAL>
+__device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiProb &pr, int bt, const int (&rt)[R],
+                                              const bool (&live)[R], const float (&v)[R], int brow, int lane) {
+    constexpr int RT = DUAL ? R / 2 : R;
+    const int nb = min(16, pr.nrows - 16 * bt);
+    if (brow >= nb) return;
+    const int E = a.xexp[a.xrows[pr.xrow_off + 16 * bt + brow]];
+    float *orow = a.out + (size_t)(pr.out_row0 + 16 * bt + brow) * a.ldo;
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        if (!live[r]) continue;
+        const int o = rt[r] * 16 + (lane & 15);
+        if (o >= a.O) continue;
+        if constexpr (DUAL) {
+            float gv = ldexpf(v[r], E), uv = ldexpf(v[r + RT], E);
+            orow[o] = silu_mul(gv, uv);
+        } else {
+            orow[o] = ldexpf(v[r], E);
+        }
     }
 }
 
@@ -313,7 +369,6 @@ template <int KIND, int R, bool DUAL, int NB4, int W>
 __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     constexpr int RT = DUAL ? R / 2 : R;
     __shared__ float red[W][R * NB4][64];
-    __shared__ unsigned last_flag;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int item = blockIdx.x;
     const int items_per_bt = a.rb_per_prob * a.splits;
@@ -332,7 +387,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
 
     const int b = lane & 15, ks = lane >> 4;
     const int Q0 = s * a.qps, Q1 = min(a.nq, Q0 + a.qps);
-    const bool use_lo = *a.haslo != 0;
+    const bool use_lo = *a.haslo >= a.lo_gen;  // >=: stays correct under graph replay
 
     // Lanes past the problem's rows read the zero fragment row.
     const _Float16 *xh = a.zero, *xl = a.zero;
@@ -364,8 +419,8 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
-    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, lane);
-    else gemv_quads<KIND, R, NB4, W, false>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, lane);
+    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
+    else gemv_quads<KIND, R, NB4, W, false>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
 
     // ---- intra-group reduction in fixed wave order; wave i finishes register i ----
 #pragma unroll
@@ -385,51 +440,54 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
         }
     }
 
-    // ---- cross-group split-K (small shapes only): fixed-order sum by the last group ----
+    // ---- split K across groups: publish the partial; coli_gemv_reduce finishes ----
     if (a.splits > 1) {
-        const size_t inst = ((size_t)p * a.n_bt + bt) * a.rb_per_prob + rb;
         if (i < NB4) {
-            float *mine = a.partial + ((inst * a.splits + s) * R * 4) * 64;
+            const size_t inst = ((size_t)p * a.n_bt + bt) * a.rb_per_prob + rb;
+            float *mine = a.partial + ((inst * a.splits + s) * R * NB4 + i) * 64 + lane;
 #pragma unroll
-            for (int r = 0; r < R; r++) mine[(r * 4 + i) * 64 + lane] = v[r];
+            for (int r = 0; r < R; r++) mine[r * NB4 * 64] = v[r];
         }
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0) last_flag = atomicAdd(&a.counters[inst], 1u) == (unsigned)(a.splits - 1);
-        __syncthreads();
-        if (!last_flag) return;
-        __threadfence();
-        if (threadIdx.x == 0) a.counters[inst] = 0u;   // self-reset for the next launch
-        if (i < NB4) {
-            const float *base = a.partial + (inst * a.splits * R * 4) * 64;
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float t = 0.0f;
-                for (int ss = 0; ss < a.splits; ss++)
-                    t += __builtin_nontemporal_load(base + ((size_t)ss * R * 4 + r * 4 + i) * 64 + lane);
-                v[r] = t;
-            }
-        }
+        return;
     }
-
-    // ---- epilogue ----
     if (i >= NB4) return;
-    const int brow = 4 * ks + i;
-    if (brow >= nb) return;
-    const int E = a.xexp[a.xrows[pr.xrow_off + 16 * bt + brow]];
-    float *orow = a.out + (size_t)(pr.out_row0 + 16 * bt + brow) * a.ldo;
+    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, ks * 4 + i, lane);
+}
+
+// Second pass of a split-K launch: sums the groups' partials in split order
+// (deterministic) and applies the epilogue. One thread per (instance, row
+// register i, lane); the instance's tiles are handled in one thread.
+template <int R, bool DUAL, int NB4>
+__global__ __launch_bounds__(256) void coli_gemv_reduce(ColiGemvArgs a) {
+    constexpr int RT = DUAL ? R / 2 : R;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int lane = (int)(t & 63), i = (int)((t >> 6) % NB4);
+    const size_t inst = (t >> 6) / NB4;
+    const size_t ninst = (size_t)a.nprob * a.n_bt * a.rb_per_prob;
+    if (inst >= ninst) return;
+    const int p = (int)(inst / ((size_t)a.n_bt * a.rb_per_prob));
+    if (a.nprob_dev && p >= *a.nprob_dev) return;
+    const int rem = (int)(inst - (size_t)p * a.n_bt * a.rb_per_prob);
+    const int bt = rem / a.rb_per_prob, rb = rem - bt * a.rb_per_prob;
+    const ColiProb pr = a.prob[p];
+    const int nb = min(16, pr.nrows - 16 * bt);
+    const int brow = 4 * (lane >> 4) + i;
+    if (nb <= 0 || brow >= nb) return;
+    float v[R];
 #pragma unroll
-    for (int r = 0; r < RT; r++) {
-        if (!live[r]) continue;
-        const int o = rt[r] * 16 + (lane & 15);
-        if (o >= a.O) continue;
-        if constexpr (DUAL) {
-            float gv = ldexpf(v[r], E), uv = ldexpf(v[r + RT], E);
-            orow[o] = silu_mul(gv, uv);
-        } else {
-            orow[o] = ldexpf(v[r], E);
-        }
+    for (int r = 0; r < R; r++) v[r] = 0.0f;
+    const float *base = a.partial + ((inst * a.splits) * R * NB4 + i) * 64 + lane;
+    for (int ss = 0; ss < a.splits; ss++)
+#pragma unroll
+        for (int r = 0; r < R; r++) v[r] += base[((size_t)ss * R + r) * NB4 * 64];
+    int rt[R];
+    bool live[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        rt[r] = rb * RT + (DUAL ? r % RT : r);
+        live[r] = rt[r] < a.nrt;
     }
+    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, brow, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -543,11 +601,25 @@ static hipError_t launch_w(const ColiGemvArgs &a, int W, int blocks, hipStream_t
     return hipGetLastError();
 }
 
+template <int R, bool DUAL, int NB4>
+static hipError_t launch_reduce(const ColiGemvArgs &a, hipStream_t st) {
+    size_t threads = (size_t)a.nprob * a.n_bt * a.rb_per_prob * NB4 * 64;
+    hipLaunchKernelGGL((coli_gemv_reduce<R, DUAL, NB4>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+template <int KIND, int R, bool DUAL, int NB4>
+static hipError_t launch_split(const ColiGemvArgs &a, int W, int blocks, hipStream_t st) {
+    hipError_t e = launch_w<KIND, R, DUAL, NB4>(a, W, blocks, st);
+    if (e != hipSuccess || a.splits <= 1) return e;
+    return launch_reduce<R, DUAL, NB4>(a, st);
+}
+
 template <int KIND, int R, bool DUAL>
 static hipError_t launch_nb(const ColiGemvArgs &a, int nb4, int W, int blocks, hipStream_t st) {
-    if (nb4 == 1) return launch_w<KIND, R, DUAL, 1>(a, W, blocks, st);
-    if (nb4 == 2) return launch_w<KIND, R, DUAL, 2>(a, W, blocks, st);
-    return launch_w<KIND, R, DUAL, 4>(a, W, blocks, st);
+    if (nb4 == 1) return launch_split<KIND, R, DUAL, 1>(a, W, blocks, st);
+    if (nb4 == 2) return launch_split<KIND, R, DUAL, 2>(a, W, blocks, st);
+    return launch_split<KIND, R, DUAL, 4>(a, W, blocks, st);
 }
 
 template <int KIND>
@@ -578,10 +650,11 @@ extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, i
 extern "C" hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row,
                                             const int *nrows_dev, int nrows, int K, int ngp,
                                             int int4_order, _Float16 *hi, _Float16 *lo,
-                                            int *exp2out, int *haslo, hipStream_t st) {
+                                            int *exp2out, int *haslo, int gen, hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(coli_prep_frag, dim3(nrows), dim3(256), 0, st, x, ldx, src_row, nrows_dev,
-                       nrows, K, ngp, int4_order, hi, lo, exp2out, haslo);
+    dim3 grid((ngp * 4 + 255) / 256, nrows);
+    hipLaunchKernelGGL(coli_prep_frag, grid, dim3(256), 0, st, x, ldx, src_row, nrows_dev, K, ngp, int4_order,
+                       hi, lo, exp2out, haslo, gen);
     return hipGetLastError();
 }
 

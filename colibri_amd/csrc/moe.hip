@@ -43,53 +43,70 @@ struct ColiHipMoe {
 };
 
 // ---------------------------------------------------------------------------
-// union + descriptor build: one thread (S*K <= 64*64 selections, E <= 4096).
+// union + descriptor build, one 256-thread block. Thread 0 walks the S*K
+// selections in (s, kk) order and assigns first-seen slots (LDS only, plus
+// fire-and-forget stores of the row lists); the descriptors are then built by
+// all threads in parallel.
 // ---------------------------------------------------------------------------
-__global__ void coli_moe_union(const int *__restrict__ idx, const int *__restrict__ keff, int S, int K, int E,
-                               int has_shared, int RS, const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
-                               ColiProb *__restrict__ pdown, int *__restrict__ uniq, int *__restrict__ xrows,
-                               int *__restrict__ hrows, int *__restrict__ slotrow, int *__restrict__ state) {
-    if (threadIdx.x || blockIdx.x) return;
-    extern __shared__ int map[];   // [E] expert -> union slot, then [S*K+1] row counts
-    int *cnt = map + E;
-    for (int e = 0; e < E; e++) map[e] = -1;
-    int nu = 0;
-    for (int t = 0; t < S; t++)
-        for (int kk = 0; kk < keff[t]; kk++) {
-            int e = idx[t * K + kk];
-            if (e < 0 || e >= E) continue;
-            if (map[e] < 0) {
-                map[e] = nu;
-                uniq[nu] = e;
-                cnt[nu] = 0;
-                nu++;
+__global__ __launch_bounds__(256) void coli_moe_union(const int *__restrict__ idx, const int *__restrict__ keff,
+                                                      int S, int K, int E, int has_shared, int RS,
+                                                      const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
+                                                      ColiProb *__restrict__ pdown, int *__restrict__ uniq,
+                                                      int *__restrict__ xrows, int *__restrict__ hrows,
+                                                      int *__restrict__ slotrow, int *__restrict__ state) {
+    extern __shared__ int sm[];   // map [E] | cnt [S*K+1] | uq [S*K+1] | sel [S*K] | ke [S]
+    int *map = sm, *cnt = map + E, *uq = cnt + S * K + 1, *sel = uq + S * K + 1, *ke = sel + S * K;
+    __shared__ int s_np, s_nu;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) map[e] = -1;
+    for (int i = threadIdx.x; i < S * K; i += blockDim.x) sel[i] = idx[i];
+    for (int t = threadIdx.x; t < S; t += blockDim.x) ke[t] = keff[t];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int nu = 0;
+        for (int t = 0; t < S; t++)
+            for (int kk = 0; kk < ke[t]; kk++) {
+                int e = sel[t * K + kk];
+                if (e < 0 || e >= E) continue;
+                if (map[e] < 0) {
+                    map[e] = nu;
+                    uq[nu] = e;
+                    cnt[nu] = 0;
+                    nu++;
+                }
+                int j = map[e], pos = cnt[j]++;
+                xrows[j * RS + pos] = t;
+                slotrow[t * K + kk] = j * RS + pos;
             }
-            int j = map[e], pos = cnt[j]++;
-            xrows[j * RS + pos] = t;
-            slotrow[t * K + kk] = j * RS + pos;
+        int np = nu;
+        if (has_shared) {
+            uq[np] = E;            // the shared expert sits at table row E
+            cnt[np] = S;
+            np++;
         }
-    int np = nu;
-    if (has_shared) {
-        for (int t = 0; t < S; t++) xrows[np * RS + t] = t;
-        cnt[np] = S;
-        np++;
+        s_np = np;
+        s_nu = nu;
+        state[0] = np;
+        state[1] = np * RS;
+        state[2] = nu;
     }
-    for (int j = 0; j < np; j++) {
-        int e = j < nu ? uniq[j] : E;   // shared expert sits at table row E
+    __syncthreads();
+    const int np = s_np, nu = s_nu;
+    for (int j = threadIdx.x; j < np; j += blockDim.x) {
+        int e = uq[j];
+        if (j < nu) uniq[j] = e;
         ColiProb d = tab[2 * e], dn = tab[2 * e + 1];
-        d.nrows = cnt[j];
-        d.xrow_off = j * RS;
-        d.out_row0 = j * RS;
-        dn.nrows = cnt[j];
-        dn.xrow_off = j * RS;
-        dn.out_row0 = j * RS;
+        d.nrows = dn.nrows = cnt[j];
+        d.xrow_off = dn.xrow_off = j * RS;
+        d.out_row0 = dn.out_row0 = j * RS;
         pdual[j] = d;
         pdown[j] = dn;
-        for (int p = 0; p < RS; p++) hrows[j * RS + p] = p < cnt[j] ? j * RS + p : -1;
     }
-    state[0] = np;
-    state[1] = np * RS;
-    state[2] = nu;
+    if (has_shared)
+        for (int t = threadIdx.x; t < S; t += blockDim.x) xrows[nu * RS + t] = t;
+    for (int r = threadIdx.x; r < np * RS; r += blockDim.x) {
+        int j = r / RS, p = r - j * RS;
+        hrows[r] = p < cnt[j] ? r : -1;
+    }
 }
 
 // out[t, d] = sum_{kk < keff[t]} w[t, kk] * y[slotrow[t, kk], d]  (+ y[shared row])
@@ -206,18 +223,15 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     hipStream_t st = ctx->stream;
     const int nq_d = (c.D + 127) / 128, nq_i = (c.I + 127) / 128;
     // make sure every scratch the kernels touch exists before the first launch
-    size_t inst_max = 0;
     {
         GemvLaunchPlan a = plan_gemv(ctx, P, (S + 15) / 16, (c.I + 15) / 16, nq_d, true, S);
         GemvLaunchPlan b = plan_gemv(ctx, P, (S + 15) / 16, (c.D + 15) / 16, nq_i, false, S);
         size_t ia = (size_t)P * ((S + 15) / 16) * a.rbpp, ib = (size_t)P * ((S + 15) / 16) * b.rbpp;
-        inst_max = std::max(ia, ib);
         size_t pa = a.splits > 1 ? ia * a.splits * a.R * 4 * 64 * 4 : 0;
         size_t pb = b.splits > 1 ? ib * b.splits * b.R * 4 * 64 * 4 : 0;
         size_t ngp_d = (size_t)nq_d * 4, ngp_i = (size_t)nq_i * 4;
         FragSet &fx = ctx->frag[ord], &fh = ctx->frag[2 + ord];
         if (!reserve(ctx, &ctx->partial, std::max<size_t>(std::max(pa, pb), 256), 0) ||
-            !reserve(ctx, &ctx->counters, inst_max * sizeof(unsigned), 1) ||
             !reserve(ctx, &fx.hi, (size_t)S * ngp_d * 64, 0) || !reserve(ctx, &fx.lo, (size_t)S * ngp_d * 64, 0) ||
             !reserve(ctx, &fx.exp, (size_t)S * 4, 0) || !reserve(ctx, &fh.hi, (size_t)P * RS * ngp_i * 64, 0) ||
             !reserve(ctx, &fh.lo, (size_t)P * RS * ngp_i * 64, 0) || !reserve(ctx, &fh.exp, (size_t)P * RS * 4, 0))
@@ -226,9 +240,10 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     int *flags = (int *)ctx->flags.p;
     FragSet &fx = ctx->frag[ord], &fh = ctx->frag[2 + ord];
     // 1. activation fragments, 2-3. router
-    if (!hip_ok(coli_launch_zero_i32(flags + ord, 1, st), "moe flag") ||
-        !hip_ok(coli_launch_prep_frag(x_dev, c.D, nullptr, nullptr, S, c.D, nq_d * 4, !ord, (_Float16 *)fx.hi.p,
-                                      (_Float16 *)fx.lo.p, (int *)fx.exp.p, flags + ord, st),
+    fx.gen = fx.gen == 0x7fffffff ? 1 : fx.gen + 1;
+    if (fx.gen == 1 && !hip_ok(coli_launch_zero_i32(flags + ord, 1, st), "moe flag")) return 0;
+    if (!hip_ok(coli_launch_prep_frag(x_dev, c.D, nullptr, nullptr, S, c.D, nq_d * 4, !ord, (_Float16 *)fx.hi.p,
+                                      (_Float16 *)fx.lo.p, (int *)fx.exp.p, flags + ord, fx.gen, st),
                 "moe x fragments") ||
         !hip_ok(coli_launch_router_logits(x_dev, S, m->rw, c.D, c.E, m->logits, st), "moe router logits") ||
         !hip_ok(coli_launch_router_select(m->logits, m->rb, S, c.E, c.K, c.route_mode, c.topp, c.norm_topk,
@@ -236,7 +251,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
                 "moe router select"))
         return 0;
     // 4. union
-    hipLaunchKernelGGL(coli_moe_union, dim3(1), dim3(64), (size_t)(c.E + S * c.K + 1) * sizeof(int), st, m->idx, m->keff, S, c.K,
+    hipLaunchKernelGGL(coli_moe_union, dim3(1), dim3(256), (size_t)(c.E + 3 * S * c.K + 2 + S) * sizeof(int), st, m->idx, m->keff, S, c.K,
                        c.E, c.has_shared, RS, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->hrows, m->slotrow,
                        m->state);
     if (!hip_ok(hipGetLastError(), "moe union")) return 0;
@@ -259,16 +274,18 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     a.xstride = nq_d * 128;
     a.xexp = (const int *)fx.exp.p;
     a.haslo = flags + ord;
+    a.lo_gen = fx.gen;
     a.zero = (const _Float16 *)ctx->zeros.p;
     a.out = m->h;
     a.ldo = c.I;
     a.partial = (float *)ctx->partial.p;
-    a.counters = (unsigned *)ctx->counters.p;
     if (!hip_ok(coli_launch_gemv(m->kind, &a, pl.R, 1, pl.W, S, st), "moe dual")) return 0;
     // 6. hidden fragments (valid slots only)
-    if (!hip_ok(coli_launch_zero_i32(flags + 2 + ord, 1, st), "moe flag") ||
-        !hip_ok(coli_launch_prep_frag(m->h, c.I, m->hrows, m->state + 1, P * RS, c.I, nq_i * 4, !ord,
-                                      (_Float16 *)fh.hi.p, (_Float16 *)fh.lo.p, (int *)fh.exp.p, flags + 2 + ord, st),
+    fh.gen = fh.gen == 0x7fffffff ? 1 : fh.gen + 1;
+    if (fh.gen == 1 && !hip_ok(coli_launch_zero_i32(flags + 2 + ord, 1, st), "moe flag")) return 0;
+    if (!hip_ok(coli_launch_prep_frag(m->h, c.I, m->hrows, m->state + 1, P * RS, c.I, nq_i * 4, !ord,
+                                      (_Float16 *)fh.hi.p, (_Float16 *)fh.lo.p, (int *)fh.exp.p, flags + 2 + ord,
+                                      fh.gen, st),
                 "moe hidden fragments"))
         return 0;
     // 7. down
@@ -286,6 +303,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     a.xstride = nq_i * 128;
     a.xexp = (const int *)fh.exp.p;
     a.haslo = flags + 2 + ord;
+    a.lo_gen = fh.gen;
     a.out = m->y;
     a.ldo = c.D;
     if (!hip_ok(coli_launch_gemv(m->kind, &a, pl.R, 0, pl.W, S, st), "moe down")) return 0;

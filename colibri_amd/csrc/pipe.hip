@@ -62,52 +62,69 @@ __global__ void coli_sum_slots(float *dst, const float *slots, int n, int D) {
 
 // ---------------------------------------------------------------------------
 // Router logits: logits[s, e] = sum_d x[s, d] * W[e, d], f32 (the router GEMV
-// of c/colibri.c:3978 / c/olmoe.c:648). One block per expert row; each thread
-// walks D with float4 loads and keeps S <= 16 accumulators; a fixed-order tree
-// reduction finishes each row.
+// of c/colibri.c:3978 / c/olmoe.c:648). EB experts per 256-thread block: each
+// thread walks D with float4 loads, keeps EB x SMAX accumulators and reuses
+// each activation load for the EB experts; fixed-order reductions (wave
+// butterfly, then the 4 waves in order) finish each dot product.
 // ---------------------------------------------------------------------------
-template <int SMAX>
+template <int SMAX, int EB>
 __global__ __launch_bounds__(256) void coli_router_logits(const float *__restrict__ x, int S,
                                                           const float *__restrict__ W, int D, int E,
                                                           float *__restrict__ logits) {
-    int e = blockIdx.x;
-    const float *w = W + (size_t)e * D;
-    float acc[SMAX];
+    const int e0 = blockIdx.x * EB;
+    float acc[EB][SMAX];
 #pragma unroll
-    for (int s = 0; s < SMAX; s++) acc[s] = 0.0f;
+    for (int k = 0; k < EB; k++)
+#pragma unroll
+        for (int s = 0; s < SMAX; s++) acc[k][s] = 0.0f;
     if ((D & 3) == 0) {
         for (int d = threadIdx.x * 4; d < D; d += 1024) {
-            float4 wv = *(const float4 *)(w + d);
+            float4 wv[EB];
+#pragma unroll
+            for (int k = 0; k < EB; k++)
+                wv[k] = e0 + k < E ? *(const float4 *)(W + (size_t)(e0 + k) * D + d) : make_float4(0, 0, 0, 0);
 #pragma unroll
             for (int s = 0; s < SMAX; s++) {
                 if (s < S) {
                     float4 xv = *(const float4 *)(x + (size_t)s * D + d);
-                    acc[s] = fmaf(xv.x, wv.x, acc[s]);
-                    acc[s] = fmaf(xv.y, wv.y, acc[s]);
-                    acc[s] = fmaf(xv.z, wv.z, acc[s]);
-                    acc[s] = fmaf(xv.w, wv.w, acc[s]);
+#pragma unroll
+                    for (int k = 0; k < EB; k++) {
+                        acc[k][s] = fmaf(xv.x, wv[k].x, acc[k][s]);
+                        acc[k][s] = fmaf(xv.y, wv[k].y, acc[k][s]);
+                        acc[k][s] = fmaf(xv.z, wv[k].z, acc[k][s]);
+                        acc[k][s] = fmaf(xv.w, wv[k].w, acc[k][s]);
+                    }
                 }
             }
         }
     } else {
         for (int d = threadIdx.x; d < D; d += 256) {
-            float wv = w[d];
 #pragma unroll
-            for (int s = 0; s < SMAX; s++)
-                if (s < S) acc[s] = fmaf(x[(size_t)s * D + d], wv, acc[s]);
+            for (int k = 0; k < EB; k++) {
+                float wv = e0 + k < E ? W[(size_t)(e0 + k) * D + d] : 0.0f;
+#pragma unroll
+                for (int s = 0; s < SMAX; s++)
+                    if (s < S) acc[k][s] = fmaf(x[(size_t)s * D + d], wv, acc[k][s]);
+            }
         }
     }
-    __shared__ float red[SMAX][256];
+    __shared__ float red[4][EB * SMAX];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int s = 0; s < SMAX; s++) red[s][threadIdx.x] = acc[s];
+    for (int k = 0; k < EB; k++)
+#pragma unroll
+        for (int s = 0; s < SMAX; s++) {
+            float v = acc[k][s];
+#pragma unroll
+            for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) red[wave][k * SMAX + s] = v;
+        }
     __syncthreads();
-    for (int st = 128; st; st >>= 1) {
-        if (threadIdx.x < st)
-#pragma unroll
-            for (int s = 0; s < SMAX; s++) red[s][threadIdx.x] += red[s][threadIdx.x + st];
-        __syncthreads();
+    for (int o = threadIdx.x; o < EB * SMAX; o += 256) {
+        int k = o / SMAX, s = o - k * SMAX;
+        if (s < S && e0 + k < E)
+            logits[(size_t)s * E + e0 + k] = ((red[0][o] + red[1][o]) + red[2][o]) + red[3][o];
     }
-    if (threadIdx.x < S && threadIdx.x < SMAX) logits[(size_t)threadIdx.x * E + e] = red[threadIdx.x][0];
 }
 
 extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E,
@@ -116,14 +133,16 @@ extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const flo
         int n = S - s0 < 16 ? S - s0 : 16;
         const float *xs = x + (size_t)s0 * D;
         float *ls = logits + (size_t)s0 * E;
-        if (n <= 4) hipLaunchKernelGGL(coli_router_logits<4>, dim3(E), dim3(256), 0, st, xs, n, W, D, E, ls);
-        else hipLaunchKernelGGL(coli_router_logits<16>, dim3(E), dim3(256), 0, st, xs, n, W, D, E, ls);
+        if (n <= 4)
+            hipLaunchKernelGGL((coli_router_logits<4, 1>), dim3(E), dim3(256), 0, st, xs, n, W, D, E, ls);
+        else
+            hipLaunchKernelGGL((coli_router_logits<16, 4>), dim3((E + 3) / 4), dim3(256), 0, st, xs, n, W, D, E, ls);
     }
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Top-K selection, one block per token row (E <= 4096, K <= 64).
+// Top-K selection, one 64-lane wave per token row (E <= 4096, K <= 64).
 //   mode 0: p = softmax(z) (max-subtracted, c/olmoe.c:246-250), select on p,
 //           weight p, optional norm over K without epsilon (c/olmoe.c:681).
 //   mode 1: p = sigmoid(z), choice = p + bias, select on choice, weight p,
@@ -134,166 +153,140 @@ extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const flo
 //           with +1e-20; TOPP keeps until cum >= topp and renormalizes the
 //           kept set (c/kimi_k3.c:1337-1370); routed_scale applied after.
 // Selection is K rounds of an argmax with strict '>' semantics (highest
-// value, lowest index on ties, NaN never selected); an all-NaN round falls
-// back to index kk (c/route_trace.h:383-393).
+// value, lowest index on ties, NaN never selected, values <= -1e30 never
+// selected); an all-NaN round falls back to index kk (c/route_trace.h:383-393).
+// Lane l owns experts e = l (mod 64); a selected expert is retired by its
+// owner lane, so the rounds need no barrier.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-    // v is better than (bv, bi): larger value, or equal value and lower index.
-    if (bi < 0) return !(v != v) && v > -1e30f;
-    if (v != v) return false;
+    // (v, i) beats (bv, bi): larger value, or equal value and lower index.
+    if (v != v || !(v > -1e30f)) return false;
+    if (bi < 0) return true;
     return v > bv || (v == bv && i < bi);
 }
 
 __global__ __launch_bounds__(256) void coli_router_select(const float *__restrict__ logits,
-                                                          const float *__restrict__ bias, int E, int K,
+                                                          const float *__restrict__ bias, int S, int E, int K,
                                                           int mode, float topp, int norm_topk,
                                                           float routed_scale, int *__restrict__ idx,
                                                           float *__restrict__ wout, int *__restrict__ keff) {
     extern __shared__ float sh[];
-    float *p = sh;          // [E] weight source
-    float *c = sh + E;      // [E] selection score
-    __shared__ float rv[256];
-    __shared__ int ri[256];
-    __shared__ int sel[64];
-    __shared__ float selw[64];
-    __shared__ float smax, ssum;
-    const int s = blockIdx.x;
-    const float *z = logits + (size_t)s * E;
-    const int tid = threadIdx.x;
-
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int s = blockIdx.x * 4 + wave;
+    float *p = sh + (size_t)wave * (2 * E + 128);     // [E] weight source
+    float *c = p + E;                                 // [E] selection score
+    int *sel = (int *)(c + E);                        // [64]
+    float *selw = c + E + 64;                         // [64]
+    const bool live = s < S;
+    const float *z = logits + (size_t)(live ? s : 0) * E;
     if (mode == 0) {
         float m = -1e30f;
-        for (int e = tid; e < E; e += 256) m = fmaxf(m, z[e] > m ? z[e] : m);
-        rv[tid] = m;
-        __syncthreads();
-        for (int st = 128; st; st >>= 1) {
-            if (tid < st) rv[tid] = fmaxf(rv[tid], rv[tid + st]);
-            __syncthreads();
-        }
-        if (tid == 0) smax = rv[0];
-        __syncthreads();
+        for (int e = lane; e < E; e += 64) m = fmaxf(m, z[e]);
+#pragma unroll
+        for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
         float part = 0.0f;
-        for (int e = tid; e < E; e += 256) {
-            float v = expf(z[e] - smax);
+        for (int e = lane; e < E; e += 64) {
+            float v = expf(z[e] - m);
             p[e] = v;
             part += v;
         }
-        rv[tid] = part;
-        __syncthreads();
-        for (int st = 128; st; st >>= 1) {
-            if (tid < st) rv[tid] += rv[tid + st];
-            __syncthreads();
-        }
-        if (tid == 0) ssum = rv[0];
-        __syncthreads();
-        for (int e = tid; e < E; e += 256) {
-            p[e] = p[e] / ssum;
+#pragma unroll
+        for (int off = 32; off; off >>= 1) part += __shfl_xor(part, off);
+        for (int e = lane; e < E; e += 64) {
+            p[e] = p[e] / part;
             c[e] = p[e];
         }
     } else {
-        for (int e = tid; e < E; e += 256) {
+        for (int e = lane; e < E; e += 64) {
             float v = 1.0f / (1.0f + expf(-z[e]));
             p[e] = v;
             c[e] = v + (bias ? bias[e] : 0.0f);
         }
     }
     __syncthreads();
-
+    if (!live) return;
     for (int kk = 0; kk < K; kk++) {
         float bv = 0.0f;
         int bi = -1;
-        for (int e = tid; e < E; e += 256) {
-            bool taken = false;
-            for (int j = 0; j < kk; j++) taken |= (sel[j] == e);
-            if (!taken && better(c[e], e, bv, bi)) { bv = c[e]; bi = e; }
+        for (int e = lane; e < E; e += 64)
+            if (better(c[e], e, bv, bi)) { bv = c[e]; bi = e; }
+#pragma unroll
+        for (int off = 32; off; off >>= 1) {
+            float ov = __shfl_xor(bv, off);
+            int oi = __shfl_xor(bi, off);
+            if (oi >= 0 && better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
         }
-        rv[tid] = bv;
-        ri[tid] = bi;
-        __syncthreads();
-        for (int st = 128; st; st >>= 1) {
-            if (tid < st) {
-                int oi = ri[tid + st];
-                if (oi >= 0 && better(rv[tid + st], oi, rv[tid], ri[tid])) {
-                    rv[tid] = rv[tid + st];
-                    ri[tid] = oi;
-                }
-            }
-            __syncthreads();
-        }
-        if (tid == 0) {
-            int best = ri[0];
-            if (best < 0) best = kk < E ? kk : 0;
+        int best = bi >= 0 ? bi : (kk < E ? kk : 0);
+        if (bi >= 0 && (best & 63) == lane) c[best] = __builtin_nanf("");   // retire
+        if (lane == 0) {
             sel[kk] = best;
             selw[kk] = p[best];
         }
-        __syncthreads();
     }
-
-    if (tid == 0) {
-        int ke = K;
-        if (mode == 0) {
-            if (norm_topk) {
-                float sm = 0.0f;
-                for (int kk = 0; kk < K; kk++) sm += selw[kk];
-                for (int kk = 0; kk < K; kk++) selw[kk] /= sm;
-            }
-        } else if (mode == 1) {
-            if (topp > 0.0f && topp < 1.0f) {
-                for (int a = 1; a < K; a++) {
-                    int ii = sel[a]; float ww = selw[a]; int b = a - 1;
-                    while (b >= 0 && selw[b] < ww) { selw[b + 1] = selw[b]; sel[b + 1] = sel[b]; b--; }
-                    selw[b + 1] = ww; sel[b + 1] = ii;
-                }
-                float tot = 1e-20f, cum = 0.0f;
-                for (int kk = 0; kk < K; kk++) tot += selw[kk];
-                for (int kk = 0; kk < K; kk++) {
-                    cum += selw[kk];
-                    if (cum >= topp * tot) { ke = kk + 1; break; }
-                }
-            }
-            if (norm_topk) {
-                float sm = 0.0f;
-                for (int kk = 0; kk < ke; kk++) sm += selw[kk];
-                sm += 1e-20f;
-                for (int kk = 0; kk < ke; kk++) selw[kk] /= sm;
-            }
-            for (int kk = 0; kk < ke; kk++) selw[kk] *= routed_scale;
-        } else {
+    if (lane != 0) return;
+    int ke = K;
+    if (mode == 0) {
+        if (norm_topk) {
             float sm = 0.0f;
             for (int kk = 0; kk < K; kk++) sm += selw[kk];
-            for (int kk = 0; kk < K; kk++) selw[kk] /= (sm + 1e-20f);
-            if (topp > 0.0f && topp < 1.0f) {
-                for (int a = 1; a < K; a++) {
-                    int e2 = sel[a]; float w2 = selw[a]; int b = a - 1;
-                    while (b >= 0 && selw[b] < w2) { sel[b + 1] = sel[b]; selw[b + 1] = selw[b]; b--; }
-                    sel[b + 1] = e2; selw[b + 1] = w2;
-                }
-                float cum = 0.0f; int keep = K;
-                for (int kk = 0; kk < K; kk++) { cum += selw[kk]; if (cum >= topp) { keep = kk + 1; break; } }
-                if (keep < K) {
-                    float s2 = 0.0f;
-                    for (int kk = 0; kk < keep; kk++) s2 += selw[kk];
-                    for (int kk = 0; kk < keep; kk++) selw[kk] /= (s2 + 1e-20f);
-                    ke = keep;
-                }
+            for (int kk = 0; kk < K; kk++) selw[kk] /= sm;
+        }
+    } else if (mode == 1) {
+        if (topp > 0.0f && topp < 1.0f) {
+            for (int a = 1; a < K; a++) {
+                int ii = sel[a]; float ww = selw[a]; int b = a - 1;
+                while (b >= 0 && selw[b] < ww) { selw[b + 1] = selw[b]; sel[b + 1] = sel[b]; b--; }
+                selw[b + 1] = ww; sel[b + 1] = ii;
             }
-            if (routed_scale != 1.0f)
-                for (int kk = 0; kk < ke; kk++) selw[kk] *= routed_scale;
+            float tot = 1e-20f, cum = 0.0f;
+            for (int kk = 0; kk < K; kk++) tot += selw[kk];
+            for (int kk = 0; kk < K; kk++) {
+                cum += selw[kk];
+                if (cum >= topp * tot) { ke = kk + 1; break; }
+            }
         }
-        for (int kk = 0; kk < K; kk++) {
-            idx[(size_t)s * K + kk] = sel[kk];
-            wout[(size_t)s * K + kk] = kk < ke ? selw[kk] : 0.0f;
+        if (norm_topk) {
+            float sm = 0.0f;
+            for (int kk = 0; kk < ke; kk++) sm += selw[kk];
+            sm += 1e-20f;
+            for (int kk = 0; kk < ke; kk++) selw[kk] /= sm;
         }
-        keff[s] = ke;
+        for (int kk = 0; kk < ke; kk++) selw[kk] *= routed_scale;
+    } else {
+        float sm = 0.0f;
+        for (int kk = 0; kk < K; kk++) sm += selw[kk];
+        for (int kk = 0; kk < K; kk++) selw[kk] /= (sm + 1e-20f);
+        if (topp > 0.0f && topp < 1.0f) {
+            for (int a = 1; a < K; a++) {
+                int e2 = sel[a]; float w2 = selw[a]; int b = a - 1;
+                while (b >= 0 && selw[b] < w2) { sel[b + 1] = sel[b]; selw[b + 1] = selw[b]; b--; }
+                sel[b + 1] = e2; selw[b + 1] = w2;
+            }
+            float cum = 0.0f; int keep = K;
+            for (int kk = 0; kk < K; kk++) { cum += selw[kk]; if (cum >= topp) { keep = kk + 1; break; } }
+            if (keep < K) {
+                float s2 = 0.0f;
+                for (int kk = 0; kk < keep; kk++) s2 += selw[kk];
+                for (int kk = 0; kk < keep; kk++) selw[kk] /= (s2 + 1e-20f);
+                ke = keep;
+            }
+        }
+        if (routed_scale != 1.0f)
+            for (int kk = 0; kk < ke; kk++) selw[kk] *= routed_scale;
     }
+    for (int kk = 0; kk < K; kk++) {
+        idx[(size_t)s * K + kk] = sel[kk];
+        wout[(size_t)s * K + kk] = kk < ke ? selw[kk] : 0.0f;
+    }
+    keff[s] = ke;
 }
 
 extern "C" hipError_t coli_launch_router_select(const float *logits, const float *bias, int S, int E,
                                                 int K, int mode, float topp, int norm_topk,
                                                 float routed_scale, int *idx, float *w, int *keff,
                                                 hipStream_t st) {
-    size_t shm = (size_t)2 * E * sizeof(float);
-    hipLaunchKernelGGL(coli_router_select, dim3(S), dim3(256), shm, st, logits, bias, E, K, mode, topp,
+    size_t shm = (size_t)4 * (2 * E + 128) * sizeof(float);
+    hipLaunchKernelGGL(coli_router_select, dim3((S + 3) / 4), dim3(256), shm, st, logits, bias, S, E, K, mode, topp,
                        norm_topk, routed_scale, idx, w, keff);
     return hipGetLastError();
 }

@@ -27,7 +27,7 @@
 float cref_e2m1_decode(uint8_t nibble) {
     int n = nibble & 15, e = (n >> 1) & 3, m = n & 1;
     float mag = e ? ldexpf(1.0f + 0.5f * (float)m, e - 1) : 0.5f * (float)m;
-    return (n & 8) ? -mag : mag;
+    return (n & 8) && mag != 0.0f ? -mag : mag;  /* code 8 decodes to +0 */
 }
 
 /* native_quant e8m0: 2^(v-127), 0xff -> NaN (c/deepseek_v4.c:10390-10393). */
@@ -137,17 +137,23 @@ static inline float hsum8(const float a[8]) {
     return (l0 + l2) + (l1 + l3);
 }
 
-/* y = x W^T, W f32 [O,I]; the scalar loop of c/quant.h:97-102: one
- * multiply and one add per element, ascending i (the reference build does
- * not contract this loop). */
+/* y = x W^T, W f32 [O,I]; the loop of c/quant.h:97-102 as gcc -O3
+ * -march=x86-64-v3 builds it: ascending i, each product rounded then added
+ * (the vectorised body) for i < (I & ~3), and the last I mod 4 columns
+ * contracted to one fma each (the scalar epilogue). */
 void cref_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O) {
+    const int body = I & ~3;
     #pragma omp parallel for schedule(static)
     for (int o = 0; o < O; o++) {
         const float *w = W + (int64_t)o * I;
         for (int s = 0; s < S; s++) {
             const float *xs = x + (int64_t)s * I;
             float a = 0.0f;
-            for (int i = 0; i < I; i++) a = a + xs[i] * w[i];
+            for (int i = 0; i < body; i++) {
+                float p = xs[i] * w[i];
+                a = a + p;
+            }
+            for (int i = body; i < I; i++) a = fmaf(xs[i], w[i], a);
             y[(int64_t)s * O + o] = a;
         }
     }
