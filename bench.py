@@ -326,12 +326,25 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-moe", action="store_true")
     ap.add_argument("--moe-steps", type=int, default=50)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only copy 256 MiB device-to-device 4 times (the known-size reference that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the expert path has no collectives; "
                                    "run with --gpus 1 (see DESIGN.md for how it would shard)"}))
         sys.exit(2)
     bench = Bench(args)
+    if args.copy_calib:
+        nb = 256 << 20
+        src, dst = bench.alloc(nb), bench.alloc(nb)
+        assert bench.b.hip_fill_random_u8(0, src, nb, 7)
+        for _ in range(4):
+            bench.hiprt.copy_d2d_async(dst, src, nb, bench.stream)
+        bench.hiprt.device_sync()
+        bench.close()
+        print(json.dumps({"copy_calib_bytes": nb, "copies": 4}))
+        return
     bench.dense()
     r = bench.dense_result
     out = {

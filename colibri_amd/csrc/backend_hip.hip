@@ -141,7 +141,7 @@ extern "C" void coli_cuda_shutdown(void) {
         if (!select_ctx(ctx)) continue;
         (void)hipStreamSynchronize(ctx->stream);
         DevBuf *bufs[] = {&ctx->x, &ctx->h, &ctx->y, &ctx->g, &ctx->u, &ctx->partial,
-                          &ctx->prob, &ctx->iota, &ctx->stage_w, &ctx->stage_s, &ctx->qdq, &ctx->flags,
+                          &ctx->prob, &ctx->stage_w, &ctx->stage_s, &ctx->qdq, &ctx->flags,
                           &ctx->rslot, &ctx->rw, &ctx->tmp_tiles, &ctx->tmp_scales, &ctx->zeros};
         for (DevBuf *b : bufs) free_buf(b);
         for (int f = 0; f < 4; f++) {

@@ -24,7 +24,7 @@ struct DevCtx {
     hipStream_t stream = nullptr;
     size_t tensor_count = 0, tensor_bytes = 0;
     // grow-only scratch
-    DevBuf x, h, y, g, u, partial, prob, iota, zeros, stage_w, stage_s, qdq, flags;
+    DevBuf x, h, y, g, u, partial, prob, zeros, stage_w, stage_s, qdq, flags;
     DevBuf rslot, rw, tmp_tiles, tmp_scales;
     FragSet frag[4];                   // 0/1: inputs (int4 / fp4 order), 2/3: hidden rows
     DevBuf pipe[COLI_PIPE_SLOTS];
@@ -58,7 +58,7 @@ hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, in
                             hipStream_t st);
 hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, const int *nrows_dev,
                                  int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
-                                 int *exp2out, int *haslo, int gen, hipStream_t st);
+                                 int *exp2out, int *haslo, int gen, const void *zero, hipStream_t st);
 hipError_t coli_launch_repack(const ColiCudaTensor *t, const uint8_t *src_w, const void *src_s,
                               hipStream_t st);
 hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const float *x, int ldx, float *y, int ldy,

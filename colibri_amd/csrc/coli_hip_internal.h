@@ -58,14 +58,15 @@ struct ColiProb {
 };
 
 struct ColiGemvArgs {
-    const ColiProb *prob;
+    const ColiProb *prob;     // device descriptors; null: the single problem prob0
+    ColiProb prob0;
     const int *nprob_dev;     // if non-null, number of live problems (device)
     int nprob;                // upper bound (grid sizing)
     int nrt, nq, O;           // tiles, real output rows
     int n_bt;                 // 16-row batch tiles per problem
     int rb_per_prob;          // row blocks per problem
     int splits, qps;          // K split
-    const int *xrows;
+    const int *xrows;         // fragment row of batch row r = xrows[xrow_off + r] (null: xrow_off + r)
     const _Float16 *xhi, *xlo;
     int xstride;              // halves per fragment row (= ngp * 32)
     const int *xexp;          // per fragment row

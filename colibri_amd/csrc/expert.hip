@@ -70,14 +70,6 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
     return p;
 }
 
-static int ensure_iota(DevCtx *ctx, int n) {
-    size_t want = (size_t)std::max(n, 4096) * sizeof(int);
-    if (ctx->iota.cap >= want) return 1;
-    if (!reserve(ctx, &ctx->iota, want, 0)) return 0;
-    std::vector<int> h(ctx->iota.cap / sizeof(int));
-    for (size_t i = 0; i < h.size(); i++) h[i] = (int)i;
-    return hip_ok(hipMemcpy(ctx->iota.p, h.data(), h.size() * sizeof(int), hipMemcpyHostToDevice), "iota");
-}
 
 static int ngp_of(int K) { return (K + 127) / 128 * 4; }
 
@@ -95,14 +87,14 @@ static int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, i
     if (f.gen == 1 && !hip_ok(coli_launch_zero_i32(flag, 1, ctx->stream), "fragment flag")) return 0;
     return hip_ok(coli_launch_prep_frag(x, ld, src_rows, nrows_dev, nrows, K, ngp, int4_order,
                                         (_Float16 *)f.hi.p, (_Float16 *)f.lo.p, (int *)f.exp.p, flag, f.gen,
-                                        ctx->stream),
+                                        ctx->zeros.p, ctx->stream),
                   "fragment prep");
 }
 
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob,
                     const int *nprob_dev, int nrt, int nq, int O, int max_rows, int set,
-                    const int *xrows_dev, float *out, int ldo) {
+                    const int *xrows_dev, float *out, int ldo, const ColiProb *inline_prob = nullptr) {
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
     GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
@@ -111,7 +103,12 @@ static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
         return 0;
     FragSet &f = ctx->frag[set];
     ColiGemvArgs a;
+    std::memset(&a, 0, sizeof(a));
     a.prob = probs_dev;
+    if (inline_prob) {
+        a.prob = nullptr;
+        a.prob0 = *inline_prob;
+    }
     a.nprob_dev = nprob_dev;
     a.nprob = nprob;
     a.nrt = nrt;
@@ -156,10 +153,8 @@ struct Member {
 // x_dev: [total, D] rows in member order; result y_dev: [total, D].
 static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, int D, int I, float *y_dev,
                             const float *x_dev) {
-    if (!ensure_iota(ctx, total)) return 0;
     if (!reserve(ctx, &ctx->h, (size_t)total * I * sizeof(float), 0)) return 0;
     float *h = (float *)ctx->h.p;
-    const int *iota = (const int *)ctx->iota.p;
 
     // classify members
     std::vector<int> dual_kind(count, -1);
@@ -236,7 +231,7 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
     for (const Launch &L : launches) {
         if (L.first >= down_first) break;
         if (!run_gemv(ctx, L.kind, L.dual, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set,
-                      iota, L.out, L.ldo))
+                      nullptr, L.out, L.ldo))
             return 0;
     }
     for (int c = 0; c < count; c++) {
@@ -259,7 +254,7 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
         if (need_h[o] && !make_frags(ctx, frag_set_of(o ? COLI_KIND_FP4 : 0, true), h, I, total, I, !o)) return 0;
     for (const Launch &L : launches) {
         if (L.first < down_first) continue;
-        if (!run_gemv(ctx, L.kind, false, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set, iota,
+        if (!run_gemv(ctx, L.kind, false, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set, nullptr,
                       L.out, L.ldo))
             return 0;
     }
@@ -410,29 +405,15 @@ extern "C" int coli_cuda_shared_mlp_w4a16(ColiCudaTensor *gate, ColiCudaTensor *
 // ---------------------------------------------------------------------------
 // Fragments of x_dev[S, I] for tensor t (input set of t's kind).
 static int gemm_prep(DevCtx *ctx, ColiCudaTensor *t, const float *x_dev, int S) {
-    if (!ensure_iota(ctx, S)) return 0;
     return make_frags(ctx, frag_set_of(t->kind, false), x_dev, t->I, S, t->I, t->kind != COLI_KIND_FP4);
 }
 
-// GEMV of t over the prepared fragments of S rows -> y_dev[S, O]. Uses the
-// tensor's cached descriptor for S <= 64 (no host synchronization).
+// GEMV of t over the prepared fragments of S rows -> y_dev[S, O]; the
+// problem travels in the kernel arguments (no descriptor, no host sync).
 static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S) {
-    const ColiProb *pd;
-    if (t->desc && S <= COLI_DESC_ROWS) {
-        pd = t->desc + (S - 1);
-    } else {
-        ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
-        if (!reserve_pinned(ctx, &ctx->host_prob, &ctx->host_prob_cap, sizeof(p)) ||
-            !reserve(ctx, &ctx->prob, sizeof(p), 0) || !hip_ok(hipStreamSynchronize(ctx->stream), "gemm staging"))
-            return 0;
-        std::memcpy(ctx->host_prob, &p, sizeof(p));
-        if (!hip_ok(hipMemcpyAsync(ctx->prob.p, ctx->host_prob, sizeof(p), hipMemcpyHostToDevice, ctx->stream),
-                    "gemm descriptor"))
-            return 0;
-        pd = (const ColiProb *)ctx->prob.p;
-    }
-    return run_gemv(ctx, t->kind, false, pd, 1, nullptr, t->nrt, t->nq, t->O, S, frag_set_of(t->kind, false),
-                    (const int *)ctx->iota.p, y_dev, t->O);
+    const ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
+    return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, frag_set_of(t->kind, false),
+                    nullptr, y_dev, t->O, &p);
 }
 
 // y_dev[S, O] = x_dev[S, I] W^T on the stream (tensor already resident).

@@ -126,65 +126,87 @@ __global__ void coli_repack_scales_e8(const uint8_t *__restrict__ src, int O, in
 // Layout per row: [ngp groups][4 kslices][8 halves]; slot t of kslice s of
 // group g holds column 32g + 8s + perm[t], perm = {0,2,4,6,1,3,5,7} (int4)
 // or identity (fp4), matching the B-operand order built in the GEMV.
-// Grid (chunks of 2048 fragment elements, rows); every block of a row derives
-// the row maximum itself (the row is L2-resident), so one launch does it all.
-// Whether any lo part is non-zero is published as `gen` into *haslo with an
-// atomic max: the GEMV of the same generation compares against `gen`, so the
-// flag never needs clearing; the GEMV treats any flag >= its generation as
-// "lo present", which stays correct when a captured graph replays an old gen.
+// One 256-thread block per fragment row: the row is read once (up to 8 slots
+// of 8 columns per thread stay in registers between the maximum and the
+// conversion; longer rows re-read the rest), reduced to its maximum, then
+// converted. Whether any lo part is non-zero is published as `gen` into
+// *haslo with an atomic max: the GEMV treats any flag >= its generation as
+// "lo present", so the flag never needs clearing and stays correct when a
+// captured graph replays an old generation.
+#define COLI_PREP_SLOTS 8
 __global__ __launch_bounds__(256) void coli_prep_frag(const float *__restrict__ x, int ldx,
                                                       const int *__restrict__ src_row,
                                                       const int *__restrict__ nrows_dev, int K, int ngp,
                                                       int int4_order, _Float16 *__restrict__ hi,
                                                       _Float16 *__restrict__ lo, int *__restrict__ exp2out,
-                                                      int *__restrict__ haslo, int gen) {
-    const int r = blockIdx.y;
+                                                      int *__restrict__ haslo, int gen, int vec,
+                                                      const float *__restrict__ zero) {
+    const int r = blockIdx.x;
     if (nrows_dev && r >= *nrows_dev) return;
     const int srow = src_row ? src_row[r] : r;
     if (srow < 0) return;
     const float *xr = x + (size_t)srow * ldx;
-    __shared__ float red[256];
-    float m = 0.0f;
-    if ((K & 3) == 0 && ((ldx & 3) == 0)) {
-        for (int k = threadIdx.x * 4; k < K; k += 1024) {
-            float4 v = *(const float4 *)(xr + k);
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const int nslot = ngp * 4;
+    auto load_slot = [&](int slot, float (&v)[8]) {
+        const int k0 = slot * 8;
+        if (vec) {   // aligned rows, K % 8 == 0: slots past K read zeros
+            const float *p = slot < nslot && k0 < K ? xr + k0 : zero;
+            const floatx4 a = *GPTR(floatx4, p), b = *GPTR(floatx4, p + 4);
+#pragma unroll
+            for (int t = 0; t < 4; t++) { v[t] = a[t]; v[t + 4] = b[t]; }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; t++) v[t] = slot < nslot && k0 + t < K ? xr[k0 + t] : 0.0f;
         }
-    } else {
-        for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+    };
+    float v[COLI_PREP_SLOTS][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < COLI_PREP_SLOTS; i++) load_slot(threadIdx.x + 256 * i, v[i]);
+#pragma unroll
+    for (int i = 0; i < COLI_PREP_SLOTS; i++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) m = fmaxf(m, fabsf(v[i][t]));
+    for (int slot = threadIdx.x + 256 * COLI_PREP_SLOTS; slot < nslot; slot += 256) {
+        float u[8];
+        load_slot(slot, u);
+#pragma unroll
+        for (int t = 0; t < 8; t++) m = fmaxf(m, fabsf(u[t]));
     }
-    red[threadIdx.x] = m;
+#pragma unroll
+    for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __shared__ float wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
     __syncthreads();
-    for (int s = 128; s; s >>= 1) {
-        if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
-    m = red[0];
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     int E = 0;
     if (m > 0.0f && isfinite(m)) frexpf(m, &E);
-    if (blockIdx.x == 0 && threadIdx.x == 0) exp2out[r] = E;
-    // one thread = one 8-half slot (kslice s of group g): source columns 32g+8s .. +7
-    const int slot = blockIdx.x * 256 + threadIdx.x;
-    if (slot >= ngp * 4) return;
-    const int k0 = slot * 8;
-    float v[8];
-#pragma unroll
-    for (int t = 0; t < 8; t++) v[t] = k0 + t < K ? xr[k0 + t] : 0.0f;
-    _Float16 h[8], l[8];
+    if (threadIdx.x == 0) exp2out[r] = E;
     bool any = false;
+    auto convert = [&](int slot, const float (&u)[8]) {
+        if (slot >= nslot) return;
+        _Float16 h[8], l[8];
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-        int off = int4_order ? ((t < 4) ? 2 * t : 2 * (t - 4) + 1) : t;
-        float y = ldexpf(v[off], -E);
-        if (int4_order && (off & 1)) y *= 0.0625f;
-        h[t] = (_Float16)y;
-        l[t] = (_Float16)(y - (float)h[t]);
-        any |= (l[t] != (_Float16)0.0f);
+        for (int t = 0; t < 8; t++) {
+            int off = int4_order ? ((t < 4) ? 2 * t : 2 * (t - 4) + 1) : t;
+            float y = ldexpf(u[off], -E);
+            if (int4_order && (off & 1)) y *= 0.0625f;
+            h[t] = (_Float16)y;
+            l[t] = (_Float16)(y - (float)h[t]);
+            any |= (l[t] != (_Float16)0.0f);
+        }
+        const size_t base = (size_t)r * ngp * 32 + (size_t)slot * 8;
+        *(half8v *)(hi + base) = (half8v){h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+        *(half8v *)(lo + base) = (half8v){l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
+    };
+#pragma unroll
+    for (int i = 0; i < COLI_PREP_SLOTS; i++) convert(threadIdx.x + 256 * i, v[i]);
+    for (int slot = threadIdx.x + 256 * COLI_PREP_SLOTS; slot < nslot; slot += 256) {
+        float u[8];
+        load_slot(slot, u);
+        convert(slot, u);
     }
-    size_t base = (size_t)r * ngp * 32 + (size_t)k0;
-    *(half8v *)(hi + base) = (half8v){h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
-    *(half8v *)(lo + base) = (half8v){l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
-    if (any) atomicMax(haslo, gen);
+    if (__syncthreads_or(any) && threadIdx.x == 0) atomicMax(haslo, gen);
 }
 
 // ---------------------------------------------------------------------------
@@ -260,7 +282,7 @@ struct Stage {
     u32x4 w[R];
     ScaleRegs<KIND> sc[R];
     half8v xh[4];
-    half8v xl[LO ? 4 : 1];
+    half8v xl[LO ? 4 : 1];   // unused (and dead) unless the lo pass runs
 };
 
 #ifndef COLI_PD
@@ -273,26 +295,34 @@ struct Stage {
 // stay in flight while the wave computes. Iterations past the end read the
 // zero buffer instead (their math is skipped), which keeps every load
 // unconditional and the in-order vmcnt accounting exact.
+template <int KIND, int R>
+__device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, bool valid, int q, const size_t (&tbase)[R],
+                                             const int (&tstep)[R], const uint8_t *const (&wb)[R],
+                                             const void *const (&sb)[R], const _Float16 *zero, int lane) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        size_t tq = valid ? tbase[r] + (size_t)q * tstep[r] : 0;
+        const uint8_t *w = valid ? wb[r] : (const uint8_t *)zero;
+        const void *sp = valid ? sb[r] : (const void *)zero;
+        sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + tq * COLI_TILE_BYTES) + lane);
+        sg.sc[r].load(sp, tq, lane & 15);
+    }
+}
+
+// The caller has already issued the weight/scale loads of iteration 0 into
+// st[0] (before it knew the activation rows), so the first HBM requests
+// leave the CU as early as possible.
 template <int KIND, int R, int NB4, int W, bool LO>
-__device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], int q_first, int Q1, const size_t (&tbase)[R],
-                                           const int (&tstep)[R], const uint8_t *const (&wb)[R],
-                                           const void *const (&sb)[R], const _Float16 *xh, const _Float16 *xl,
-                                           const _Float16 *zero, int lane) {
+__device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, true> (&st)[COLI_PD], int q_first, int Q1,
+                                           const size_t (&tbase)[R], const int (&tstep)[R],
+                                           const uint8_t *const (&wb)[R], const void *const (&sb)[R],
+                                           const _Float16 *xh, const _Float16 *xl, const _Float16 *zero, int lane) {
     constexpr int PD = COLI_PD;
     if (q_first >= Q1) return;
     const int nit = (Q1 - q_first + W - 1) / W;
-    Stage<KIND, R, LO> st[PD];
-    auto load = [&](Stage<KIND, R, LO> &sg, int it) {
+    auto load_x = [&](Stage<KIND, R, true> &sg, int it) {
         const bool valid = it < nit;
         const int q = q_first + it * W;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            size_t tq = valid ? tbase[r] + (size_t)q * tstep[r] : 0;
-            const uint8_t *w = valid ? wb[r] : (const uint8_t *)zero;
-            const void *sp = valid ? sb[r] : (const void *)zero;
-            sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + tq * COLI_TILE_BYTES) + lane);
-            sg.sc[r].load(sp, tq, lane & 15);
-        }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const _Float16 *ph = valid ? xh + (size_t)(4 * q + j) * 32 : zero;
@@ -303,7 +333,11 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], int q_first, int Q
             }
         }
     };
-    auto compute = [&](const Stage<KIND, R, LO> &sg) {
+    auto load = [&](Stage<KIND, R, true> &sg, int it) {
+        load_weights<KIND, R>(sg, it < nit, q_first + it * W, tbase, tstep, wb, sb, zero, lane);
+        load_x(sg, it);
+    };
+    auto compute = [&](const Stage<KIND, R, true> &sg) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
 #pragma unroll
@@ -317,8 +351,9 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], int q_first, int Q
             }
         }
     };
+    load_x(st[0], 0);
 #pragma unroll
-    for (int p = 0; p < PD - 1; p++) load(st[p], p);
+    for (int p = 1; p < PD - 1; p++) load(st[p], p);
     for (int it0 = 0; it0 < nit; it0 += PD) {
 #pragma unroll
         for (int u = 0; u < PD; u++) {
@@ -333,11 +368,11 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], int q_first, int Q
 // DUAL, silu(gate) * up of the paired tiles.
 template <int R, bool DUAL>
 __device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiProb &pr, int bt, const int (&rt)[R],
-                                              const bool (&live)[R], const float (&v)[R], int brow, int lane) {
+                                              const bool (&live)[R], const float (&v)[R], int brow, int lane,
+                                              int E) {
     constexpr int RT = DUAL ? R / 2 : R;
     const int nb = min(16, pr.nrows - 16 * bt);
     if (brow >= nb) return;
-    const int E = a.xexp[a.xrows[pr.xrow_off + 16 * bt + brow]];
     float *orow = a.out + (size_t)(pr.out_row0 + 16 * bt + brow) * a.ldo;
 #pragma unroll
     for (int r = 0; r < RT; r++) {
@@ -381,21 +416,12 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     rem -= bt * items_per_bt;
     const int rb = rem / a.splits;
     const int s = rem - rb * a.splits;
-    const ColiProb pr = a.prob[p];
+    const ColiProb pr = a.prob ? a.prob[p] : a.prob0;
     const int nb = min(16, pr.nrows - 16 * bt);
     if (nb <= 0) return;
 
     const int b = lane & 15, ks = lane >> 4;
     const int Q0 = s * a.qps, Q1 = min(a.nq, Q0 + a.qps);
-    const bool use_lo = *a.haslo >= a.lo_gen;  // >=: stays correct under graph replay
-
-    // Lanes past the problem's rows read the zero fragment row.
-    const _Float16 *xh = a.zero, *xl = a.zero;
-    if (b < nb) {
-        const int fr = a.xrows[pr.xrow_off + 16 * bt + b];
-        xh = a.xhi + (size_t)fr * a.xstride + ks * 8;
-        xl = a.xlo + (size_t)fr * a.xstride + ks * 8;
-    }
 
     // Row tiles past the matrix read the zero buffer (zero scale: no contribution).
     int rt[R];
@@ -415,12 +441,35 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
         tbase[r] = live[r] ? (size_t)rt[r] * a.nq : 0;
         tstep[r] = live[r] ? 1 : 0;
     }
+    // the first weight stage goes out before anything else is resolved
+    Stage<KIND, R, true> st[COLI_PD];
+    const int q_first = Q0 + wave;
+    load_weights<KIND, R>(st[0], q_first < Q1, q_first, tbase, tstep, wb, sb, a.zero, lane);
+
+    const bool use_lo = *a.haslo >= a.lo_gen;  // >=: stays correct under graph replay
+    // Lanes past the problem's rows read the zero fragment row.
+    const _Float16 *xh = a.zero, *xl = a.zero;
+    if (b < nb) {
+        const int br = pr.xrow_off + 16 * bt + b;
+        const int fr = a.xrows ? a.xrows[br] : br;
+        xh = a.xhi + (size_t)fr * a.xstride + ks * 8;
+        xl = a.xlo + (size_t)fr * a.xstride + ks * 8;
+    }
+    // exponent of the batch row this wave finishes (used after the loop)
+    int E_out = 0;
+    if (a.splits == 1 && wave < NB4) {
+        const int brow = ks * 4 + wave;
+        if (brow < nb) {
+            const int br = pr.xrow_off + 16 * bt + brow;
+            E_out = a.xexp[a.xrows ? a.xrows[br] : br];
+        }
+    }
 
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
-    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
-    else gemv_quads<KIND, R, NB4, W, false>(acc, Q0 + wave, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
+    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, st, q_first, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
+    else gemv_quads<KIND, R, NB4, W, false>(acc, st, q_first, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
 
     // ---- intra-group reduction in fixed wave order; wave i finishes register i ----
 #pragma unroll
@@ -451,7 +500,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
         return;
     }
     if (i >= NB4) return;
-    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, ks * 4 + i, lane);
+    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, ks * 4 + i, lane, E_out);
 }
 
 // Second pass of a split-K launch: sums the groups' partials in split order
@@ -469,10 +518,12 @@ __global__ __launch_bounds__(256) void coli_gemv_reduce(ColiGemvArgs a) {
     if (a.nprob_dev && p >= *a.nprob_dev) return;
     const int rem = (int)(inst - (size_t)p * a.n_bt * a.rb_per_prob);
     const int bt = rem / a.rb_per_prob, rb = rem - bt * a.rb_per_prob;
-    const ColiProb pr = a.prob[p];
+    const ColiProb pr = a.prob ? a.prob[p] : a.prob0;
     const int nb = min(16, pr.nrows - 16 * bt);
     const int brow = 4 * (lane >> 4) + i;
     if (nb <= 0 || brow >= nb) return;
+    const int br = pr.xrow_off + 16 * bt + brow;
+    const int E = a.xexp[a.xrows ? a.xrows[br] : br];
     float v[R];
 #pragma unroll
     for (int r = 0; r < R; r++) v[r] = 0.0f;
@@ -487,7 +538,7 @@ __global__ __launch_bounds__(256) void coli_gemv_reduce(ColiGemvArgs a) {
         rt[r] = rb * RT + (DUAL ? r % RT : r);
         live[r] = rt[r] < a.nrt;
     }
-    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, brow, lane);
+    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, brow, lane, E);
 }
 
 // ---------------------------------------------------------------------------
@@ -650,11 +701,12 @@ extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, i
 extern "C" hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row,
                                             const int *nrows_dev, int nrows, int K, int ngp,
                                             int int4_order, _Float16 *hi, _Float16 *lo,
-                                            int *exp2out, int *haslo, int gen, hipStream_t st) {
+                                            int *exp2out, int *haslo, int gen, const void *zero,
+                                            hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
-    dim3 grid((ngp * 4 + 255) / 256, nrows);
-    hipLaunchKernelGGL(coli_prep_frag, grid, dim3(256), 0, st, x, ldx, src_row, nrows_dev, K, ngp, int4_order,
-                       hi, lo, exp2out, haslo, gen);
+    const int vec = ((uintptr_t)x % 16 == 0) && (ldx % 4 == 0) && (K % 8 == 0);
+    hipLaunchKernelGGL(coli_prep_frag, dim3(nrows), dim3(256), 0, st, x, ldx, src_row, nrows_dev, K, ngp, int4_order,
+                       hi, lo, exp2out, haslo, gen, vec, (const float *)zero);
     return hipGetLastError();
 }
 

@@ -243,7 +243,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     fx.gen = fx.gen == 0x7fffffff ? 1 : fx.gen + 1;
     if (fx.gen == 1 && !hip_ok(coli_launch_zero_i32(flags + ord, 1, st), "moe flag")) return 0;
     if (!hip_ok(coli_launch_prep_frag(x_dev, c.D, nullptr, nullptr, S, c.D, nq_d * 4, !ord, (_Float16 *)fx.hi.p,
-                                      (_Float16 *)fx.lo.p, (int *)fx.exp.p, flags + ord, fx.gen, st),
+                                      (_Float16 *)fx.lo.p, (int *)fx.exp.p, flags + ord, fx.gen, ctx->zeros.p, st),
                 "moe x fragments") ||
         !hip_ok(coli_launch_router_logits(x_dev, S, m->rw, c.D, c.E, m->logits, st), "moe router logits") ||
         !hip_ok(coli_launch_router_select(m->logits, m->rb, S, c.E, c.K, c.route_mode, c.topp, c.norm_topk,
@@ -285,7 +285,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     if (fh.gen == 1 && !hip_ok(coli_launch_zero_i32(flags + 2 + ord, 1, st), "moe flag")) return 0;
     if (!hip_ok(coli_launch_prep_frag(m->h, c.I, m->hrows, m->state + 1, P * RS, c.I, nq_i * 4, !ord,
                                       (_Float16 *)fh.hi.p, (_Float16 *)fh.lo.p, (int *)fh.exp.p, flags + 2 + ord,
-                                      fh.gen, st),
+                                      fh.gen, ctx->zeros.p, st),
                 "moe hidden fragments"))
         return 0;
     // 7. down
@@ -297,7 +297,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     a.rb_per_prob = pl.rbpp;
     a.splits = pl.splits;
     a.qps = pl.qps;
-    a.xrows = m->hrows;
+    a.xrows = nullptr;   // hidden rows are fragment rows
     a.xhi = (const _Float16 *)fh.hi.p;
     a.xlo = (const _Float16 *)fh.lo.p;
     a.xstride = nq_i * 128;

@@ -27,6 +27,7 @@ def lib():
         _lib.hipEventDestroy.argtypes = [C.c_void_p]
         _lib.hipStreamSynchronize.argtypes = [C.c_void_p]
         _lib.hipDeviceSynchronize.argtypes = []
+        _lib.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
     return _lib
 
 
@@ -60,3 +61,8 @@ def device_sync():
 
 def stream_sync(stream):
     check(lib().hipStreamSynchronize(stream), "hipStreamSynchronize")
+
+
+def copy_d2d_async(dst, src, nbytes, stream):
+    """Device-to-device copy on `stream` (hipMemcpyDeviceToDevice = 3)."""
+    check(lib().hipMemcpyAsync(dst, src, nbytes, 3, stream), "hipMemcpyAsync")
