@@ -28,6 +28,12 @@ def lib():
         _lib.hipStreamSynchronize.argtypes = [C.c_void_p]
         _lib.hipDeviceSynchronize.argtypes = []
         _lib.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        _lib.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        _lib.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        _lib.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+        _lib.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        _lib.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        _lib.hipGraphDestroy.argtypes = [C.c_void_p]
     return _lib
 
 
@@ -66,3 +72,34 @@ def stream_sync(stream):
 def copy_d2d_async(dst, src, nbytes, stream):
     """Device-to-device copy on `stream` (hipMemcpyDeviceToDevice = 3)."""
     check(lib().hipMemcpyAsync(dst, src, nbytes, 3, stream), "hipMemcpyAsync")
+
+
+class Graph:
+    """A HIP graph captured from everything enqueued on `stream` inside the
+    `with` block (thread-local capture mode), then instantiated for replay."""
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.graph = C.c_void_p()
+        self.exec = C.c_void_p()
+
+    def __enter__(self):
+        check(lib().hipStreamBeginCapture(self.stream, 1), "hipStreamBeginCapture")
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        err = lib().hipStreamEndCapture(self.stream, C.byref(self.graph))
+        if exc_type is None:
+            check(err, "hipStreamEndCapture")
+            check(lib().hipGraphInstantiate(C.byref(self.exec), self.graph, None, None, 0), "hipGraphInstantiate")
+        return False
+
+    def launch(self):
+        check(lib().hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def __del__(self):
+        if _lib is not None:
+            if self.exec:
+                _lib.hipGraphExecDestroy(self.exec)
+            if self.graph:
+                _lib.hipGraphDestroy(self.graph)
