@@ -344,6 +344,18 @@ class Bench:
         self.s.close()
 
 
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (scaled by a calibration copy of known size); None when
+    that profile is absent."""
+    path = os.path.join(ROOT, "profiles", "coli_gemv_tiles_dense_int4_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -385,7 +397,7 @@ def main():
                    "weight_copies": r["copies"], "distinct_weight_GB": round(r["copies"] * r["pair"] / 1e9, 2)},
         "frac_of_peak": round(r["value"] / PEAK_GBS, 3),
         "roofline": {"bound": "hbm", "achieved": round(r["kern_gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r["kern_gbs"] / PEAK_GBS, 3), "traffic": None,
+                     "frac": round(r["kern_gbs"] / PEAK_GBS, 3), "traffic": measured_traffic(),
                      "kernel": "coli_gemv_tiles", "avg_launch_us": round(r["kern_avg_us"], 2),
                      "avg_launch_bytes": int(r["kern_avg_bytes"])},
         "gemv_by_batch": r["by_batch"],
