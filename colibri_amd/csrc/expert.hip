@@ -605,19 +605,20 @@ extern "C" int coli_cuda_pipe_router(int device, const float *x_dev, const void 
                                      int E, int Ksel, float topp, int norm_topk, float routed_scale, int *idx_host,
                                      float *w_host, int *keff_host) {
     DevCtx *ctx = find_ctx(device);
-    if (!x_dev || !rw_dev || !rb_dev || D < 1 || E < 1 || E > 4096 || Ksel < 1 || Ksel > 64 || !idx_host ||
+    if (!x_dev || !rw_dev || !rb_dev || D < 1 || E < 1 || E > 1024 || Ksel < 1 || Ksel > 64 || !idx_host ||
         !w_host || !keff_host || !select_ctx(ctx))
         return 0;
-    size_t pack = (size_t)E * sizeof(float) + (size_t)Ksel * 8 + 16;
+    const int nch = coli_router_chunks(D);
+    size_t pack = (size_t)nch * E * sizeof(float) + (size_t)Ksel * 8 + 16;
     if (!reserve(ctx, &ctx->pipe[22], pack, 0) ||
         !reserve_pinned(ctx, &ctx->host_small, &ctx->host_small_cap, (size_t)Ksel * 8 + 16))
         return 0;
     float *logit = (float *)ctx->pipe[22].p;
-    int *idx = (int *)(logit + E);
+    int *idx = (int *)(logit + (size_t)nch * E);
     float *w = (float *)(idx + Ksel);
     int *keff = (int *)(w + Ksel);
     if (!hip_ok(coli_launch_router_logits(x_dev, 1, (const float *)rw_dev, D, E, logit, ctx->stream), "router logits") ||
-        !hip_ok(coli_launch_router_select(logit, (const float *)rb_dev, 1, E, Ksel, 1, topp, norm_topk, routed_scale,
+        !hip_ok(coli_launch_router_select(logit, nch, (const float *)rb_dev, 1, E, Ksel, 1, topp, norm_topk, routed_scale,
                                           idx, w, keff, ctx->stream),
                 "router select") ||
         !hip_ok(hipMemcpyAsync(ctx->host_small, idx, (size_t)Ksel * 8 + sizeof(int), hipMemcpyDeviceToHost,

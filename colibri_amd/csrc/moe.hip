@@ -1,6 +1,6 @@
 // moe.hip -- one device-resident MoE layer for decode / verification rows.
 //
-//   x [S, D] --router GEMV--> logits [S, E] --top-K--> idx, w, keff
+//   x [S, D] --router GEMV--> logits [S, E] (column-chunk partials) --top-K--> idx, w, keff
 //            --union (first-seen order)--> per-expert row lists + descriptors
 //            --dual GEMV (gate/up + SwiGLU)--> h [P, RS, I]
 //            --down GEMV--> y [P, RS, D]
@@ -43,10 +43,13 @@ struct ColiHipMoe {
 };
 
 // ---------------------------------------------------------------------------
-// union + descriptor build, one 256-thread block. Thread 0 walks the S*K
-// selections in (s, kk) order and assigns first-seen slots (LDS only, plus
-// fire-and-forget stores of the row lists); the descriptors are then built by
-// all threads in parallel.
+// union + descriptor build, one 256-thread block, all threads in parallel.
+// Selection i = (t, kk) in row-major order is live when kk < keff[t] and its
+// expert is in range. The union lists the experts in first-seen order: a
+// live selection opens a new slot when no earlier live selection names the
+// same expert, and its slot number is the count of such openings before it.
+// Within an expert, rows keep their selection order (pos = earlier live
+// selections of the same expert), so every list is the reference's.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void coli_moe_union(const int *__restrict__ idx, const int *__restrict__ keff,
                                                       int S, int K, int E, int has_shared, int RS,
@@ -54,58 +57,100 @@ __global__ __launch_bounds__(256) void coli_moe_union(const int *__restrict__ id
                                                       ColiProb *__restrict__ pdown, int *__restrict__ uniq,
                                                       int *__restrict__ xrows, int *__restrict__ hrows,
                                                       int *__restrict__ slotrow, int *__restrict__ state) {
-    extern __shared__ int sm[];   // map [E] | cnt [S*K+1] | uq [S*K+1] | sel [S*K] | ke [S]
-    int *map = sm, *cnt = map + E, *uq = cnt + S * K + 1, *sel = uq + S * K + 1, *ke = sel + S * K;
-    __shared__ int s_np, s_nu;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) map[e] = -1;
-    for (int i = threadIdx.x; i < S * K; i += blockDim.x) sel[i] = idx[i];
-    for (int t = threadIdx.x; t < S; t += blockDim.x) ke[t] = keff[t];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int nu = 0;
-        for (int t = 0; t < S; t++)
-            for (int kk = 0; kk < ke[t]; kk++) {
-                int e = sel[t * K + kk];
-                if (e < 0 || e >= E) continue;
-                if (map[e] < 0) {
-                    map[e] = nu;
-                    uq[nu] = e;
-                    cnt[nu] = 0;
-                    nu++;
-                }
-                int j = map[e], pos = cnt[j]++;
-                xrows[j * RS + pos] = t;
-                slotrow[t * K + kk] = j * RS + pos;
-            }
-        int np = nu;
-        if (has_shared) {
-            uq[np] = E;            // the shared expert sits at table row E
-            cnt[np] = S;
-            np++;
+    // sel [n4] | open [n4 + 1] | uq [n4 + 1] | cnt [n4 + 1] | map [E]; n4 = n rounded up to 4
+    // (int4 scans); open[] later holds the per-slot counts, shared expert included
+    extern __shared__ int sm[];
+    const int n = S * K, n4 = (n + 3) & ~3;
+    int *sel = sm, *open = sel + n4, *uq = open + n4 + 1, *cnt = uq + n4 + 1, *map = cnt + n4 + 1;
+    __shared__ int s_nu;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+        int e = -1;
+        if (i < n) {
+            const int t = i / K, kk = i - t * K;
+            const int v = idx[i];
+            if (kk < keff[t] && v >= 0 && v < E) e = v;
         }
-        s_np = np;
-        s_nu = nu;
+        sel[i] = e;
+    }
+    __syncthreads();
+    // pass 1: earlier and total occurrences of this selection's expert
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int e = sel[i];
+        int before = 0, total = 0;
+        if (e >= 0) {
+            for (int j = 0; j < n4; j += 4) {
+                const int4 v = *(const int4 *)(sel + j);
+                const int m0 = v.x == e, m1 = v.y == e, m2 = v.z == e, m3 = v.w == e;
+                total += m0 + m1 + m2 + m3;
+                before += (j < i ? m0 : 0) + (j + 1 < i ? m1 : 0) + (j + 2 < i ? m2 : 0) + (j + 3 < i ? m3 : 0);
+            }
+        }
+        open[i] = e >= 0 && before == 0;
+        cnt[i] = total;       // kept at the opening index until the slot is known
+        slotrow[i] = before;  // position inside the expert's list, finished below
+    }
+    for (int i = n + threadIdx.x; i < n4; i += blockDim.x) open[i] = 0;
+    __syncthreads();
+    // pass 2: slot = openings before this one
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        if (!open[i]) continue;
+        int slot = 0;
+        for (int j = 0; j < n4; j += 4) {
+            const int4 v = *(const int4 *)(open + j);
+            slot += (j < i ? v.x : 0) + (j + 1 < i ? v.y : 0) + (j + 2 < i ? v.z : 0) + (j + 3 < i ? v.w : 0);
+        }
+        map[sel[i]] = slot;
+    }
+    if (threadIdx.x < 64) {   // number of openings, one wave
+        int c = 0;
+        for (int j = threadIdx.x; j < n; j += 64) c += open[j];
+#pragma unroll
+        for (int off = 32; off; off >>= 1) c += __shfl_xor(c, off);
+        if (threadIdx.x == 0) s_nu = c;
+    }
+    __syncthreads();
+    const int nu = s_nu;
+    int *cslot = open;   // open[] is not read past the barrier above: reuse it for per-slot counts
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int e = sel[i];
+        if (e < 0) continue;
+        const int slot = map[e], before = slotrow[i];
+        if (before == 0) {
+            uq[slot] = e;
+            cslot[slot] = cnt[i];
+        }
+        const int row = slot * RS + before;
+        xrows[row] = i / K;
+        slotrow[i] = row;
+    }
+    int np = nu;
+    if (has_shared) {
+        if (threadIdx.x == 0) {
+            uq[nu] = E;            // the shared expert sits at table row E
+            cslot[nu] = S;
+        }
+        np++;
+        for (int t = threadIdx.x; t < S; t += blockDim.x) xrows[nu * RS + t] = t;
+    }
+    if (threadIdx.x == 0) {
         state[0] = np;
         state[1] = np * RS;
         state[2] = nu;
     }
     __syncthreads();
-    const int np = s_np, nu = s_nu;
     for (int j = threadIdx.x; j < np; j += blockDim.x) {
-        int e = uq[j];
+        const int e = uq[j];
         if (j < nu) uniq[j] = e;
         ColiProb d = tab[2 * e], dn = tab[2 * e + 1];
-        d.nrows = dn.nrows = cnt[j];
+        d.nrows = dn.nrows = cslot[j];
         d.xrow_off = dn.xrow_off = j * RS;
         d.out_row0 = dn.out_row0 = j * RS;
         pdual[j] = d;
         pdown[j] = dn;
     }
-    if (has_shared)
-        for (int t = threadIdx.x; t < S; t += blockDim.x) xrows[nu * RS + t] = t;
     for (int r = threadIdx.x; r < np * RS; r += blockDim.x) {
-        int j = r / RS, p = r - j * RS;
-        hrows[r] = p < cnt[j] ? r : -1;
+        const int j = r / RS, p = r - j * RS;
+        hrows[r] = p < cslot[j] ? r : -1;
     }
 }
 
@@ -142,7 +187,7 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
                                    ColiCudaTensor *sg, ColiCudaTensor *su, ColiCudaTensor *sd) {
     if (!out || !cfg || !router_w || !gates || !ups || !downs) return 0;
     const ColiHipMoeConfig c = *cfg;
-    if (c.D < 1 || c.I < 1 || c.E < 1 || c.E > 4096 || c.K < 1 || c.K > 64 || c.K > c.E || c.route_mode < 0 ||
+    if (c.D < 1 || c.I < 1 || c.E < 1 || c.E > 1024 || c.K < 1 || c.K > 64 || c.K > c.E || c.route_mode < 0 ||
         c.route_mode > 2)
         return 0;
     if (c.has_shared && (!sg || !su || !sd)) return 0;
@@ -200,7 +245,7 @@ static int moe_reserve(DevCtx *ctx, ColiHipMoe *m, int S) {
             (void)hipFree(*b);
             *b = nullptr;
         }
-    size_t sizes[] = {(size_t)S * c.E * 4, (size_t)S * c.K * 4, (size_t)P * RS * c.I * 4, (size_t)P * RS * c.D * 4,
+    size_t sizes[] = {(size_t)coli_router_chunks(c.D) * S * c.E * 4, (size_t)S * c.K * 4, (size_t)P * RS * c.I * 4, (size_t)P * RS * c.D * 4,
                       (size_t)S * c.K * 4, (size_t)S * 4, 16, (size_t)c.E * 4, (size_t)P * RS * 4,
                       (size_t)P * RS * 4, (size_t)S * c.K * 4, (size_t)P * sizeof(ColiProb),
                       (size_t)P * sizeof(ColiProb)};
@@ -246,12 +291,13 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
                                       (_Float16 *)fx.lo.p, (int *)fx.exp.p, flags + ord, fx.gen, ctx->zeros.p, st),
                 "moe x fragments") ||
         !hip_ok(coli_launch_router_logits(x_dev, S, m->rw, c.D, c.E, m->logits, st), "moe router logits") ||
-        !hip_ok(coli_launch_router_select(m->logits, m->rb, S, c.E, c.K, c.route_mode, c.topp, c.norm_topk,
+        !hip_ok(coli_launch_router_select(m->logits, coli_router_chunks(c.D), m->rb, S, c.E, c.K, c.route_mode, c.topp,
+                                          c.norm_topk,
                                           c.routed_scale, m->idx, m->wsel, m->keff, st),
                 "moe router select"))
         return 0;
     // 4. union
-    hipLaunchKernelGGL(coli_moe_union, dim3(1), dim3(256), (size_t)(c.E + 3 * S * c.K + 2 + S) * sizeof(int), st, m->idx, m->keff, S, c.K,
+    hipLaunchKernelGGL(coli_moe_union, dim3(1), dim3(256), (size_t)(c.E + 4 * ((S * c.K + 3) & ~3) + 3) * sizeof(int), st, m->idx, m->keff, S, c.K,
                        c.E, c.has_shared, RS, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->hrows, m->slotrow,
                        m->state);
     if (!hip_ok(hipGetLastError(), "moe union")) return 0;

