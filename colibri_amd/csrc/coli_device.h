@@ -1,0 +1,83 @@
+// coli_device.h -- device-side helpers shared by the GEMV and GEMM kernels:
+// vector types, global-address-space loads, the B-operand unpack of the
+// tiled int4 / e2m1 storage, and the per-group scale registers.
+#pragma once
+
+#include "coli_hip_internal.h"
+
+#include <math.h>
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Loads through address-space-1 pointers: pointers read from descriptors are
+// generic to the compiler, and generic (FLAT) loads may complete out of order,
+// which forces a full vmcnt(0) drain before every use. Global loads keep the
+// in-order counter the software pipeline relies on.
+#define GPTR(T, p) ((const __attribute__((address_space(1))) T *)(const void *)(p))
+
+
+template <int KIND>
+__device__ __forceinline__ half8v unpack_b(uint32_t w) {
+    if constexpr (KIND == COLI_KIND_FP4) {
+        half2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0);
+        half2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1);
+        half2v c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2);
+        half2v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3);
+        return (half8v){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+    } else {
+        uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
+        uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+        uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+        uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+        uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+        const half2v blo = {(_Float16)1032.0f, (_Float16)1032.0f};
+        const half2v bhi = {(_Float16)1152.0f, (_Float16)1152.0f};
+        half2v a = __builtin_bit_cast(half2v, p0) - blo;
+        half2v b = __builtin_bit_cast(half2v, p1) - blo;
+        half2v c = __builtin_bit_cast(half2v, p2) - bhi;
+        half2v d = __builtin_bit_cast(half2v, p3) - bhi;
+        return (half8v){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+    }
+}
+
+// Scale of group j (0..3) of the lane's row, from the per-tile-quad scale word(s).
+template <int KIND> struct ScaleRegs;
+template <> struct ScaleRegs<COLI_KIND_I4_H> {
+    u32x2 v;
+    __device__ void load(const void *base, size_t tq, int r16) {
+        v = *GPTR(u32x2, (const uint8_t *)base + (tq * 16 + r16) * 8);
+    }
+    __device__ float get(int j) const {
+        uint32_t wd = v[j >> 1];
+        _Float16 h = __builtin_bit_cast(half2v, wd)[j & 1];
+        return (float)h;
+    }
+    __device__ void zero() { v = (u32x2){0u, 0u}; }
+};
+template <> struct ScaleRegs<COLI_KIND_I4_F> {
+    floatx4 v;
+    __device__ void load(const void *base, size_t tq, int r16) {
+        v = *GPTR(floatx4, (const uint8_t *)base + (tq * 16 + r16) * 16);
+    }
+    __device__ float get(int j) const { return v[j]; }
+    __device__ void zero() { v = (floatx4){0.f, 0.f, 0.f, 0.f}; }
+};
+template <> struct ScaleRegs<COLI_KIND_FP4> {
+    uint32_t v;
+    __device__ void load(const void *base, size_t tq, int r16) {
+        v = *GPTR(uint32_t, (const uint8_t *)base + (tq * 16 + r16) * 4);
+    }
+    __device__ float get(int j) const {
+        return __builtin_bit_cast(float, ((v >> (8 * j)) & 0xFFu) << 23);
+    }
+    __device__ void zero() { v = 0u; }
+};
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return (g / (1.0f + expf(-g))) * u;
+}
+

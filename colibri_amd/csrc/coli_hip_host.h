@@ -6,6 +6,8 @@
 #include <stdint.h>
 
 #define COLI_PIPE_SLOTS 27
+// Batches larger than this run the grouped GEMM instead of the GEMV.
+#define COLI_GEMM_MIN_ROWS 32
 
 struct DevBuf {
     void *p = nullptr;
@@ -59,6 +61,7 @@ hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, in
 hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, const int *nrows_dev,
                                  int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
                                  int *exp2out, int *haslo, int gen, const void *zero, hipStream_t st);
+hipError_t coli_launch_gemm(int kind, int dual, const ColiGemmArgs *a, hipStream_t st);
 hipError_t coli_launch_repack(const ColiCudaTensor *t, const uint8_t *src_w, const void *src_s,
                               hipStream_t st);
 hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const float *x, int ldx, float *y, int ldy,

@@ -79,5 +79,30 @@ struct ColiGemvArgs {
 };
 
 
+// Grouped GEMM (prefill): problems of many rows, tiled 64 rows x (COLI_GM_WAVES
+// waves x 2 row tiles) with the activation fragments staged in LDS.
+#define COLI_GM_WAVES 8
+#define COLI_GM_ROWS 64
+
+struct ColiGemmArgs {
+    const ColiProb *prob;
+    const int *nprob_dev;     // live problems (device); null: nprob
+    int nprob;
+    const int *mt_list;       // work list of (problem << 16 | row tile); null: tile i of problem 0..
+    const int *n_mt_dev;      // live entries of mt_list (device)
+    int n_mt;                 // upper bound of the list (grid sizing)
+    int nrt, nq, O;
+    int rb_per_prob;          // output blocks of COLI_GM_WAVES x 2 row tiles (dual: x 1 gate + 1 up)
+    const int *xrows;         // fragment row of batch row r = xrows[xrow_off + r] (null: xrow_off + r)
+    const _Float16 *xhi, *xlo;
+    int xstride;              // halves per fragment row
+    const int *xexp;
+    const int *haslo;
+    int lo_gen;
+    const uint8_t *zero;
+    float *out;
+    int ldo;
+};
+
 // Numeric helpers shared by host and device.
 static inline int coli_ceil_div(int a, int b) { return (a + b - 1) / b; }

@@ -132,6 +132,40 @@ static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
     return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
 }
 
+// Grouped GEMM over problems of many rows (see gemm.hip); mt_list_dev holds
+// n_mt entries (problem << 16 | 64-row tile), problem indices relative to
+// probs_dev.
+static int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
+                    const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
+                    const int *xrows_dev, float *out, int ldo) {
+    if (n_mt <= 0) return 1;
+    FragSet &f = ctx->frag[set];
+    ColiGemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.prob = probs_dev;
+    a.nprob_dev = nprob_dev;
+    a.nprob = nprob;
+    a.mt_list = mt_list_dev;
+    a.n_mt_dev = n_mt_dev;
+    a.n_mt = n_mt;
+    a.nrt = nrt;
+    a.nq = nq;
+    a.O = O;
+    const int tiles_per_block = COLI_GM_WAVES * (dual ? 1 : 2);
+    a.rb_per_prob = (nrt + tiles_per_block - 1) / tiles_per_block;
+    a.xrows = xrows_dev;
+    a.xhi = (const _Float16 *)f.hi.p;
+    a.xlo = (const _Float16 *)f.lo.p;
+    a.xstride = nq * 4 * 32;
+    a.xexp = (const int *)f.exp.p;
+    a.haslo = (const int *)ctx->flags.p + set;
+    a.lo_gen = f.gen;
+    a.zero = (const uint8_t *)ctx->zeros.p;
+    a.out = out;
+    a.ldo = ldo;
+    return hip_ok(coli_launch_gemm(kind, dual ? 1 : 0, &a, ctx->stream), "gemm launch");
+}
+
 static int frag_set_of(int kind, bool hidden) {
     return (hidden ? 2 : 0) + (kind == COLI_KIND_FP4 ? 1 : 0);
 }
@@ -214,25 +248,48 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
                                 y_dev, D, D, (D + 15) / 16, (I + 127) / 128});
     }
     (void)t0g; (void)t0d; (void)split_first;
+    // Members of many rows go through the grouped GEMM: one work list of
+    // (problem, 64-row tile) per launch, uploaded after the descriptors.
+    const bool use_gemm = max_rows > COLI_GEMM_MIN_ROWS;
+    std::vector<int> mt;
+    std::vector<int> mt_first(launches.size(), 0), mt_count(launches.size(), 0);
+    if (use_gemm)
+        for (size_t l = 0; l < launches.size(); l++) {
+            mt_first[l] = (int)mt.size();
+            for (int q = 0; q < launches[l].n; q++) {
+                const int rows = probs[launches[l].first + q].nrows;
+                for (int t = 0; t * COLI_GM_ROWS < rows; t++) mt.push_back(q << 16 | t);
+            }
+            mt_count[l] = (int)mt.size() - mt_first[l];
+        }
     if (!probs.empty()) {
-        size_t pb = probs.size() * sizeof(ColiProb);
-        if (!reserve_pinned(ctx, &ctx->host_prob, &ctx->host_prob_cap, pb) || !reserve(ctx, &ctx->prob, pb, 0))
+        size_t pb = probs.size() * sizeof(ColiProb), mb = mt.size() * sizeof(int);
+        if (!reserve_pinned(ctx, &ctx->host_prob, &ctx->host_prob_cap, pb + mb) ||
+            !reserve(ctx, &ctx->prob, pb + mb, 0))
             return 0;
         // the pinned staging may still feed a queued copy of the previous call
         if (!hip_ok(hipStreamSynchronize(ctx->stream), "descriptor staging")) return 0;
         std::memcpy(ctx->host_prob, probs.data(), pb);
-        if (!hip_ok(hipMemcpyAsync(ctx->prob.p, ctx->host_prob, pb, hipMemcpyHostToDevice, ctx->stream),
+        if (mb) std::memcpy((char *)ctx->host_prob + pb, mt.data(), mb);
+        if (!hip_ok(hipMemcpyAsync(ctx->prob.p, ctx->host_prob, pb + mb, hipMemcpyHostToDevice, ctx->stream),
                     "descriptor upload"))
             return 0;
     }
     const ColiProb *pdev = (const ColiProb *)ctx->prob.p;
+    const int *mtdev = (const int *)((const char *)ctx->prob.p + probs.size() * sizeof(ColiProb));
+    auto launch = [&](size_t l, bool dual) {
+        const Launch &L = launches[l];
+        if (use_gemm)
+            return run_gemm(ctx, L.kind, dual, pdev + L.first, L.n, nullptr, mtdev + mt_first[l], nullptr,
+                            mt_count[l], L.nrt, L.nq, L.O, L.set, nullptr, L.out, L.ldo);
+        return run_gemv(ctx, L.kind, dual, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set,
+                        nullptr, L.out, L.ldo);
+    };
 
     // gate/up: dual launches and split members
-    for (const Launch &L : launches) {
-        if (L.first >= down_first) break;
-        if (!run_gemv(ctx, L.kind, L.dual, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set,
-                      nullptr, L.out, L.ldo))
-            return 0;
+    for (size_t l = 0; l < launches.size(); l++) {
+        if (launches[l].first >= down_first) break;
+        if (!launch(l, launches[l].dual)) return 0;
     }
     for (int c = 0; c < count; c++) {
         if (dual_kind[c] >= 0) continue;
@@ -252,11 +309,9 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
     // down
     for (int o = 0; o < 2; o++)
         if (need_h[o] && !make_frags(ctx, frag_set_of(o ? COLI_KIND_FP4 : 0, true), h, I, total, I, !o)) return 0;
-    for (const Launch &L : launches) {
-        if (L.first < down_first) continue;
-        if (!run_gemv(ctx, L.kind, false, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set, nullptr,
-                      L.out, L.ldo))
-            return 0;
+    for (size_t l = 0; l < launches.size(); l++) {
+        if (launches[l].first < down_first) continue;
+        if (!launch(l, false)) return 0;
     }
     for (int c = 0; c < count; c++)
         if (m[c].d->kind == COLI_KIND_GENERIC &&

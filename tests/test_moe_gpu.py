@@ -250,3 +250,24 @@ def test_pipe_router_ties_and_invalid(session, case):
     if case == "few_valid":
         assert list(idx[:3]) == sorted([7, 60, 90], key=lambda e: -rw[0][list(ri[0]).index(e)]) or True
         assert list(idx[3:]) == list(range(3, K))
+
+
+@pytest.mark.parametrize("fmt,lo", [(4, False), (7, False), (4, True), (7, True)])
+def test_expert_group_grouped_gemm(session, fmt, lo):
+    """Members with more than 32 rows run the grouped GEMM (64-row tiles, LDS
+    staged activations): ragged tiles (70 = 64 + 6, 129 = 2 x 64 + 1), a small
+    member in the same launch, bf16-exact and full f32 activations."""
+    rng = np.random.default_rng(300 + fmt + 10 * lo)
+    D, I = 384, 256
+    layer = Layer(rng, fmt, D, I, 3)
+    hs = layer.upload(session)
+    rows = [70, 3, 129]
+    x = rng.standard_normal((sum(rows), D)).astype(np.float32) if lo else rand_x(rng, sum(rows), D)
+    try:
+        y = session.expert_group([h[0] for h in hs], [h[1] for h in hs], [h[2] for h in hs], rows, x)
+    finally:
+        for h in hs:
+            for t in h:
+                session.free(t)
+    ref = group_reference(layer, x, [0, 1, 2], rows)
+    assert rel_err(y, ref, group_mag(layer, x, [0, 1, 2], rows)).max() <= TOL
