@@ -91,3 +91,19 @@ struct GemvLaunchPlan {
     int R, W, rbpp, splits, qps;
 };
 GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual, int max_rows);
+
+// Activation fragments of rows x[0..nrows) (or src_rows[r]; nrows_dev: live
+// count on the device) of width K into fragment set `set` (0/1: inputs of the
+// int4 / fp4 order, 2/3: hidden rows).
+int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
+               const int *src_rows = nullptr, const int *nrows_dev = nullptr);
+int frag_set_of(int kind, bool hidden);
+// One tiled GEMV over `nprob` problems (descriptors on the device, or one
+// inline problem) reading fragment set `set`.
+int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
+             int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
+             const ColiProb *inline_prob = nullptr);
+// One grouped GEMM over a device work list of (problem << 16 | 64-row tile).
+int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
+             const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
+             const int *xrows_dev, float *out, int ldo);

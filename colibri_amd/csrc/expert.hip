@@ -74,8 +74,8 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
 static int ngp_of(int K) { return (K + 127) / 128 * 4; }
 
 // Fragments of rows x[0..nrows) (or src_rows[r]) of width K into set `set`.
-static int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
-                      const int *src_rows = nullptr, const int *nrows_dev = nullptr) {
+int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
+               const int *src_rows, const int *nrows_dev) {
     FragSet &f = ctx->frag[set];
     int ngp = ngp_of(K);
     size_t halves = (size_t)nrows * ngp * 32;
@@ -92,9 +92,9 @@ static int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, i
 }
 
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
-static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob,
-                    const int *nprob_dev, int nrt, int nq, int O, int max_rows, int set,
-                    const int *xrows_dev, float *out, int ldo, const ColiProb *inline_prob = nullptr) {
+int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
+             int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
+             const ColiProb *inline_prob) {
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
     GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
@@ -135,9 +135,9 @@ static int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
 // Grouped GEMM over problems of many rows (see gemm.hip); mt_list_dev holds
 // n_mt entries (problem << 16 | 64-row tile), problem indices relative to
 // probs_dev.
-static int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
-                    const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
-                    const int *xrows_dev, float *out, int ldo) {
+int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
+             const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
+             const int *xrows_dev, float *out, int ldo) {
     if (n_mt <= 0) return 1;
     FragSet &f = ctx->frag[set];
     ColiGemmArgs a;
@@ -166,7 +166,7 @@ static int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev,
     return hip_ok(coli_launch_gemm(kind, dual ? 1 : 0, &a, ctx->stream), "gemm launch");
 }
 
-static int frag_set_of(int kind, bool hidden) {
+int frag_set_of(int kind, bool hidden) {
     return (hidden ? 2 : 0) + (kind == COLI_KIND_FP4 ? 1 : 0);
 }
 

@@ -69,9 +69,11 @@ int coli_hip_moe_create(ColiHipMoe **moe, int device, const ColiHipMoeConfig *cf
                         ColiCudaTensor *shared_up, ColiCudaTensor *shared_down);
 void coli_hip_moe_free(ColiHipMoe *moe);
 
-/* Device-resident forward of S <= 16 decode rows: x_dev [S, D] f32 ->
- * out_dev [S, D] f32, asynchronous on the backend stream (no host sync, no
- * allocation after the first call at a given S). */
+/* Device-resident forward of S <= 2048 rows (decode, verification or
+ * prefill; S * K <= 16384): x_dev [S, D] f32 -> out_dev [S, D] f32,
+ * asynchronous on the backend stream (no host sync, no allocation after the
+ * first call at a given S). Up to 32 rows the experts run the tiled GEMV,
+ * beyond it the grouped GEMM. */
 int coli_hip_moe_forward_dev(ColiHipMoe *moe, const float *x_dev, float *out_dev, int S);
 
 /* Host forward with routing read back: idx/w [S, K], keff [S] (may be NULL). */

@@ -173,7 +173,8 @@ def make_moe(session, layer, W, b, K, mode, norm_topk=0, topp=0.0, routed_scale=
 
 
 @pytest.mark.parametrize("fmt,mode,S,shared", [(4, 0, 1, False), (4, 0, 5, False), (7, 2, 1, True),
-                                               (7, 2, 16, True), (4, 1, 21, False), (7, 1, 3, False)])
+                                               (7, 2, 16, True), (4, 1, 21, False), (7, 1, 3, False),
+                                               (4, 1, 80, True), (7, 2, 150, False)])
 def test_moe_layer(session, fmt, mode, S, shared):
     rng = np.random.default_rng(100 + fmt * 10 + mode + S)
     D, I, E, K = 512, 256, 32, 4
