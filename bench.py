@@ -243,7 +243,15 @@ class Bench:
                 "ms_per_step": round(dt / reps * 1e3, 2)}
 
     # -- fused MoE layer ------------------------------
-    def moe(self, name, fmt, D, I, E, K, mode, shared, batches, layers_for_anticache, bias, zipf=None):
+    def moe(self, name, fmt, D, I, E, K, mode, shared, batches, layers_for_anticache, bias, zipf=None,
+            per_token=False, steps=None, w_std=0.02):
+        """One fused MoE layer (router -> union -> experts -> SwiGLU -> combine)
+        timed over `steps` calls per batch size, replayed from a captured graph.
+        per_token: each step runs the B rows as B separate 1-row layers (the
+        per-token GEMV alternative to the union GEMM). zipf: selection bias
+        -(zipf / 11) * ln(1 + e) on top of sigmoid scores of logits ~N(0, 1):
+        for zipf = 1.1 and 512 tokens about 150 of 384 experts are touched and
+        the head expert takes ~300 rows (skewed, Zipf-like loads)."""
         from colibri_amd.backend import ColiHipMoeConfig, f32p, tensor_array
         b, hrt = self.b, self.hiprt
         sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -267,8 +275,11 @@ class Bench:
                         e8 = self.rng.integers(119, 124, (O, II // 32), dtype=np.uint8)
                         trip.append(self.tensor_fp4(stage, O, II, e8, seed))
                 hs.append(trip)
-            W = (self.rng.standard_normal((E, D)) * 0.02).astype(np.float32)
-            bvec = (self.rng.standard_normal(E) * 0.01).astype(np.float32) if bias else None
+            W = (self.rng.standard_normal((E, D)) * w_std).astype(np.float32)
+            if zipf is not None:
+                bvec = (-zipf / 11.0 * np.log1p(np.arange(E))).astype(np.float32)
+            else:
+                bvec = (self.rng.standard_normal(E) * 0.01).astype(np.float32) if bias else None
             routed = hs[:E]
             sh = hs[E] if shared else [None, None, None]
             g, ga = tensor_array([t[0] for t in routed])
@@ -276,32 +287,46 @@ class Bench:
             d, da = tensor_array([t[2] for t in routed])
             cfg = ColiHipMoeConfig(D, I, E, K, mode, 0, 0.0, 1.0, 1 if shared else 0)
             m = C.c_void_p()
-            if not b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(W), f32p(bvec) if bias else None,
+            if not b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(W), f32p(bvec) if bvec is not None else None,
                                     g, u, d, sh[0], sh[1], sh[2]):
                 raise RuntimeError("moe_create failed")
             layers.append((m, hs, W, bvec))
-        npool = 64
+        npool = max(64, max(batches))
         xpool = bf16_exact(self.rng.standard_normal((npool, D)).astype(np.float32))
         xd = self.put(xpool)
-        od = self.alloc(64 * D * 4)
+        od = self.alloc(npool * D * 4)
         result = {}
         for B in batches:
-            steps = self.args.moe_steps
-            # unique experts per call, from the reference router on the same inputs
-            nus = []
-            for k in range(steps):
+            n_steps = steps or self.args.moe_steps
+            # unique experts (and rows per expert) per call, from the reference
+            # router on the same inputs
+            nus, loads = [], []
+            for k in range(n_steps):
                 L = k % n_layers
-                rows = [(k * B + r) % npool for r in range(B)]
-                xb = np.ascontiguousarray(xpool[rows])
+                r0 = (k * B) % npool
+                if r0 + B > npool:
+                    r0 = 0
+                xb = np.ascontiguousarray(xpool[r0:r0 + B])
                 W, bvec = layers[L][2], layers[L][3]
                 idx, _, keff = cref.route(cref.matmul_f32(xb, W), K, mode, bias=bvec)
-                nus.append(len({int(e) for s in range(B) for e in idx[s, :keff[s]]}) + (1 if shared else 0))
+                sel = [int(e) for s_ in range(B) for e in idx[s_, :keff[s_]]]
+                if per_token:
+                    nus.append(B * (K + (1 if shared else 0)))
+                else:
+                    nus.append(len(set(sel)) + (1 if shared else 0))
+                loads.append(np.bincount(np.array(sel), minlength=E))
+
             def call(k):
                 L = k % n_layers
                 r0 = (k * B) % npool
                 if r0 + B > npool:
                     r0 = 0
-                if not b.hip_moe_forward_dev(layers[L][0], C.c_void_p(xd + r0 * D * 4), od, B):
+                if per_token:
+                    for r in range(B):
+                        if not b.hip_moe_forward_dev(layers[L][0], C.c_void_p(xd + (r0 + r) * D * 4),
+                                                     C.c_void_p(od + r * D * 4), 1):
+                            raise RuntimeError("moe forward failed")
+                elif not b.hip_moe_forward_dev(layers[L][0], C.c_void_p(xd + r0 * D * 4), od, B):
                     raise RuntimeError("moe forward failed")
 
             for k in range(max(self.args.warmup, n_layers)):   # every layer sized before capture
@@ -309,7 +334,7 @@ class Bench:
             hrt.device_sync()
             # timed layers replayed from one captured graph (see dense())
             with hrt.Graph(self.stream) as graph:
-                for k in range(steps):
+                for k in range(n_steps):
                     call(k)
             graph.launch()
             hrt.device_sync()
@@ -323,12 +348,18 @@ class Bench:
             gpu_ms = e0.elapsed_ms(e1)
             router = E * D * 4
             byts = np.array([nu * per_expert + router + 2 * B * D * 2 for nu in nus], np.float64)
-            result[f"B{B}"] = {"tokens_per_s": round(B * steps / wall, 1),
-                               "layer_us": round(gpu_ms / steps * 1e3, 2),
-                               "layer_us_wall": round(wall / steps * 1e6, 2),
-                               "avg_unique_experts": round(float(np.mean(nus)), 2),
-                               "GBs": round(byts.sum() / gpu_ms / 1e6, 1),
-                               "frac_of_peak": round(byts.sum() / gpu_ms / 1e6 / PEAK_GBS, 3)}
+            rec = {"tokens_per_s": round(B * n_steps / wall, 1),
+                   "layer_us": round(gpu_ms / n_steps * 1e3, 2),
+                   "layer_us_wall": round(wall / n_steps * 1e6, 2),
+                   "avg_unique_experts": round(float(np.mean(nus)), 2),
+                   "GBs": round(byts.sum() / gpu_ms / 1e6, 1),
+                   "frac_of_peak": round(byts.sum() / gpu_ms / 1e6 / PEAK_GBS, 3)}
+            if B >= 64:
+                flops = 2.0 * 3 * D * I * (B * K + (B if shared else 0))
+                rec["max_rows_per_expert"] = int(max(int(l.max()) for l in loads))
+                rec["mfma_TFLOPs"] = round(flops * n_steps / gpu_ms / 1e9, 1)
+                rec["mfma_frac_of_fp16_peak"] = round(flops * n_steps / gpu_ms / 1e9 / 2500.0, 4)
+            result[f"B{B}" + ("_per_token" if per_token else "")] = rec
         for (m, hs, W, bvec) in layers:
             b.hip_moe_free(m)
             for trip in hs:
@@ -407,6 +438,21 @@ def main():
             "configs[0]_olmoe_int4": bench.moe("olmoe", 4, 2048, 1024, 64, 8, 0, False, (1,), 10, False),
             "configs[2]_dsv3_mxfp4": bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 16), 1, True),
         }
+        # one verification step of 21 rows (16-node tree + 5-token
+        # draft) on the configs[2] layer shape, union GEMM vs 21 per-token passes
+        ver = {}
+        for fmt, tag in ((7, "mxfp4"), (4, "int4")):
+            r = bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True, steps=20)
+            r.update({k + "": v for k, v in bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True,
+                                                          steps=5, per_token=True).items() if k.startswith("B")})
+            ver[tag] = r
+        out["moe_layer"]["configs[3]_verification_21rows"] = ver
+        # Kimi-shaped prefill chunk, 512 tokens, 384 experts top-8,
+        # router logits ~N(0,1) with a Zipf(1.1) selection bias
+        out["moe_layer"]["configs[4]_kimi_prefill_512"] = {
+            tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+                           w_std=1.0 / math.sqrt(7168))
+            for fmt, tag in ((7, "mxfp4"), (4, "int4"))}
     if not args.skip_cpu:
         out["cpu_baseline"] = bench.cpu_baseline()
     bench.close()

@@ -10,6 +10,8 @@
 #include "coli_hip_ext.h"
 #include "coli_hip_host.h"
 
+#include <rocblas/rocblas.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -155,6 +157,7 @@ extern "C" void coli_cuda_shutdown(void) {
         if (ctx->host_prob) (void)hipHostFree(ctx->host_prob);
         if (ctx->host_small) (void)hipHostFree(ctx->host_small);
         if (ctx->ev_ok) (void)hipEventDestroy(ctx->ev_done);
+        if (ctx->blas) (void)rocblas_destroy_handle((rocblas_handle)ctx->blas);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         *ctx = DevCtx();
     }

@@ -34,6 +34,7 @@ struct DevCtx {
     void *host_x = nullptr, *host_y = nullptr, *host_prob = nullptr, *host_small = nullptr;
     size_t host_x_cap = 0, host_y_cap = 0, host_prob_cap = 0, host_small_cap = 0;
     int group_pending = 0;
+    void *blas = nullptr;              // rocblas_handle, created on first use
     hipEvent_t ev_done = nullptr;
     int ev_ok = 0;
     // statistics
@@ -107,3 +108,8 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
              const int *xrows_dev, float *out, int ldo);
+
+// Router logits of S rows into `part`; returns the number of column-chunk
+// partials the selection must add (1 when the batch went through one GEMM),
+// or 0 on failure.
+int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int E, float *part);

@@ -8,6 +8,8 @@
 // 1677-1812 for issue/take).
 #include "coli_hip_host.h"
 
+#include <rocblas/rocblas.h>
+
 #include "coli_backend_abi.h"
 #include "coli_hip_ext.h"
 
@@ -651,6 +653,35 @@ extern "C" int coli_cuda_expert_group_resident_take(int home_device, const int *
         if (!hip_ok(hipStreamWaitEvent(home->stream, src->ev_done, 0), "resident take wait")) return 0;
     }
     return hip_ok(coli_launch_sum_slots(acc_dev, slots_dev, n_issued, D, home->stream), "resident take reduce");
+}
+
+// ---------------------------------------------------------------------------
+// Router logits. Decode batches (<= 16 rows) use the chunked partial kernel
+// (pipe.hip); larger batches are a plain f32 GEMM, logits[S, E] = x W^T,
+// which rocBLAS runs on the backend stream (col-major: C(E x S) = W^T(E x D)
+// x^T... i.e. op(A) = A^T with A = W as a D x E col-major matrix).
+// ---------------------------------------------------------------------------
+int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int E, float *part) {
+    if (S <= 16)
+        return hip_ok(coli_launch_router_logits(x, S, W, D, E, part, ctx->stream), "router logits")
+                   ? coli_router_chunks(D)
+                   : 0;
+    rocblas_handle h = (rocblas_handle)ctx->blas;
+    if (!h) {
+        if (rocblas_create_handle(&h) != rocblas_status_success) {
+            std::fprintf(stderr, "[HIP] rocblas handle creation failed\n");
+            return 0;
+        }
+        ctx->blas = h;
+    }
+    const float one = 1.0f, zero = 0.0f;
+    if (rocblas_set_stream(h, ctx->stream) != rocblas_status_success ||
+        rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, E, S, D, &one, W, D, x, D, &zero, part,
+                      E) != rocblas_status_success) {
+        std::fprintf(stderr, "[HIP] router sgemm failed\n");
+        return 0;
+    }
+    return 1;
 }
 
 // ---------------------------------------------------------------------------

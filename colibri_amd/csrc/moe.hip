@@ -268,11 +268,11 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     const int int4 = m->kind != COLI_KIND_FP4;
     hipStream_t st = ctx->stream;
     // 1. activation fragments, 2-3. router
-    if (!make_frags(ctx, fx, x_dev, c.D, S, c.D, int4) ||
-        !hip_ok(coli_launch_router_logits(x_dev, S, m->rw, c.D, c.E, m->logits, st), "moe router logits") ||
-        !hip_ok(coli_launch_router_select(m->logits, coli_router_chunks(c.D), m->rb, S, c.E, c.K, c.route_mode,
-                                          c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, st),
-                "moe router select"))
+    if (!make_frags(ctx, fx, x_dev, c.D, S, c.D, int4)) return 0;
+    const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
+    if (!nch || !hip_ok(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
+                                                  c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, st),
+                        "moe router select"))
         return 0;
     // 4. union
     const size_t ush = (size_t)(7 * c.E + 5) * sizeof(int);
