@@ -144,7 +144,8 @@ extern "C" void coli_cuda_shutdown(void) {
         (void)hipStreamSynchronize(ctx->stream);
         DevBuf *bufs[] = {&ctx->x, &ctx->h, &ctx->y, &ctx->g, &ctx->u, &ctx->partial,
                           &ctx->prob, &ctx->stage_w, &ctx->stage_s, &ctx->qdq, &ctx->flags,
-                          &ctx->rslot, &ctx->rw, &ctx->tmp_tiles, &ctx->tmp_scales, &ctx->zeros};
+                          &ctx->rslot, &ctx->rw, &ctx->tmp_tiles, &ctx->tmp_scales, &ctx->zeros,
+                          &ctx->split_cnt};
         for (DevBuf *b : bufs) free_buf(b);
         for (int f = 0; f < 4; f++) {
             free_buf(&ctx->frag[f].hi);

@@ -19,6 +19,29 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // in-order counter the software pipeline relies on.
 #define GPTR(T, p) ((const __attribute__((address_space(1))) T *)(const void *)(p))
 
+// A pointer every lane of the wave holds, moved to scalar registers (values
+// read from memory by a vector load otherwise stay in VGPRs, and so would all
+// address arithmetic derived from them).
+__device__ __forceinline__ const uint8_t *uniform_ptr(const void *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const uint8_t *)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ ColiProb uniform_prob(const ColiProb &p) {
+    ColiProb u;
+    u.w0 = uniform_ptr(p.w0);
+    u.s0 = uniform_ptr(p.s0);
+    u.w1 = uniform_ptr(p.w1);
+    u.s1 = uniform_ptr(p.s1);
+    u.nrows = __builtin_amdgcn_readfirstlane(p.nrows);
+    u.xrow_off = __builtin_amdgcn_readfirstlane(p.xrow_off);
+    u.out_row0 = __builtin_amdgcn_readfirstlane(p.out_row0);
+    u.pad = 0;
+    return u;
+}
+
 
 template <int KIND>
 __device__ __forceinline__ half8v unpack_b(uint32_t w) {
@@ -47,6 +70,7 @@ __device__ __forceinline__ half8v unpack_b(uint32_t w) {
 // Scale of group j (0..3) of the lane's row, from the per-tile-quad scale word(s).
 template <int KIND> struct ScaleRegs;
 template <> struct ScaleRegs<COLI_KIND_I4_H> {
+    static constexpr int kTileBytes = 16 * 8;
     u32x2 v;
     __device__ void load(const void *base, size_t tq, int r16) {
         v = *GPTR(u32x2, (const uint8_t *)base + (tq * 16 + r16) * 8);
@@ -59,6 +83,7 @@ template <> struct ScaleRegs<COLI_KIND_I4_H> {
     __device__ void zero() { v = (u32x2){0u, 0u}; }
 };
 template <> struct ScaleRegs<COLI_KIND_I4_F> {
+    static constexpr int kTileBytes = 16 * 16;
     floatx4 v;
     __device__ void load(const void *base, size_t tq, int r16) {
         v = *GPTR(floatx4, (const uint8_t *)base + (tq * 16 + r16) * 16);
@@ -67,6 +92,7 @@ template <> struct ScaleRegs<COLI_KIND_I4_F> {
     __device__ void zero() { v = (floatx4){0.f, 0.f, 0.f, 0.f}; }
 };
 template <> struct ScaleRegs<COLI_KIND_FP4> {
+    static constexpr int kTileBytes = 16 * 4;
     uint32_t v;
     __device__ void load(const void *base, size_t tq, int r16) {
         v = *GPTR(uint32_t, (const uint8_t *)base + (tq * 16 + r16) * 4);

@@ -27,7 +27,7 @@ struct DevCtx {
     size_t tensor_count = 0, tensor_bytes = 0;
     // grow-only scratch
     DevBuf x, h, y, g, u, partial, prob, zeros, stage_w, stage_s, qdq, flags;
-    DevBuf rslot, rw, tmp_tiles, tmp_scales;
+    DevBuf rslot, rw, tmp_tiles, tmp_scales, split_cnt;
     FragSet frag[4];                   // 0/1: inputs (int4 / fp4 order), 2/3: hidden rows
     DevBuf pipe[COLI_PIPE_SLOTS];
     // pinned staging

@@ -76,6 +76,7 @@ struct ColiGemvArgs {
     float *out;
     int ldo;
     float *partial;           // split-K partials: [instance][split][R][NB4][64]
+    int *split_cnt;           // split-K arrival counters, one per instance; zero between launches
 };
 
 

@@ -29,7 +29,7 @@
 //    fragment load feeds four tiles. Narrow matrices fall back to 2 or 1.
 //  * K is split across the W waves of a group (LDS reduction) and, when the
 //    rows alone cannot fill the chip with ~12 waves per CU, across groups
-//    (partials reduced in split order by a second kernel).
+//    (partials summed in split order by the last group to arrive).
 //  * Every wave keeps at least 2 quads.
 GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual, int max_rows) {
     (void)max_rows;
@@ -46,7 +46,7 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
     long groups = (long)nprob * n_bt * p.rbpp;
     p.W = 4;
     if (groups * 4 < target_waves && nq >= 16) p.W = 8;
-    // K splits cost a partial round trip and a second launch: only worth it
+    // K splits cost a partial round trip and a serial tail: only worth it
     // when the row tiles alone leave the chip under 4 waves per CU (long-K,
     // narrow-O shapes such as a dense down projection).
     p.splits = 1;
@@ -101,7 +101,8 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     int n_bt = (max_rows + 15) / 16;
     GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
     size_t inst = (size_t)nprob * n_bt * pl.rbpp;
-    if (pl.splits > 1 && !reserve(ctx, &ctx->partial, inst * pl.splits * pl.R * 4 * 64 * sizeof(float), 0))
+    if (pl.splits > 1 && (!reserve(ctx, &ctx->partial, inst * pl.splits * pl.R * 4 * 64 * sizeof(float), 0) ||
+                          !reserve(ctx, &ctx->split_cnt, inst * sizeof(int), 1)))
         return 0;
     FragSet &f = ctx->frag[set];
     ColiGemvArgs a;
@@ -131,6 +132,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.out = out;
     a.ldo = ldo;
     a.partial = (float *)ctx->partial.p;
+    a.split_cnt = (int *)ctx->split_cnt.p;
     return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
 }
 

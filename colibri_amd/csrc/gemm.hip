@@ -30,7 +30,9 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
     constexpr int PD = 3;
     constexpr int BUF = 32768;           // one staging buffer: hi 16 KiB + lo 16 KiB
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // readfirstlane: the wave index is wave-uniform, so everything derived from it
+    // (tile indices, validity, base pointers) stays in scalar registers.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
     const int item = blockIdx.x / a.rb_per_prob, rb = blockIdx.x - item * a.rb_per_prob;
     if (a.n_mt_dev && item >= *a.n_mt_dev) return;
@@ -38,7 +40,7 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
     const int tag = a.mt_list[item];
     const int p = tag >> 16, mt = tag & 0xffff;
     if (p >= a.nprob || (a.nprob_dev && p >= *a.nprob_dev)) return;
-    const ColiProb pr = a.prob[p];
+    const ColiProb pr = uniform_prob(a.prob[p]);
     const int m0 = mt * COLI_GM_ROWS;
     const int nrows = min(COLI_GM_ROWS, pr.nrows - m0);
     if (nrows <= 0) return;

@@ -22,8 +22,8 @@
 //    every lo part is zero (bf16-exact inputs).
 //  * K is split across the waves of a workgroup (LDS reduction in fixed wave
 //    order) and, for shapes whose rows cannot fill the chip, across
-//    workgroups (partials summed in split order by a second kernel; no
-//    device-scope fences, no atomics on the data), then fused epilogues:
+//    workgroups (the last group to arrive sums the partials in split order;
+//    one launch, no atomics on the data), then fused epilogues:
 //    plain store, or SwiGLU (silu(g)*u, the expression of
 //    c/backend_cuda.cu:618-624) for gate/up pairs. Results are bitwise
 //    reproducible run to run.
@@ -218,53 +218,58 @@ struct Stage {
 #define COLI_PD 2
 #endif
 
+// Scalar-register addressing of the R row tiles one wave accumulates: every
+// load below is a wave-uniform base (SGPRs) plus the lane's fixed byte offset
+// (VGPR), so the per-iteration address work is scalar.
+template <int KIND, int R>
+struct TileRows {
+    const uint8_t *w[R];   // quad 0 of the row tile, or the zero tile (dead row tile)
+    const uint8_t *s[R];   // its scale block, or zeros
+    int qstep[R];          // 1 for a live row tile, 0 for a dead one
+};
+
 // Main loop of one wave over its quads q = q_first + it*W, it < nit.
 // A ring of PD stages: the loads of iteration it+PD-1 are issued (as one
 // branch-free batch) before the math of iteration it, so up to PD-1 stages
-// stay in flight while the wave computes. Iterations past the end read the
-// zero buffer instead (their math is skipped), which keeps every load
-// unconditional and the in-order vmcnt accounting exact.
+// stay in flight while the wave computes. Iterations past the end re-read
+// the wave's last quad (an L2 hit; their math is skipped), which keeps every
+// load unconditional and the in-order vmcnt accounting exact.
 template <int KIND, int R>
-__device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, bool valid, int q, const size_t (&tbase)[R],
-                                             const int (&tstep)[R], const uint8_t *const (&wb)[R],
-                                             const void *const (&sb)[R], const _Float16 *zero, int lane) {
+__device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, int q, const TileRows<KIND, R> &rows,
+                                             int lane) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        size_t tq = valid ? tbase[r] + (size_t)q * tstep[r] : 0;
-        const uint8_t *w = valid ? wb[r] : (const uint8_t *)zero;
-        const void *sp = valid ? sb[r] : (const void *)zero;
-        sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + tq * COLI_TILE_BYTES) + lane);
-        sg.sc[r].load(sp, tq, lane & 15);
+        const int qq = q * rows.qstep[r];
+        sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, rows.w[r] + (size_t)qq * COLI_TILE_BYTES) + lane);
+        sg.sc[r].load(rows.s[r], (size_t)qq, lane & 15);
     }
 }
 
-// The caller has already issued the weight/scale loads of iteration 0 into
-// st[0] (before it knew the activation rows), so the first HBM requests
-// leave the CU as early as possible.
+// The caller has already issued the weight/scale loads and the hi fragments
+// of iteration 0 into st[0] (before it knew whether lo fragments exist), so
+// the first requests leave the CU as early as possible. xoff = the lane's
+// byte offset of its fragment row and k-slice inside xh / xl.
 template <int KIND, int R, int NB4, int W, bool LO>
 __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, true> (&st)[COLI_PD], int q_first, int Q1,
-                                           const size_t (&tbase)[R], const int (&tstep)[R],
-                                           const uint8_t *const (&wb)[R], const void *const (&sb)[R],
-                                           const _Float16 *xh, const _Float16 *xl, const _Float16 *zero, int lane) {
+                                           const TileRows<KIND, R> &rows, const uint8_t *xh, const uint8_t *xl,
+                                           uint32_t xoff, int lane) {
     constexpr int PD = COLI_PD;
     if (q_first >= Q1) return;
     const int nit = (Q1 - q_first + W - 1) / W;
-    auto load_x = [&](Stage<KIND, R, true> &sg, int it) {
-        const bool valid = it < nit;
-        const int q = q_first + it * W;
+    const int q_last = q_first + (nit - 1) * W;
+    auto qof = [&](int it) { return it < nit ? q_first + it * W : q_last; };
+    auto load_x = [&](Stage<KIND, R, true> &sg, int q) {
+        const uint8_t *qh = xh + (size_t)q * 256, *ql = xl + (size_t)q * 256;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const _Float16 *ph = valid ? xh + (size_t)(4 * q + j) * 32 : zero;
-            sg.xh[j] = *GPTR(half8v, ph);
-            if constexpr (LO) {
-                const _Float16 *pl = valid ? xl + (size_t)(4 * q + j) * 32 : zero;
-                sg.xl[j] = *GPTR(half8v, pl);
-            }
+            sg.xh[j] = *GPTR(half8v, qh + xoff + j * 64);
+            if constexpr (LO) sg.xl[j] = *GPTR(half8v, ql + xoff + j * 64);
         }
     };
     auto load = [&](Stage<KIND, R, true> &sg, int it) {
-        load_weights<KIND, R>(sg, it < nit, q_first + it * W, tbase, tstep, wb, sb, zero, lane);
-        load_x(sg, it);
+        const int q = qof(it);
+        load_weights<KIND, R>(sg, q, rows, lane);
+        load_x(sg, q);
     };
     auto compute = [&](const Stage<KIND, R, true> &sg) {
 #pragma unroll
@@ -280,7 +285,11 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
             }
         }
     };
-    load_x(st[0], 0);
+    if constexpr (LO) {
+        const uint8_t *ql = xl + (size_t)q_first * 256;
+#pragma unroll
+        for (int j = 0; j < 4; j++) st[0].xl[j] = *GPTR(half8v, ql + xoff + j * 64);
+    }
 #pragma unroll
     for (int p = 1; p < PD - 1; p++) load(st[p], p);
     for (int it0 = 0; it0 < nit; it0 += PD) {
@@ -329,61 +338,82 @@ __device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiP
 // per lane that can hold real batch rows (1, 2 or 4): the MFMA result row of
 // lane l, register i is batch row 4*(l/16)+i, its column is output row
 // 16*tile + (l%16).
-template <int KIND, int R, bool DUAL, int NB4, int W>
+// INL: the single problem a.prob0 (a.prob null, a.nprob 1, a.nprob_dev null):
+// no check precedes the first weight loads, so the kernel arguments arrive
+// as one batch of scalar loads and the HBM requests follow at once (early
+// exits split the scalar loads into dependent round trips).
+template <int KIND, int R, bool DUAL, int NB4, int W, bool INL>
 __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     constexpr int RT = DUAL ? R / 2 : R;
     __shared__ float red[W][R * NB4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int item = blockIdx.x;
-    const int items_per_bt = a.rb_per_prob * a.splits;
-    const int items_per_p = a.n_bt * items_per_bt;
-    const int p = item / items_per_p;
-    if (p >= a.nprob) return;
-    if (a.nprob_dev && p >= *a.nprob_dev) return;
-    int rem = item - p * items_per_p;
-    const int bt = rem / items_per_bt;
-    rem -= bt * items_per_bt;
-    const int rb = rem / a.splits;
-    const int s = rem - rb * a.splits;
-    const ColiProb pr = a.prob ? a.prob[p] : a.prob0;
+    __shared__ int split_last;
+    // readfirstlane: the wave index is wave-uniform, so everything derived from it
+    // (tile indices, validity, base pointers) stays in scalar registers.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // INL launches a 3-D grid (row block, split, batch tile): no index
+    // arithmetic on kernel arguments precedes the first loads.
+    int p = 0, bt, rb, s;
+    if constexpr (INL) {
+        rb = blockIdx.x;
+        s = blockIdx.y;
+        bt = blockIdx.z;
+    } else {
+        const int item = blockIdx.x;
+        const int items_per_bt = a.rb_per_prob * a.splits;
+        const int items_per_p = a.n_bt * items_per_bt;
+        p = item / items_per_p;
+        if (p >= a.nprob) return;
+        if (a.nprob_dev && p >= *a.nprob_dev) return;
+        int rem = item - p * items_per_p;
+        bt = rem / items_per_bt;
+        rem -= bt * items_per_bt;
+        rb = rem / a.splits;
+        s = rem - rb * a.splits;
+    }
+    const ColiProb pr = uniform_prob(INL ? a.prob0 : a.prob[p]);
     const int nb = min(16, pr.nrows - 16 * bt);
-    if (nb <= 0) return;
+    if constexpr (!INL) {
+        if (nb <= 0) return;
+    }
 
     const int b = lane & 15, ks = lane >> 4;
     const int Q0 = s * a.qps, Q1 = min(a.nq, Q0 + a.qps);
 
-    // Row tiles past the matrix read the zero buffer (zero scale: no contribution).
+    // Row tiles past the matrix read the zero tile (zero scale: no contribution).
     int rt[R];
     bool live[R];
-    const uint8_t *wb[R];
-    const void *sb[R];
-    size_t tbase[R];
-    int tstep[R];
+    TileRows<KIND, R> rows;
 #pragma unroll
     for (int r = 0; r < R; r++) {
         int rr = DUAL ? (r % RT) : r;
         rt[r] = rb * RT + rr;
         live[r] = rt[r] < a.nrt;
-        bool second = DUAL && r >= RT;
-        wb[r] = live[r] ? (second ? pr.w1 : pr.w0) : (const uint8_t *)a.zero;
-        sb[r] = live[r] ? (second ? pr.s1 : pr.s0) : (const void *)a.zero;
-        tbase[r] = live[r] ? (size_t)rt[r] * a.nq : 0;
-        tstep[r] = live[r] ? 1 : 0;
+        const bool second = DUAL && r >= RT;
+        // (branch-free: the clamped row tile is computed either way)
+        const size_t t0 = (size_t)(uint32_t)min(rt[r], a.nrt - 1) * (uint32_t)a.nq;
+        const uint8_t *wl = (second ? pr.w1 : pr.w0) + t0 * COLI_TILE_BYTES;
+        const uint8_t *sl = (const uint8_t *)(second ? pr.s1 : pr.s0) + t0 * ScaleRegs<KIND>::kTileBytes;
+        rows.w[r] = live[r] ? wl : (const uint8_t *)a.zero;
+        rows.s[r] = live[r] ? sl : (const uint8_t *)a.zero;
+        rows.qstep[r] = live[r] ? 1 : 0;
     }
     // the first weight stage goes out before anything else is resolved
     Stage<KIND, R, true> st[COLI_PD];
     const int q_first = Q0 + wave;
-    load_weights<KIND, R>(st[0], q_first < Q1, q_first, tbase, tstep, wb, sb, a.zero, lane);
+    load_weights<KIND, R>(st[0], max(0, min(q_first, Q1 - 1)), rows, lane);
+    // Lanes past the problem's rows read the last real row: MFMA output rows
+    // are independent, and those rows are never stored.
+    const int br_lane = pr.xrow_off + 16 * bt + min(b, nb - 1);
+    const int fr = a.xrows ? a.xrows[br_lane] : br_lane;
+    const uint32_t xoff = ((uint32_t)fr * (uint32_t)a.xstride + ks * 8) * 2;
+    const uint8_t *xh = (const uint8_t *)a.xhi, *xl = (const uint8_t *)a.xlo;
+    if (q_first < Q1) {
+        const uint8_t *qh = xh + (size_t)q_first * 256;
+#pragma unroll
+        for (int j = 0; j < 4; j++) st[0].xh[j] = *GPTR(half8v, qh + xoff + j * 64);
+    }
 
     const bool use_lo = *a.haslo >= a.lo_gen;  // >=: stays correct under graph replay
-    // Lanes past the problem's rows read the zero fragment row.
-    const _Float16 *xh = a.zero, *xl = a.zero;
-    if (b < nb) {
-        const int br = pr.xrow_off + 16 * bt + b;
-        const int fr = a.xrows ? a.xrows[br] : br;
-        xh = a.xhi + (size_t)fr * a.xstride + ks * 8;
-        xl = a.xlo + (size_t)fr * a.xstride + ks * 8;
-    }
     // exponent of the batch row this wave finishes (used after the loop)
     int E_out = 0;
     if (a.splits == 1 && wave < NB4) {
@@ -397,8 +427,8 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
-    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, st, q_first, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
-    else gemv_quads<KIND, R, NB4, W, false>(acc, st, q_first, Q1, tbase, tstep, wb, sb, xh, xl, a.zero, lane);
+    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, st, q_first, Q1, rows, xh, xl, xoff, lane);
+    else gemv_quads<KIND, R, NB4, W, false>(acc, st, q_first, Q1, rows, xh, xl, xoff, lane);
 
     // ---- intra-group reduction in fixed wave order; wave i finishes register i ----
 #pragma unroll
@@ -418,56 +448,47 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
         }
     }
 
-    // ---- split K across groups: publish the partial; coli_gemv_reduce finishes ----
+    // ---- split K across groups: publish the partial; the last group of the
+    // instance to arrive sums all partials in split order (deterministic) and
+    // runs the epilogue. The groups of one instance may sit on different XCDs,
+    // whose L2s are not coherent with each other: partials are written and
+    // read as agent-scope atomics (coherent by themselves, no whole-cache
+    // writeback or invalidate), and every group waits for its stores to
+    // complete before it counts its arrival. The counter is reset by the last
+    // group, so it is zero again for the next launch.
     if (a.splits > 1) {
+        const size_t inst = ((size_t)p * a.n_bt + bt) * a.rb_per_prob + rb;
+        const size_t pbase = (inst * a.splits * R * NB4 + i) * 64 + lane;
         if (i < NB4) {
-            const size_t inst = ((size_t)p * a.n_bt + bt) * a.rb_per_prob + rb;
-            float *mine = a.partial + ((inst * a.splits + s) * R * NB4 + i) * 64 + lane;
 #pragma unroll
-            for (int r = 0; r < R; r++) mine[r * NB4 * 64] = v[r];
+            for (int r = 0; r < R; r++)
+                __hip_atomic_store(a.partial + pbase + ((size_t)s * R + r) * NB4 * 64, v[r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
-        return;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int old = __hip_atomic_fetch_add(a.split_cnt + inst, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            split_last = old == a.splits - 1;
+            if (split_last) __hip_atomic_store(a.split_cnt + inst, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!split_last || i >= NB4) return;
+#pragma unroll
+        for (int r = 0; r < R; r++) v[r] = 0.0f;
+        for (int ss = 0; ss < a.splits; ss++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                v[r] += __hip_atomic_load(a.partial + pbase + ((size_t)ss * R + r) * NB4 * 64, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        const int brow = ks * 4 + i;
+        if (brow < nb) {
+            const int br = pr.xrow_off + 16 * bt + brow;
+            E_out = a.xexp[a.xrows ? a.xrows[br] : br];
+        }
     }
     if (i >= NB4) return;
     gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, ks * 4 + i, lane, E_out);
-}
-
-// Second pass of a split-K launch: sums the groups' partials in split order
-// (deterministic) and applies the epilogue. One thread per (instance, row
-// register i, lane); the instance's tiles are handled in one thread.
-template <int R, bool DUAL, int NB4>
-__global__ __launch_bounds__(256) void coli_gemv_reduce(ColiGemvArgs a) {
-    constexpr int RT = DUAL ? R / 2 : R;
-    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const int lane = (int)(t & 63), i = (int)((t >> 6) % NB4);
-    const size_t inst = (t >> 6) / NB4;
-    const size_t ninst = (size_t)a.nprob * a.n_bt * a.rb_per_prob;
-    if (inst >= ninst) return;
-    const int p = (int)(inst / ((size_t)a.n_bt * a.rb_per_prob));
-    if (a.nprob_dev && p >= *a.nprob_dev) return;
-    const int rem = (int)(inst - (size_t)p * a.n_bt * a.rb_per_prob);
-    const int bt = rem / a.rb_per_prob, rb = rem - bt * a.rb_per_prob;
-    const ColiProb pr = a.prob ? a.prob[p] : a.prob0;
-    const int nb = min(16, pr.nrows - 16 * bt);
-    const int brow = 4 * (lane >> 4) + i;
-    if (nb <= 0 || brow >= nb) return;
-    const int br = pr.xrow_off + 16 * bt + brow;
-    const int E = a.xexp[a.xrows ? a.xrows[br] : br];
-    float v[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) v[r] = 0.0f;
-    const float *base = a.partial + ((inst * a.splits) * R * NB4 + i) * 64 + lane;
-    for (int ss = 0; ss < a.splits; ss++)
-#pragma unroll
-        for (int r = 0; r < R; r++) v[r] += base[((size_t)ss * R + r) * NB4 * 64];
-    int rt[R];
-    bool live[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        rt[r] = rb * RT + (DUAL ? r % RT : r);
-        live[r] = rt[r] < a.nrt;
-    }
-    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, brow, lane, E);
 }
 
 // ---------------------------------------------------------------------------
@@ -570,36 +591,30 @@ struct ColiGemvPlan {
 // 1024-thread group would spill.
 template <int KIND, int R, bool DUAL, int NB4>
 static hipError_t launch_w(const ColiGemvArgs &a, int W, int blocks, hipStream_t st) {
+    const bool inl = a.prob == nullptr;
+    const dim3 grid = inl ? dim3(a.rb_per_prob, a.splits, a.n_bt) : dim3(blocks);
     if constexpr (R <= 2) {
         if (W == 16) {
-            hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 16>), dim3(blocks), dim3(1024), 0, st, a);
+            if (inl) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 16, true>), grid, dim3(1024), 0, st, a);
+            else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 16, false>), grid, dim3(1024), 0, st, a);
             return hipGetLastError();
         }
     }
-    if (W >= 8) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 8>), dim3(blocks), dim3(512), 0, st, a);
-    else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 4>), dim3(blocks), dim3(256), 0, st, a);
+    if (W >= 8) {
+        if (inl) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 8, true>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 8, false>), grid, dim3(512), 0, st, a);
+    } else {
+        if (inl) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 4, true>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 4, false>), grid, dim3(256), 0, st, a);
+    }
     return hipGetLastError();
-}
-
-template <int R, bool DUAL, int NB4>
-static hipError_t launch_reduce(const ColiGemvArgs &a, hipStream_t st) {
-    size_t threads = (size_t)a.nprob * a.n_bt * a.rb_per_prob * NB4 * 64;
-    hipLaunchKernelGGL((coli_gemv_reduce<R, DUAL, NB4>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
-    return hipGetLastError();
-}
-
-template <int KIND, int R, bool DUAL, int NB4>
-static hipError_t launch_split(const ColiGemvArgs &a, int W, int blocks, hipStream_t st) {
-    hipError_t e = launch_w<KIND, R, DUAL, NB4>(a, W, blocks, st);
-    if (e != hipSuccess || a.splits <= 1) return e;
-    return launch_reduce<R, DUAL, NB4>(a, st);
 }
 
 template <int KIND, int R, bool DUAL>
 static hipError_t launch_nb(const ColiGemvArgs &a, int nb4, int W, int blocks, hipStream_t st) {
-    if (nb4 == 1) return launch_split<KIND, R, DUAL, 1>(a, W, blocks, st);
-    if (nb4 == 2) return launch_split<KIND, R, DUAL, 2>(a, W, blocks, st);
-    return launch_split<KIND, R, DUAL, 4>(a, W, blocks, st);
+    if (nb4 == 1) return launch_w<KIND, R, DUAL, 1>(a, W, blocks, st);
+    if (nb4 == 2) return launch_w<KIND, R, DUAL, 2>(a, W, blocks, st);
+    return launch_w<KIND, R, DUAL, 4>(a, W, blocks, st);
 }
 
 template <int KIND>
@@ -616,6 +631,7 @@ static hipError_t launch_kind(const ColiGemvArgs &a, int R, bool dual, int nb4, 
 extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, int W, int max_rows,
                                        hipStream_t st) {
     int nb4 = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
+    if (!a->prob && (a->nprob != 1 || a->nprob_dev)) return hipErrorInvalidValue;   // inline problem: exactly one
     long items = (long)a->nprob * a->n_bt * a->rb_per_prob * a->splits;
     int blocks = (int)items;
     if (blocks <= 0) return hipSuccess;

@@ -74,7 +74,9 @@ template <int SMAX>
 __global__ __launch_bounds__(256) void coli_router_partial(const float *__restrict__ x, int S,
                                                            const float *__restrict__ W, int D, int E,
                                                            float *__restrict__ part, size_t chstride) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // readfirstlane: the wave index is wave-uniform, so everything derived from it
+    // (tile indices, validity, base pointers) stays in scalar registers.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int e = blockIdx.x * 4 + wave, ch = blockIdx.y;
     if (e >= E) return;
     const float *wr = W + (size_t)e * D;
@@ -165,7 +167,9 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
                                                           float routed_scale, int *__restrict__ idx,
                                                           float *__restrict__ wout, int *__restrict__ keff) {
     extern __shared__ float sh[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // readfirstlane: the wave index is wave-uniform, so everything derived from it
+    // (tile indices, validity, base pointers) stays in scalar registers.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = blockIdx.x * 4 + wave;
     float *p = sh + (size_t)wave * (2 * E + 128);     // [E] weight source
     float *c = p + E;                                 // [E] selection score

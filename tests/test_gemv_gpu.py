@@ -35,6 +35,25 @@ def test_int4_g32_fp16_scales(session, O, I, S):
     check(y, ref, magnitude(x, deq_i4(q4, sc, I, 32)))
 
 
+# The dense benchmark shapes: the up projection runs one group per
+# row block, the down projection splits K across workgroups.
+@pytest.mark.parametrize("O,I", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("S", [1, 16])
+def test_int4_dense_bench_shapes(session, O, I, S):
+    rng = np.random.default_rng(O + I + S)
+    q4, sc = rand_i4(rng, O, I, 32)
+    x = rand_x(rng, S, I)
+    h = session.upload(q4, sc, 4, I, O, 32)
+    try:
+        y = session.matmul(h, x, 4, I, O, 32)
+        y2 = session.matmul(h, x, 4, I, O, 32)
+    finally:
+        session.free(h)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))   # run-to-run bitwise
+    ref = cref.matmul_i4_grouped(x, q4, sc, O, I, 32)
+    check(y, ref, magnitude(x, deq_i4(q4, sc, I, 32)))
+
+
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("S", [1, 5])
 def test_int4_f32_scales_and_group_sizes(session, gs, S):

@@ -30,12 +30,15 @@ def _get(b, p, shape):
     return out
 
 
+# (200, 384): one group per row block; (128, 16384): long K split across
+# workgroups, whose arrival counters must be back at zero after every launch.
 @pytest.mark.parametrize("fmt", [4, 7])
-def test_gemm_graph_replays_match_eager(session, fmt):
+@pytest.mark.parametrize("O,I", [(200, 384), (128, 16384)])
+def test_gemm_graph_replays_match_eager(session, fmt, O, I):
     b = session.b
     st = b.hip_stream(0)
-    rng = np.random.default_rng(50 + fmt)
-    O, I, S = 200, 384, 3
+    rng = np.random.default_rng(50 + fmt + I)
+    S = 3
     if fmt == 4:
         q4, sc = rand_i4(rng, O, I, 32)
         h = session.upload(q4, sc, 4, I, O, 32)
