@@ -154,13 +154,97 @@ extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const flo
 //           kept set (c/kimi_k3.c:1337-1370); routed_scale applied after.
 // The reference selects by K rounds of an argmax with strict '>' (highest
 // value, lowest index on ties; NaN and values <= -1e30 never chosen; a round
-// with nothing left picks index kk, c/route_trace.h:383-393). The same order
-// is computed here in one pass: a valid expert's rank is the number of valid
-// experts that beat it, and rank r < K lands in slot r. Ranks are distinct
-// because the order is total (ties go to the lower index).
+// with nothing left picks index kk, c/route_trace.h:383-393). The same rounds
+// run here across the wave: each is a 64-lane argmax over order-preserving
+// keys, which leaves the chosen expert and its weight in lane kk; the
+// post-processing (normalization, TOPP ranks and cumulative sums) then runs
+// with one slot per lane.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool valid_score(float v) { return v == v && v > -1e30f; }
 
+// Wave-wide reductions without LDS round trips: a butterfly inside each
+// 16-lane row through DPP lane moves (quad_perm xor 1, xor 2, then row
+// rotations by 4 and 8), then the four row results read into scalar registers
+// and combined in row order. Every lane returns the same value; the
+// combination order is fixed, so results are reproducible.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+#define COLI_DPP_XOR1 0xB1    // quad_perm [1, 0, 3, 2]
+#define COLI_DPP_XOR2 0x4E    // quad_perm [2, 3, 0, 1]
+#define COLI_DPP_ROR4 0x124   // row_ror:4
+#define COLI_DPP_ROR8 0x128   // row_ror:8
+
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = op(v, __int_as_float(dpp_mov<COLI_DPP_XOR1>(__float_as_int(v))));
+    v = op(v, __int_as_float(dpp_mov<COLI_DPP_XOR2>(__float_as_int(v))));
+    v = op(v, __int_as_float(dpp_mov<COLI_DPP_ROR4>(__float_as_int(v))));
+    v = op(v, __int_as_float(dpp_mov<COLI_DPP_ROR8>(__float_as_int(v))));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return op(op(op(r0, r1), r2), r3);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    return wave_reduce(v, [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ float wave_max(float v) {
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+    v += dpp_mov<COLI_DPP_XOR1>(v);
+    v += dpp_mov<COLI_DPP_XOR2>(v);
+    v += dpp_mov<COLI_DPP_ROR4>(v);
+    v += dpp_mov<COLI_DPP_ROR8>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, dpp_mov<COLI_DPP_XOR1>(v));
+    v = min(v, dpp_mov<COLI_DPP_XOR2>(v));
+    v = min(v, dpp_mov<COLI_DPP_ROR4>(v));
+    v = min(v, dpp_mov<COLI_DPP_ROR8>(v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+// Argmax over (key, then lowest index) carrying a payload; uniform result.
+__device__ __forceinline__ void wave_argmax(unsigned &k, int &e, float &w) {
+    auto step = [&](unsigned ok, int oe, float ow) {
+        if (ok > k || (ok == k && oe < e)) {
+            k = ok;
+            e = oe;
+            w = ow;
+        }
+    };
+#define COLI_ARGMAX_STEP(CTRL) \
+    step((unsigned)dpp_mov<CTRL>((int)k), dpp_mov<CTRL>(e), __int_as_float(dpp_mov<CTRL>(__float_as_int(w))))
+    COLI_ARGMAX_STEP(COLI_DPP_XOR1);
+    COLI_ARGMAX_STEP(COLI_DPP_XOR2);
+    COLI_ARGMAX_STEP(COLI_DPP_ROR4);
+    COLI_ARGMAX_STEP(COLI_DPP_ROR8);
+#undef COLI_ARGMAX_STEP
+    unsigned rk[4];
+    int re[4];
+    float rw[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        rk[r] = (unsigned)__builtin_amdgcn_readlane((int)k, 16 * r);
+        re[r] = __builtin_amdgcn_readlane(e, 16 * r);
+        rw[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 16 * r));
+    }
+    k = rk[0];
+    e = re[0];
+    w = rw[0];
+#pragma unroll
+    for (int r = 1; r < 4; r++) step(rk[r], re[r], rw[r]);
+}
+
+#define COLI_SEL_BATCH 4   // experts per lane whose chunk partials are loaded together (JM >= 4)
+#define COLI_SEL_MAXCH 16  // chunk partials held in registers (more are added from memory)
+template <int JM>
 __global__ __launch_bounds__(256) void coli_router_select(const float *__restrict__ part, int nch,
                                                           const float *__restrict__ bias, int S, int E, int K,
                                                           int mode, float topp, int norm_topk,
@@ -171,64 +255,80 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
     // (tile indices, validity, base pointers) stays in scalar registers.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int s = blockIdx.x * 4 + wave;
-    float *p = sh + (size_t)wave * (2 * E + 128);     // [E] weight source
-    float *c = p + E;                                 // [E] selection score
-    int *sel = (int *)(c + E);                        // [64]
-    float *selw = c + E + 64;                         // [64]
+    float *p = sh + (size_t)wave * E;                 // [E] weight source (fallback slots read it)
     const bool live = s < S;
     const size_t chstride = (size_t)S * E;
     const float *z0 = part + (size_t)(live ? s : 0) * E;
-    auto logit = [&](int e) {
-        float v = z0[e];
-        for (int ch = 1; ch < nch; ch++) v += z0[(size_t)ch * chstride + e];
-        return v;
-    };
-    if (mode == 0) {
-        float m = -1e30f;
-        for (int e = lane; e < E; e += 64) {
-            const float v = logit(e);
-            p[e] = v;
-            m = fmaxf(m, v);
+    // Lane l owns experts e = l + 64 j (E <= 1024: j < 16). Their chunk
+    // partials (and bias) are all requested before the first add: every load
+    // is unconditional (indices clamped into range, the extra values masked
+    // in the sum), so none waits for another. Logits are summed in chunk order.
+    constexpr int CB = COLI_SEL_BATCH < JM ? COLI_SEL_BATCH : JM, CH = COLI_SEL_MAXCH;
+    const int nmine = (E - lane + 63) / 64;   // this lane's experts
+    const int jmax = (E + 63) / 64;           // wave-uniform bound
+    float lg[JM] = {}, bs[JM] = {};
+#pragma unroll
+    for (int j0 = 0; j0 < JM; j0 += CB) {
+        if (j0 >= jmax) continue;
+        float t[CB][CH];
+        int ee[CB];
+#pragma unroll
+        for (int jj = 0; jj < CB; jj++) {
+            ee[jj] = min(lane + 64 * (j0 + jj), E - 1);
+#pragma unroll
+            for (int ch = 0; ch < CH; ch++) t[jj][ch] = z0[(size_t)min(ch, nch - 1) * chstride + ee[jj]];
+            bs[j0 + jj] = bias ? bias[ee[jj]] : 0.0f;
         }
 #pragma unroll
-        for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        float sum = 0.0f;
-        for (int e = lane; e < E; e += 64) {
-            const float v = expf(p[e] - m);
-            p[e] = v;
-            sum += v;
-        }
+        for (int jj = 0; jj < CB; jj++) {
+            float v = t[jj][0];
 #pragma unroll
-        for (int off = 32; off; off >>= 1) sum += __shfl_xor(sum, off);
-        for (int e = lane; e < E; e += 64) {
-            p[e] = p[e] / sum;
-            c[e] = p[e];
-        }
-    } else {
-        for (int e = lane; e < E; e += 64) {
-            const float v = 1.0f / (1.0f + expf(-logit(e)));
-            p[e] = v;
-            c[e] = v + (bias ? bias[e] : 0.0f);
+            for (int ch = 1; ch < CH; ch++) v += ch < nch ? t[jj][ch] : 0.0f;
+            for (int ch = CH; ch < nch; ch++) v += z0[(size_t)ch * chstride + ee[jj]];
+            lg[j0 + jj] = v;
         }
     }
-    if (lane < 64) sel[lane] = -1;
-    __syncthreads();
-    if (!live) return;
-    // ranks of this lane's experts among the valid ones
-    // Radix select on order-preserving keys (a valid score maps to a key > 0,
-    // an invalid one to 0; +0 and -0 share a key, as they compare equal):
-    // T = the K-th largest key, then everything above T plus the lowest-index
-    // experts equal to T; the chosen ones are ranked among themselves.
-    // Lane l holds experts l, l + 64, ... (E <= 1024: at most 16).
-    int nvalid = 0;
-    unsigned key[16];
-    const int nmine = (E - lane + 63) / 64;   // this lane's experts
-    const int jmax = (E + 63) / 64;           // wave-uniform bound (keys past nmine are 0)
+    // weight source pv (also in LDS, for the fallback slots) and selection score cv
+    float cv[JM], pv[JM];
+    if (mode == 0) {
+        float m = -1e30f;
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
+        for (int j = 0; j < JM; j++)
+            if (j < nmine) m = fmaxf(m, lg[j]);
+        m = wave_max(m);
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < JM; j++) {
+            lg[j] = j < nmine ? expf(lg[j] - m) : 0.0f;
+            sum += lg[j];
+        }
+        sum = wave_sum(sum);
+#pragma unroll
+        for (int j = 0; j < JM; j++) {
+            const float v = lg[j] / sum;
+            if (j < nmine) p[lane + 64 * j] = v;
+            cv[j] = v;
+            pv[j] = v;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < JM; j++) {
+            const float v = 1.0f / (1.0f + expf(-lg[j]));
+            if (j < nmine) p[lane + 64 * j] = v;
+            cv[j] = v + bs[j];
+            pv[j] = v;
+        }
+    }
+    if (!live) return;
+    // Order-preserving keys: a valid score maps to a key > 0, an invalid one
+    // (NaN, or <= -1e30) to 0; +0 and -0 share a key, as they compare equal.
+    int nvalid = 0;
+    unsigned key[JM];
+#pragma unroll
+    for (int j = 0; j < JM; j++) {
         unsigned k = 0;
         if (j < nmine) {
-            float v = c[lane + 64 * j];
+            float v = cv[j];
             if (valid_score(v)) {
                 if (v == 0.0f) v = 0.0f;
                 const unsigned b = __float_as_uint(v);
@@ -238,133 +338,105 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
         key[j] = k;
         nvalid += k != 0;
     }
-#pragma unroll
-    for (int off = 32; off; off >>= 1) nvalid += __shfl_xor(nvalid, off);
+    nvalid = wave_sum_i(nvalid);
     const int want = nvalid < K ? nvalid : K;
-    unsigned T = 0;
-    if (want > 0) {
-        for (int bit = 31; bit >= 0; bit--) {
-            const unsigned cand = T | (1u << bit);
-            int cnt = 0;
+    // K rounds of a wave-wide argmax (largest key, then lowest expert index):
+    // round kk yields the expert of rank kk (and its weight source), which its
+    // owner lane then retires; lane kk keeps slot kk.
+    int my_e = 0;
+    float my_w = 0.0f;
+    for (int kk = 0; kk < want; kk++) {
+        unsigned bk = 0;
+        int be = 0x7fffffff;
+        float bw = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                if (j >= jmax) break;
-                cnt += __popcll(__ballot(key[j] >= cand));
+        for (int j = 0; j < JM; j++)
+            if (key[j] > bk) {   // strict: the lower index (smaller j) wins a tie
+                bk = key[j];
+                be = lane + 64 * j;
+                bw = pv[j];
             }
-            if (cnt >= want) T = cand;
-        }
-    }
-    // chosen: key > T, or key == T among the first (want - above) in index order
-    int above = 0;
+        wave_argmax(bk, be, bw);
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        if (j >= jmax) break;
-        above += __popcll(__ballot(key[j] > T));
-    }
-    const unsigned long long lt = (1ull << lane) - 1ull;
-    int eq_before = 0;          // experts equal to T with a lower index, running over j
-    int nchosen = 0;
-    __shared__ unsigned ckey[4][64];
-    __shared__ int cexp[4][64];
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        if (j >= jmax) break;
-        const bool gt = want > 0 && key[j] > T;
-        const bool eq = want > 0 && key[j] == T && key[j] != 0;
-        const unsigned long long meq = __ballot(eq);
-        const bool take_eq = eq && eq_before + __popcll(meq & lt) < want - above;
-        const bool take = gt || take_eq;
-        const unsigned long long mt = __ballot(take);
-        if (take) {
-            const int slot = nchosen + __popcll(mt & lt);
-            ckey[wave][slot] = key[j];
-            cexp[wave][slot] = lane + 64 * j;
+        for (int j = 0; j < JM; j++)
+            if (lane + 64 * j == be) key[j] = 0;
+        if (lane == kk) {
+            my_e = be;
+            my_w = bw;
         }
-        nchosen += __popcll(mt);
-        eq_before += __popcll(meq);
     }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (lane < nchosen) {   // rank among the chosen: larger key first, lower index on ties
-        const unsigned k0 = ckey[wave][lane];
-        const int e0 = cexp[wave][lane];
-        int rank = 0;
-        for (int q = 0; q < nchosen; q++) {
-            const unsigned k1 = ckey[wave][q];
-            const int e1 = cexp[wave][q];
-            rank += (k1 > k0 || (k1 == k0 && e1 < e0)) ? 1 : 0;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // p[] written by all lanes
+    const bool act = lane < K;
+    if (act && lane >= want) {   // fewer valid scores than K: experts 0, 1, ... fill the rest
+        my_e = lane < E ? lane : 0;
+        my_w = p[my_e];
+    }
+    if (!act) my_w = 0.0f;
+    auto wsum = [](float v) { return wave_sum(v); };
+    // rank of this slot when sorted by weight, descending and stable (ties
+    // keep slot order), and the inclusive cumulative weight in that order
+    auto sort_rank = [&](int &rank, float &cum) {
+        rank = 0;
+        cum = 0.0f;
+        for (int j = 0; j < K; j++) {
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
+            const bool before = wj > my_w || (wj == my_w && j < lane);
+            rank += before ? 1 : 0;
+            cum += (before || j == lane) ? wj : 0.0f;
         }
-        sel[rank] = e0;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // sel[] written by its owner lanes
-    if (lane != 0) return;
-    for (int kk = 0; kk < K; kk++) {
-        if (kk >= nvalid) sel[kk] = kk < E ? kk : 0;
-        selw[kk] = p[sel[kk]];
-    }
-    int ke = K;
+    };
+    int slot = lane, ke = K;
+    const bool cut = topp > 0.0f && topp < 1.0f;
     if (mode == 0) {
-        if (norm_topk) {
-            float sm = 0.0f;
-            for (int kk = 0; kk < K; kk++) sm += selw[kk];
-            for (int kk = 0; kk < K; kk++) selw[kk] /= sm;
-        }
+        if (norm_topk) my_w /= wsum(my_w);
     } else if (mode == 1) {
-        if (topp > 0.0f && topp < 1.0f) {
-            for (int a = 1; a < K; a++) {
-                int ii = sel[a]; float ww = selw[a]; int b = a - 1;
-                while (b >= 0 && selw[b] < ww) { selw[b + 1] = selw[b]; sel[b + 1] = sel[b]; b--; }
-                selw[b + 1] = ww; sel[b + 1] = ii;
-            }
-            float tot = 1e-20f, cum = 0.0f;
-            for (int kk = 0; kk < K; kk++) tot += selw[kk];
-            for (int kk = 0; kk < K; kk++) {
-                cum += selw[kk];
-                if (cum >= topp * tot) { ke = kk + 1; break; }
-            }
+        if (cut) {
+            float cum;
+            sort_rank(slot, cum);
+            const float tot = 1e-20f + wsum(my_w);
+            const int first = wave_min_i(act && cum >= topp * tot ? slot : K - 1);
+            ke = first + 1;
         }
-        if (norm_topk) {
-            float sm = 0.0f;
-            for (int kk = 0; kk < ke; kk++) sm += selw[kk];
-            sm += 1e-20f;
-            for (int kk = 0; kk < ke; kk++) selw[kk] /= sm;
-        }
-        for (int kk = 0; kk < ke; kk++) selw[kk] *= routed_scale;
+        if (norm_topk) my_w /= wsum(act && slot < ke ? my_w : 0.0f) + 1e-20f;
+        if (slot < ke) my_w *= routed_scale;
     } else {
-        float sm = 0.0f;
-        for (int kk = 0; kk < K; kk++) sm += selw[kk];
-        for (int kk = 0; kk < K; kk++) selw[kk] /= (sm + 1e-20f);
-        if (topp > 0.0f && topp < 1.0f) {
-            for (int a = 1; a < K; a++) {
-                int e2 = sel[a]; float w2 = selw[a]; int b = a - 1;
-                while (b >= 0 && selw[b] < w2) { sel[b + 1] = sel[b]; selw[b + 1] = selw[b]; b--; }
-                sel[b + 1] = e2; selw[b + 1] = w2;
-            }
-            float cum = 0.0f; int keep = K;
-            for (int kk = 0; kk < K; kk++) { cum += selw[kk]; if (cum >= topp) { keep = kk + 1; break; } }
+        my_w /= wsum(my_w) + 1e-20f;
+        if (cut) {
+            float cum;
+            sort_rank(slot, cum);
+            const int keep = wave_min_i(act && cum >= topp ? slot + 1 : K);
             if (keep < K) {
-                float s2 = 0.0f;
-                for (int kk = 0; kk < keep; kk++) s2 += selw[kk];
-                for (int kk = 0; kk < keep; kk++) selw[kk] /= (s2 + 1e-20f);
+                my_w /= wsum(act && slot < keep ? my_w : 0.0f) + 1e-20f;
                 ke = keep;
             }
         }
-        if (routed_scale != 1.0f)
-            for (int kk = 0; kk < ke; kk++) selw[kk] *= routed_scale;
+        if (routed_scale != 1.0f && slot < ke) my_w *= routed_scale;
     }
-    for (int kk = 0; kk < K; kk++) {
-        idx[(size_t)s * K + kk] = sel[kk];
-        wout[(size_t)s * K + kk] = kk < ke ? selw[kk] : 0.0f;
+    if (act) {
+        idx[(size_t)s * K + slot] = my_e;
+        wout[(size_t)s * K + slot] = slot < ke ? my_w : 0.0f;
     }
-    keff[s] = ke;
+    if (lane == 0) keff[s] = ke;
 }
 
 extern "C" hipError_t coli_launch_router_select(const float *part, int nch, const float *bias, int S, int E,
                                                 int K, int mode, float topp, int norm_topk,
                                                 float routed_scale, int *idx, float *w, int *keff,
                                                 hipStream_t st) {
-    size_t shm = (size_t)4 * (2 * E + 128) * sizeof(float);
-    hipLaunchKernelGGL(coli_router_select, dim3((S + 3) / 4), dim3(256), shm, st, part, nch, bias, S, E, K, mode,
-                       topp, norm_topk, routed_scale, idx, w, keff);
+    size_t shm = (size_t)4 * E * sizeof(float);
+    // experts per lane, rounded up to a power of two (E <= 1024)
+    const int jm = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+#define COLI_SEL_LAUNCH(JM)                                                                                       \
+    hipLaunchKernelGGL(coli_router_select<JM>, dim3((S + 3) / 4), dim3(256), shm, st, part, nch, bias, S, E, K, mode, \
+                       topp, norm_topk, routed_scale, idx, w, keff)
+    switch (jm) {
+    case 1: COLI_SEL_LAUNCH(1); break;
+    case 2: COLI_SEL_LAUNCH(2); break;
+    case 4: COLI_SEL_LAUNCH(4); break;
+    case 8: COLI_SEL_LAUNCH(8); break;
+    default: COLI_SEL_LAUNCH(16); break;
+    }
+#undef COLI_SEL_LAUNCH
     return hipGetLastError();
 }
 
