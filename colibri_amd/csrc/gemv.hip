@@ -230,10 +230,8 @@ struct TileRows {
 
 // Main loop of one wave over its quads q = q_first + it*W, it < nit.
 // A ring of PD stages: the loads of iteration it+PD-1 are issued (as one
-// branch-free batch) before the math of iteration it, so up to PD-1 stages
-// stay in flight while the wave computes. Iterations past the end re-read
-// the wave's last quad (an L2 hit; their math is skipped), which keeps every
-// load unconditional and the in-order vmcnt accounting exact.
+// batch) before the math of iteration it, so up to PD-1 stages stay in flight
+// while the wave computes.
 template <int KIND, int R>
 __device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, int q, const TileRows<KIND, R> &rows,
                                              int lane) {
@@ -256,8 +254,7 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
     constexpr int PD = COLI_PD;
     if (q_first >= Q1) return;
     const int nit = (Q1 - q_first + W - 1) / W;
-    const int q_last = q_first + (nit - 1) * W;
-    auto qof = [&](int it) { return it < nit ? q_first + it * W : q_last; };
+    auto qof = [&](int it) { return q_first + it * W; };
     auto load_x = [&](Stage<KIND, R, true> &sg, int q) {
         const uint8_t *qh = xh + (size_t)q * 256, *ql = xl + (size_t)q * 256;
 #pragma unroll
@@ -290,14 +287,24 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
 #pragma unroll
         for (int j = 0; j < 4; j++) st[0].xl[j] = *GPTR(half8v, ql + xoff + j * 64);
     }
-#pragma unroll
-    for (int p = 1; p < PD - 1; p++) load(st[p], p);
-    for (int it0 = 0; it0 < nit; it0 += PD) {
-#pragma unroll
-        for (int u = 0; u < PD; u++) {
-            load(st[(u + PD - 1) % PD], it0 + u + PD - 1);
-            if (it0 + u < nit) compute(st[u]);
-        }
+    // Two-stage ring, unrolled by two so the stage registers are static; the
+    // tail issues no load past the wave's last quad (such loads would fetch
+    // tiles from HBM again). Every path leaves the loop with the same loads
+    // outstanding, so the compiler's vmcnt waits stay exact.
+    static_assert(PD == 2, "the loop below is written for a two-stage ring");
+    int it = 0;
+    for (; it + 2 < nit; it += 2) {
+        load(st[1], it + 1);
+        compute(st[0]);
+        load(st[0], it + 2);
+        compute(st[1]);
+    }
+    if (it + 1 < nit) {
+        load(st[1], it + 1);
+        compute(st[0]);
+        compute(st[1]);
+    } else {
+        compute(st[0]);
     }
 }
 
