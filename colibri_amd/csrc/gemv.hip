@@ -230,16 +230,21 @@ struct TileRows {
 
 // Main loop of one wave over its quads q = q_first + it*W, it < nit.
 // A ring of PD stages: the loads of iteration it+PD-1 are issued (as one
-// batch) before the math of iteration it, so up to PD-1 stages stay in flight
-// while the wave computes.
+// branch-free batch) before the math of iteration it, so up to PD-1 stages
+// stay in flight while the wave computes. Iterations past the end (their
+// math is skipped) read the zero tile instead of weights, and the wave's last
+// activation quad again (an L2 hit): every load stays unconditional, which
+// keeps the in-order vmcnt accounting exact, and no tile is fetched twice.
 template <int KIND, int R>
-__device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, int q, const TileRows<KIND, R> &rows,
-                                             int lane) {
+__device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, bool valid, int q,
+                                             const TileRows<KIND, R> &rows, const void *zero, int lane) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const int qq = q * rows.qstep[r];
-        sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, rows.w[r] + (size_t)qq * COLI_TILE_BYTES) + lane);
-        sg.sc[r].load(rows.s[r], (size_t)qq, lane & 15);
+        const int qq = valid ? q * rows.qstep[r] : 0;
+        const uint8_t *w = valid ? rows.w[r] : (const uint8_t *)zero;
+        const uint8_t *sp = valid ? rows.s[r] : (const uint8_t *)zero;
+        sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + (size_t)qq * COLI_TILE_BYTES) + lane);
+        sg.sc[r].load(sp, (size_t)qq, lane & 15);
     }
 }
 
@@ -247,14 +252,14 @@ __device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, int q, co
 // of iteration 0 into st[0] (before it knew whether lo fragments exist), so
 // the first requests leave the CU as early as possible. xoff = the lane's
 // byte offset of its fragment row and k-slice inside xh / xl.
-template <int KIND, int R, int NB4, int W, bool LO>
+template <int KIND, int R, int NB4, int W, bool LO, bool PEEL>
 __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, true> (&st)[COLI_PD], int q_first, int Q1,
                                            const TileRows<KIND, R> &rows, const uint8_t *xh, const uint8_t *xl,
-                                           uint32_t xoff, int lane) {
+                                           uint32_t xoff, const void *zero, int lane) {
     constexpr int PD = COLI_PD;
     if (q_first >= Q1) return;
     const int nit = (Q1 - q_first + W - 1) / W;
-    auto qof = [&](int it) { return q_first + it * W; };
+    const int q_last = q_first + (nit - 1) * W;
     auto load_x = [&](Stage<KIND, R, true> &sg, int q) {
         const uint8_t *qh = xh + (size_t)q * 256, *ql = xl + (size_t)q * 256;
 #pragma unroll
@@ -264,9 +269,10 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
         }
     };
     auto load = [&](Stage<KIND, R, true> &sg, int it) {
-        const int q = qof(it);
-        load_weights<KIND, R>(sg, q, rows, lane);
-        load_x(sg, q);
+        const bool valid = it < nit;
+        const int q = q_first + it * W;
+        load_weights<KIND, R>(sg, valid, q, rows, zero, lane);
+        load_x(sg, valid ? q : q_last);
     };
     auto compute = [&](const Stage<KIND, R, true> &sg) {
 #pragma unroll
@@ -287,24 +293,36 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
 #pragma unroll
         for (int j = 0; j < 4; j++) st[0].xl[j] = *GPTR(half8v, ql + xoff + j * 64);
     }
-    // Two-stage ring, unrolled by two so the stage registers are static; the
-    // tail issues no load past the wave's last quad (such loads would fetch
-    // tiles from HBM again). Every path leaves the loop with the same loads
-    // outstanding, so the compiler's vmcnt waits stay exact.
-    static_assert(PD == 2, "the loop below is written for a two-stage ring");
-    int it = 0;
-    for (; it + 2 < nit; it += 2) {
-        load(st[1], it + 1);
-        compute(st[0]);
-        load(st[0], it + 2);
-        compute(st[1]);
-    }
-    if (it + 1 < nit) {
-        load(st[1], it + 1);
-        compute(st[0]);
-        compute(st[1]);
+    if constexpr (PEEL) {
+        // Two-stage ring unrolled by two, with a tail that issues no load past
+        // the wave's last quad. Every path leaves the loop with the same loads
+        // outstanding, so the compiler's vmcnt waits stay exact. (Used where
+        // its larger code keeps the register budget of two waves per SIMD.)
+        static_assert(PD == 2, "the peeled loop is written for a two-stage ring");
+        int it = 0;
+        for (; it + 2 < nit; it += 2) {
+            load(st[1], it + 1);
+            compute(st[0]);
+            load(st[0], it + 2);
+            compute(st[1]);
+        }
+        if (it + 1 < nit) {
+            load(st[1], it + 1);
+            compute(st[0]);
+            compute(st[1]);
+        } else {
+            compute(st[0]);
+        }
     } else {
-        compute(st[0]);
+#pragma unroll
+        for (int p = 1; p < PD - 1; p++) load(st[p], p);
+        for (int it0 = 0; it0 < nit; it0 += PD) {
+#pragma unroll
+            for (int u = 0; u < PD; u++) {
+                load(st[(u + PD - 1) % PD], it0 + u + PD - 1);
+                if (it0 + u < nit) compute(st[u]);
+            }
+        }
     }
 }
 
@@ -407,7 +425,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     // the first weight stage goes out before anything else is resolved
     Stage<KIND, R, true> st[COLI_PD];
     const int q_first = Q0 + wave;
-    load_weights<KIND, R>(st[0], max(0, min(q_first, Q1 - 1)), rows, lane);
+    load_weights<KIND, R>(st[0], q_first < Q1, q_first, rows, a.zero, lane);
     // Lanes past the problem's rows read the last real row: MFMA output rows
     // are independent, and those rows are never stored.
     const int br_lane = pr.xrow_off + 16 * bt + min(b, nb - 1);
@@ -434,8 +452,10 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
-    if (use_lo) gemv_quads<KIND, R, NB4, W, true>(acc, st, q_first, Q1, rows, xh, xl, xoff, lane);
-    else gemv_quads<KIND, R, NB4, W, false>(acc, st, q_first, Q1, rows, xh, xl, xoff, lane);
+    // the peeled loop fits two waves per SIMD only in these variants
+    constexpr bool PEEL = INL && W == 8 && KIND == COLI_KIND_I4_H && R >= 2;
+    if (use_lo) gemv_quads<KIND, R, NB4, W, true, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
+    else gemv_quads<KIND, R, NB4, W, false, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
 
     // ---- intra-group reduction in fixed wave order; wave i finishes register i ----
 #pragma unroll
