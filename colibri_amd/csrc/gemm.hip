@@ -101,16 +101,19 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
         }
         dst[k] = hl * 16384 + (((m * 4 + j) * 4 + ks) * 16 + b) * 16;
     }
-    u32x4 creg[4];
-    auto gload = [&](int q) {
+    // Activation staging ring: quad q's fragments are read into registers two
+    // iterations ahead (slot q % 3) and written to LDS one iteration ahead, so
+    // their L2 latency is covered by a full iteration of math.
+    u32x4 creg[PD][4];
+    auto gload = [&](u32x4 (&cr)[4], int q) {
         if (!stager) return;
 #pragma unroll
-        for (int k = 0; k < 4; k++) creg[k] = *GPTR(u32x4, src[k] + (size_t)q * sstep[k]);
+        for (int k = 0; k < 4; k++) cr[k] = *GPTR(u32x4, src[k] + (size_t)q * sstep[k]);
     };
-    auto swrite = [&](int buf) {
+    auto swrite = [&](const u32x4 (&cr)[4], int buf) {
         if (!stager) return;
 #pragma unroll
-        for (int k = 0; k < 4; k++) *(u32x4 *)(lds + buf * BUF + dst[k]) = creg[k];
+        for (int k = 0; k < 4; k++) *(u32x4 *)(lds + buf * BUF + dst[k]) = cr[k];
     };
 
     floatx4 acc[R][4];
@@ -148,18 +151,20 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
         }
     };
 
-    gload(0);
-    swrite(0);
+    static_assert(PD == 3, "the staging ring below is written for three slots");
+    gload(creg[0], 0);
+    if (a.nq > 1) gload(creg[1], 1);
+    swrite(creg[0], 0);
     __syncthreads();
     for (int q0 = 0; q0 < a.nq; q0 += PD) {
 #pragma unroll
         for (int u = 0; u < PD; u++) {
             const int q = q0 + u;
             if (q >= a.nq) break;
-            if (q + 1 < a.nq) gload(q + 1);
+            if (q + 2 < a.nq) gload(creg[(u + 2) % PD], q + 2);
             load_w(st[(u + PD - 1) % PD], q + PD - 1);
             compute(st[u], q & 1);
-            if (q + 1 < a.nq) swrite((q + 1) & 1);
+            if (q + 1 < a.nq) swrite(creg[(u + 1) % PD], (q + 1) & 1);
             __syncthreads();
         }
     }
