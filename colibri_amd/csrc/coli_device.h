@@ -107,3 +107,27 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
+// Output of one lane for batch row `brow` of the problem: output row
+// rt*16 + (lane & 15) of every live tile, scaled back by the row's 2^E; for
+// DUAL, silu(gate) * up of the paired tiles.
+template <int R, bool DUAL>
+__device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiProb &pr, int bt, const int (&rt)[R],
+                                              const bool (&live)[R], const float (&v)[R], int brow, int lane,
+                                              int E) {
+    constexpr int RT = DUAL ? R / 2 : R;
+    const int nb = min(16, pr.nrows - 16 * bt);
+    if (brow >= nb) return;
+    float *orow = a.out + (size_t)(pr.out_row0 + 16 * bt + brow) * a.ldo;
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        if (!live[r]) continue;
+        const int o = rt[r] * 16 + (lane & 15);
+        if (o >= a.O) continue;
+        if constexpr (DUAL) {
+            float gv = ldexpf(v[r], E), uv = ldexpf(v[r + RT], E);
+            orow[o] = silu_mul(gv, uv);
+        } else {
+            orow[o] = ldexpf(v[r], E);
+        }
+    }
+}

@@ -59,6 +59,8 @@ int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scale
 extern "C" {
 hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, int W, int max_rows,
                             hipStream_t st);
+hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual, int PD, int max_rows,
+                                hipStream_t st);
 hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, const int *nrows_dev,
                                  int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
                                  int *exp2out, int *haslo, int gen, const void *zero, hipStream_t st);
@@ -90,6 +92,7 @@ hipError_t coli_launch_sum_slots(float *dst, const float *slots, int n, int D, h
 // issue, expert_mlp, resident_issue and the MoE layer.
 struct GemvLaunchPlan {
     int R, W, rbpp, splits, qps;
+    int dma, PD;   // LDS-ring kernel (gemv_dma.hip) and its ring depth
 };
 GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq, bool dual, int max_rows);
 

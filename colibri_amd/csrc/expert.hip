@@ -69,9 +69,59 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
     }
     p.qps = (nq + p.splits - 1) / p.splits;
     p.splits = (nq + p.qps - 1) / p.qps;
+    p.dma = 0;
+    p.PD = 0;
     return p;
 }
 
+// LDS bytes of one ring slot of coli_gemv_dma (mirrors DmaGeom in gemv_dma.hip).
+static int dma_slot_bytes(int kind, int R, int max_rows) {
+    const int sb = kind == COLI_KIND_I4_F ? 256 : (kind == COLI_KIND_FP4 ? 64 : 128);
+    const int per = 256 / sb;
+    const int scale_inst = (R + per - 1) / per;
+    const int nxr = max_rows <= 1 ? 1 : (max_rows <= 4 ? 4 : (max_rows <= 8 ? 8 : 16));
+    return R * COLI_TILE_BYTES + scale_inst * 256 + 2 * nxr * 256;
+}
+
+// Decomposition of the LDS-ring GEMV (gemv_dma.hip): one group of 8 waves per
+// row block over the full K (no split). R row tiles per wave: one while the
+// row tiles alone give about one group per CU (long-K, narrow-O shapes), two
+// beyond that, four when there are many more and the batch tile is full; the
+// ring is 3 stages deep for one tile, 2 for more. Returns false when the GEMV
+// should stay on coli_gemv_tiles: rows too few to put one group on every CU
+// (its K split fills the chip instead), or no decomposition fits the LDS.
+static bool plan_dma(const DevCtx *ctx, GemvLaunchPlan &p, int kind, int nprob, int n_bt, int nrt, int nq, bool dual,
+                     int max_rows) {
+    const long cus = ctx && ctx->cu_count ? ctx->cu_count : 256;
+    const long tiles = (long)nprob * n_bt * nrt;   // (gate, up) pairs for dual
+    int force = 0;   // COLI_HIP_GEMV=dma|tiles pins the kernel (tuning and tests)
+    if (const char *f = std::getenv("COLI_HIP_GEMV"))
+        force = std::strcmp(f, "dma") == 0 ? 1 : (std::strcmp(f, "tiles") == 0 ? -1 : 0);
+    if (force < 0 || max_rows > 16 || nq < 1) return false;
+    // above four rows the staged activation block outweighs the tiles it feeds
+    if (force == 0 && max_rows > 4) return false;
+    if (force == 0 && tiles < cus) return false;
+    int RT = 1;
+    if (tiles >= 2 * cus) RT = 2;
+    if (!dual && tiles >= 2 * cus && max_rows > 8) RT = 4;
+    if (dual) RT = std::min(RT, 2);
+    for (; RT >= 1; RT /= 2) {
+        const int R = dual ? 2 * RT : RT;
+        for (int PD = (R == 1 ? 3 : 2); PD >= 2; PD--) {
+            if (8L * PD * dma_slot_bytes(kind, R, max_rows) <= 160 * 1024) {
+                p.R = R;
+                p.W = 8;
+                p.PD = PD;
+                p.dma = 1;
+                p.rbpp = (nrt + RT - 1) / RT;
+                p.splits = 1;
+                p.qps = nq;
+                return true;
+            }
+        }
+    }
+    return false;
+}
 
 static int ngp_of(int K) { return (K + 127) / 128 * 4; }
 
@@ -100,6 +150,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
     GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
+    plan_dma(ctx, pl, kind, nprob, n_bt, nrt, nq, dual, max_rows);
     size_t inst = (size_t)nprob * n_bt * pl.rbpp;
     if (pl.splits > 1 && (!reserve(ctx, &ctx->partial, inst * pl.splits * pl.R * 4 * 64 * sizeof(float), 0) ||
                           !reserve(ctx, &ctx->split_cnt, inst * sizeof(int), 1)))
@@ -133,6 +184,8 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.ldo = ldo;
     a.partial = (float *)ctx->partial.p;
     a.split_cnt = (int *)ctx->split_cnt.p;
+    if (pl.dma) return hip_ok(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.PD, max_rows, ctx->stream),
+                              "gemv launch");
     return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
 }
 

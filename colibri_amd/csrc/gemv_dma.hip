@@ -1,0 +1,348 @@
+// gemv_dma.hip -- the decode GEMV with weights streamed through an LDS ring.
+//
+// Same problem, data layout and arithmetic as coli_gemv_tiles (gemv.hip):
+// y[b, o] = sum_g scale[o, g] * sum_{k in g} x[b, k] * w[o, k], one
+// v_mfma_f32_16x16x32_f16 per 32-column group with the weights unpacked to
+// exact fp16 in registers, the group scale applied to the MFMA result, K split
+// across the W waves of a workgroup and summed in fixed wave order. Results
+// are bitwise identical to coli_gemv_tiles for the same decomposition.
+//
+// What differs is how the bytes arrive. Every load of the main loop is an
+// LDS DMA (global_load_lds_dword / _dwordx4): the weight tiles (one 1 KiB
+// dwordx4 per tile), the tile scales and the activation fragments of the
+// stage go straight into a per-wave ring of PD slots, so
+//  * the depth of the prefetch costs LDS, not VGPRs;
+//  * the loop waits with exact s_waitcnt vmcnt(N) of its own (the compiler
+//    neither tracks nor reorders these loads), and past a wave's last quad it
+//    issues nothing: no tile is fetched twice and no wave re-reads a shared
+//    zero tile at its tail (thousands of such reads of one address serialize
+//    on one L2 channel);
+//  * a group needs no split of K across workgroups: long-K narrow-O shapes
+//    use one row tile per group and eight waves over K (no partials, no
+//    arrival counter, no tail of dependent round trips).
+// Activation fragments of one batch row (every problem of the launch has one
+// row) arrive as one 256 B dword DMA per stage and are read as a broadcast.
+// For more rows, each dwordx4 DMA stages four rows of the quad (1 KiB); lane
+// l of the DMA fetches 16 B chunk (l % 16) ^ row of row l / 16, so the
+// sixteen lanes of one k-slice read sixteen different bank groups (the
+// A-operand reads are free of bank conflicts). The ring always reserves room
+// for the lo fragments; they are fetched only when the fragment set has any.
+#include "coli_hip_internal.h"
+
+#include <math.h>
+
+#include <type_traits>
+
+#include "coli_device.h"
+
+typedef __attribute__((address_space(3))) void lds_void;
+// LDS written by the DMA is invisible to the compiler's memory model: read it
+// through volatile pointers so no read is folded or reordered across a wait.
+#define LDS_RD(T, p) (*(const volatile __attribute__((address_space(3))) T *)(lds_void *)(p))
+
+// Scale bytes of one tile quad: 16 rows x 4 groups of fp16 / f32 / e8m0.
+template <int KIND> struct ScaleGeom {
+    static constexpr int kBytes = ScaleRegs<KIND>::kTileBytes;   // 128 / 256 / 64
+    static constexpr int kLanes = kBytes / 4;                      // dword lanes per tile
+    static constexpr int kPerInst = 64 / kLanes;                   // tiles per dword DMA
+};
+
+template <int KIND>
+__device__ __forceinline__ void scale_from_lds(ScaleRegs<KIND> &s, const uint8_t *p, int r16) {
+    if constexpr (KIND == COLI_KIND_I4_H) s.v = LDS_RD(u32x2, p + r16 * 8);
+    else if constexpr (KIND == COLI_KIND_I4_F) s.v = LDS_RD(floatx4, p + r16 * 16);
+    else s.v = LDS_RD(uint32_t, p + r16 * 4);
+}
+
+// Wait until at most `pend` (0 .. PD-2) stages of L loads are still in flight.
+template <int L, int PD>
+__device__ __forceinline__ void dma_wait_tail(int pend) {
+#define COLI_WT(k)                                                         \
+    if (pend == k) {                                                       \
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(k * L) : "memory");       \
+        return;                                                            \
+    }
+    if constexpr (PD > 4) { COLI_WT(3) }
+    if constexpr (PD > 3) { COLI_WT(2) }
+    if constexpr (PD > 2) { COLI_WT(1) }
+#undef COLI_WT
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// NXR: batch rows staged per problem and stage (1, 4, 8 or 16).
+template <int KIND, int R, int NXR>
+struct DmaGeom {
+    static constexpr int kScaleOff = R * COLI_TILE_BYTES;
+    static constexpr int kScaleInst = (R + ScaleGeom<KIND>::kPerInst - 1) / ScaleGeom<KIND>::kPerInst;
+    static constexpr int kXOff = kScaleOff + kScaleInst * 256;
+    static constexpr int kXInst = NXR == 1 ? 1 : NXR / 4;   // DMA instructions per fragment half
+    static constexpr int kXBytes = NXR * 256;
+    static constexpr int kSlot = kXOff + 2 * kXBytes;     // room for hi + lo
+    static constexpr int loads(bool lo) { return R + kScaleInst + kXInst * (lo ? 2 : 1); }
+};
+
+// INL: the single problem a.prob0 (3-D grid: row block, 1, batch tile).
+template <int KIND, int R, bool DUAL, int NB4, int W, int PD, int NXR, bool INL>
+__global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
+    using G = DmaGeom<KIND, R, NXR>;
+    constexpr bool XF = NXR > 1;
+    constexpr int RT = DUAL ? R / 2 : R;
+    constexpr int RING = W * PD * G::kSlot;
+    constexpr int RED = W * R * NB4 * 64 * 4;
+    static_assert(RING <= 160 * 1024 && RED <= 160 * 1024, "LDS budget");
+    static_assert((PD - 1) * G::loads(true) <= 63, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[RING > RED ? RING : RED];
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int p = 0, bt, rb;
+    if constexpr (INL) {
+        rb = blockIdx.x;
+        bt = blockIdx.z;
+    } else {
+        const int item = blockIdx.x;
+        const int items_per_p = a.n_bt * a.rb_per_prob;
+        p = item / items_per_p;
+        if (p >= a.nprob) return;
+        if (a.nprob_dev && p >= *a.nprob_dev) return;
+        const int rem = item - p * items_per_p;
+        bt = rem / a.rb_per_prob;
+        rb = rem - bt * a.rb_per_prob;
+    }
+    const ColiProb pr = uniform_prob(INL ? a.prob0 : a.prob[p]);
+    const int nb = min(16, pr.nrows - 16 * bt);
+    if constexpr (!INL) {
+        if (nb <= 0) return;
+    }
+    const int b = lane & 15, ks = lane >> 4;
+    const int nq = a.nq;
+    const int q_first = wave;
+    const int nit = q_first < nq ? (nq - q_first + W - 1) / W : 0;
+
+    // row tiles of this group (dead ones read the zero tile, whose scales are zero)
+    int rt[R];
+    bool live[R];
+    const uint8_t *wr[R], *sr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int rr = DUAL ? (r % RT) : r;
+        rt[r] = rb * RT + rr;
+        live[r] = rt[r] < a.nrt;
+        const bool second = DUAL && r >= RT;
+        const size_t t0 = (size_t)(uint32_t)min(rt[r], a.nrt - 1) * (uint32_t)nq;
+        wr[r] = live[r] ? (second ? pr.w1 : pr.w0) + t0 * COLI_TILE_BYTES : (const uint8_t *)a.zero;
+        sr[r] = live[r] ? (const uint8_t *)(second ? pr.s1 : pr.s0) + t0 * ScaleGeom<KIND>::kBytes
+                        : (const uint8_t *)a.zero;
+    }
+    // per-lane activation source of the DMA: NXR > 1: row 4k + lane/16 of
+    // the batch tile (clamped to the last real row) for instruction k, chunk
+    // (lane % 16) ^ row; else the problem's one row, 4 bytes per lane
+    const uint8_t *xsrc_hi[G::kXInst], *xsrc_lo[G::kXInst];
+#pragma unroll
+    for (int k = 0; k < G::kXInst; k++) {
+        const int brow = XF ? min(4 * k + (lane >> 4), nb - 1) : 0;
+        const int br = pr.xrow_off + 16 * bt + brow;
+        const int fr = a.xrows ? a.xrows[br] : br;
+        const size_t off = (size_t)fr * a.xstride * 2 + (XF ? (((lane & 15) ^ (4 * k + (lane >> 4))) * 16) : lane * 4);
+        xsrc_hi[k] = (const uint8_t *)a.xhi + off;
+        xsrc_lo[k] = (const uint8_t *)a.xlo + off;
+    }
+    uint8_t *ring = lds + wave * PD * G::kSlot;
+    // the ring is written behind the compiler's back: let it escape, so the
+    // "memory" clobbers of the waits below force fresh reads
+    asm volatile("" ::"v"(lds) : "memory");
+
+    auto issue = [&](int it, int slot, bool lo) {
+        const int q = q_first + it * W;
+        uint8_t *dst = ring + slot * G::kSlot;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            __builtin_amdgcn_global_load_lds((const void *)(wr[r] + (size_t)(live[r] ? q : 0) * COLI_TILE_BYTES + lane * 16),
+                                             (lds_void *)(dst + r * COLI_TILE_BYTES), 16, 0, 0);
+#pragma unroll
+        for (int k = 0; k < G::kScaleInst; k++) {
+            constexpr int LPT = ScaleGeom<KIND>::kLanes;
+            const int r = min(R - 1, k * ScaleGeom<KIND>::kPerInst + lane / LPT);
+            // (branch-free: a per-lane select between R scalar bases)
+            const uint8_t *base = sr[0];
+            size_t qo = live[0] ? (size_t)q * ScaleGeom<KIND>::kBytes : 0;
+#pragma unroll
+            for (int rr = 1; rr < R; rr++) {
+                if (r == rr) {
+                    base = sr[rr];
+                    qo = live[rr] ? (size_t)q * ScaleGeom<KIND>::kBytes : 0;
+                }
+            }
+            __builtin_amdgcn_global_load_lds((const void *)(base + qo + (lane % LPT) * 4),
+                                             (lds_void *)(dst + G::kScaleOff + k * 256), 4, 0, 0);
+        }
+        const size_t xo = (size_t)q * 256;
+        auto xdma = [&](const uint8_t *src, int off) {
+            if constexpr (NXR > 1) __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(dst + off), 16, 0, 0);
+            else __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(dst + off), 4, 0, 0);
+        };
+        constexpr int xb = NXR > 1 ? 1024 : 256;   // bytes per DMA instruction
+#pragma unroll
+        for (int k = 0; k < G::kXInst; k++) xdma(xsrc_hi[k] + xo, G::kXOff + k * xb);
+        if (lo) {
+#pragma unroll
+            for (int k = 0; k < G::kXInst; k++) xdma(xsrc_lo[k] + xo, G::kXOff + G::kXBytes + k * xb);
+        }
+    };
+
+    floatx4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    // A operand of lane (b, ks), group j: chunk 4j + ks of row min(b, nb-1)
+    // (swizzled by the row when NXR > 1; one row read as a broadcast else)
+    const int xrow = XF ? min(b, nb - 1) : 0;
+    auto xaddr = [&](int j) -> uint32_t {
+        return XF ? (uint32_t)(xrow * 16 + ((4 * j + ks) ^ xrow)) * 16 : (uint32_t)(j * 64 + ks * 16);
+    };
+
+    auto compute = [&](int slot, auto lo_tag) {
+        constexpr bool LO = decltype(lo_tag)::value;
+        const uint8_t *src = ring + slot * G::kSlot;
+        u32x4 w[R];
+        ScaleRegs<KIND> sc[R];
+        half8v xh[4], xl[LO ? 4 : 1];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            xh[j] = LDS_RD(half8v, src + G::kXOff + xaddr(j));
+            if constexpr (LO) xl[j] = LDS_RD(half8v, src + G::kXOff + G::kXBytes + xaddr(j));
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = LDS_RD(u32x4, src + r * COLI_TILE_BYTES + lane * 16);
+            scale_from_lds<KIND>(sc[r], src + G::kScaleOff + r * ScaleGeom<KIND>::kBytes, lane & 15);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const half8v bw = unpack_b<KIND>(w[r][j]);
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
+                const float scl = sc[r].get(j);
+#pragma unroll
+                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
+            }
+        }
+    };
+
+    auto run = [&](auto lo_tag) {
+        constexpr bool LO = decltype(lo_tag)::value;
+        constexpr int L = G::loads(LO);
+#pragma unroll
+        for (int s = 0; s < PD - 1; s++)
+            if (s < nit) issue(s, s, LO);
+        for (int it0 = 0; it0 < nit; it0 += PD) {
+#pragma unroll
+            for (int u = 0; u < PD; u++) {
+                const int it = it0 + u;
+                if (it >= nit) break;
+                if (it + PD - 1 < nit) {
+                    issue(it + PD - 1, (u + PD - 1) % PD, LO);
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PD - 1) * L) : "memory");
+                } else {
+                    dma_wait_tail<L, PD>(nit - 1 - it);
+                }
+                compute(u, lo_tag);
+            }
+        }
+    };
+    if (*a.haslo >= a.lo_gen) run(std::true_type{});   // >=: stays correct under graph replay
+    else run(std::false_type{});
+
+    // exponent of the batch row this wave finishes
+    int E_out = 0;
+    if (wave < NB4) {
+        const int brow = ks * 4 + wave;
+        if (brow < nb) {
+            const int br = pr.xrow_off + 16 * bt + brow;
+            E_out = a.xexp[a.xrows ? a.xrows[br] : br];
+        }
+    }
+    // ---- reduction in fixed wave order through the (drained) ring ----
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    float *red = (float *)lds;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < NB4; i++) red[((wave * R + r) * NB4 + i) * 64 + lane] = acc[r][i];
+    __syncthreads();
+    const int i = wave;
+    if (i >= NB4) return;
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float t = red[(r * NB4 + i) * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < W; w++) t += red[((w * R + r) * NB4 + i) * 64 + lane];
+        v[r] = t;
+    }
+    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, ks * 4 + i, lane, E_out);
+}
+
+// ---------------------------------------------------------------------------
+// launcher
+// ---------------------------------------------------------------------------
+template <int KIND, int R, bool DUAL, int NB4, int PD, int NXR>
+static hipError_t launch_dma4(const ColiGemvArgs &a, int blocks, hipStream_t st) {
+    constexpr int W = 8;
+    if constexpr (W * PD * DmaGeom<KIND, R, NXR>::kSlot > 160 * 1024) {
+        return hipErrorInvalidConfiguration;
+    } else {
+        if (!a.prob)
+            hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, true>), dim3(a.rb_per_prob, 1, a.n_bt),
+                               dim3(64 * W), 0, st, a);
+        else
+            hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, false>), dim3(blocks), dim3(64 * W), 0,
+                               st, a);
+        return hipGetLastError();
+    }
+}
+
+template <int KIND, int R, bool DUAL, int NB4, int NXR>
+static hipError_t launch_dma3(const ColiGemvArgs &a, int PD, int blocks, hipStream_t st) {
+    if (PD == 2) return launch_dma4<KIND, R, DUAL, NB4, 2, NXR>(a, blocks, st);
+    return launch_dma4<KIND, R, DUAL, NB4, 3, NXR>(a, blocks, st);
+}
+
+template <int KIND, int R, bool DUAL>
+static hipError_t launch_dma2(const ColiGemvArgs &a, int max_rows, int PD, int blocks, hipStream_t st) {
+    if (max_rows <= 1) return launch_dma3<KIND, R, DUAL, 1, 1>(a, PD, blocks, st);
+    if (max_rows <= 2) return launch_dma3<KIND, R, DUAL, 2, 4>(a, PD, blocks, st);
+    if (max_rows <= 4) return launch_dma3<KIND, R, DUAL, 4, 4>(a, PD, blocks, st);
+    if (max_rows <= 8) return launch_dma3<KIND, R, DUAL, 4, 8>(a, PD, blocks, st);
+    return launch_dma3<KIND, R, DUAL, 4, 16>(a, PD, blocks, st);
+}
+
+template <int KIND>
+static hipError_t launch_dma1(const ColiGemvArgs &a, int R, bool dual, int max_rows, int PD, int blocks,
+                              hipStream_t st) {
+    if (dual) {
+        if (R == 4) return launch_dma2<KIND, 4, true>(a, max_rows, PD, blocks, st);
+        return launch_dma2<KIND, 2, true>(a, max_rows, PD, blocks, st);
+    }
+    if (R == 4) return launch_dma2<KIND, 4, false>(a, max_rows, PD, blocks, st);
+    if (R == 2) return launch_dma2<KIND, 2, false>(a, max_rows, PD, blocks, st);
+    return launch_dma2<KIND, 1, false>(a, max_rows, PD, blocks, st);
+}
+
+// Returns hipErrorInvalidConfiguration for a decomposition the ring cannot
+// hold (the caller then uses coli_gemv_tiles).
+extern "C" hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual, int PD, int max_rows,
+                                           hipStream_t st) {
+    if (a->splits != 1 || max_rows < 1 || max_rows > 16) return hipErrorInvalidValue;
+    if (!a->prob && (a->nprob != 1 || a->nprob_dev)) return hipErrorInvalidValue;
+    const long items = (long)a->nprob * a->n_bt * a->rb_per_prob;
+    if (items <= 0) return hipSuccess;
+    const int blocks = (int)items;
+    switch (kind) {
+    case COLI_KIND_I4_H: return launch_dma1<COLI_KIND_I4_H>(*a, R, dual, max_rows, PD, blocks, st);
+    case COLI_KIND_I4_F: return launch_dma1<COLI_KIND_I4_F>(*a, R, dual, max_rows, PD, blocks, st);
+    case COLI_KIND_FP4: return launch_dma1<COLI_KIND_FP4>(*a, R, dual, max_rows, PD, blocks, st);
+    default: return hipErrorInvalidValue;
+    }
+}
