@@ -453,6 +453,16 @@ def main():
             tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
                            w_std=1.0 / math.sqrt(7168))
             for fmt, tag in ((7, "mxfp4"), (4, "int4"))}
+        # the opt-in MXFP4 GEMM on the block-scaled MFMA (COLI_HIP_MX=1; not
+        # fp32-exact: the hardware's per-block summation error is ~2^-15 of the
+        # block's magnitude sum)
+        os.environ["COLI_HIP_MX"] = "1"
+        try:
+            out["moe_layer"]["configs[4]_kimi_prefill_512"]["mxfp4_block_scaled_mfma_optin"] = bench.moe(
+                "kimi", 7, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+                w_std=1.0 / math.sqrt(7168))
+        finally:
+            del os.environ["COLI_HIP_MX"]
     if not args.skip_cpu:
         out["cpu_baseline"] = bench.cpu_baseline()
     bench.close()

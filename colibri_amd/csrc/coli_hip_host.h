@@ -18,6 +18,9 @@ struct DevBuf {
 struct FragSet {
     DevBuf hi, lo, exp;
     int gen = 0;      // generation of the last prep (see coli_prep_frag)
+    DevBuf p8, s8;    // e4m3 pieces + e8m0 scales for the MXFP4 GEMM (coli_prep_fp8)
+    int prow = 0;     // rows per piece plane
+    int gen8 = 0;     // generation of the last piece prep (flag slot 8 + set)
 };
 
 struct DevCtx {
@@ -65,6 +68,10 @@ hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, co
                                  int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
                                  int *exp2out, int *haslo, int gen, const void *zero, hipStream_t st);
 hipError_t coli_launch_gemm(int kind, int dual, const ColiGemmArgs *a, hipStream_t st);
+hipError_t coli_launch_gemm_mx(int dual, const ColiGemmMxArgs *a, hipStream_t st);
+hipError_t coli_launch_prep_fp8(const float *x, int ldx, const int *src_row, const int *nrows_dev, int nrows, int K,
+                                int nq, int prow, uint8_t *p8, uint8_t *s8, int *more, int gen, hipStream_t st);
+int coli_mx_pieces(void);
 hipError_t coli_launch_repack(const ColiCudaTensor *t, const uint8_t *src_w, const void *src_s,
                               hipStream_t st);
 hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const float *x, int ldx, float *y, int ldy,
@@ -102,6 +109,11 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
 int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
                const int *src_rows = nullptr, const int *nrows_dev = nullptr);
 int frag_set_of(int kind, bool hidden);
+// Activation pieces of the MXFP4 grouped GEMM (e4m3 + e8m0 per 32 columns)
+// of the same rows, into fragment set `set`.
+bool mx_gemm_enabled();
+int make_frags8(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, const int *src_rows = nullptr,
+                const int *nrows_dev = nullptr);
 // One tiled GEMV over `nprob` problems (descriptors on the device, or one
 // inline problem) reading fragment set `set`.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,

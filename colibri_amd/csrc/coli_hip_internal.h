@@ -105,5 +105,27 @@ struct ColiGemmArgs {
     int ldo;
 };
 
+// Grouped MXFP4 GEMM on the block-scaled MFMA (gemm_mx.hip): activations as
+// e4m3 pieces with e8m0 scales per 32 columns (coli_prep_fp8).
+struct ColiGemmMxArgs {
+    const ColiProb *prob;
+    const int *nprob_dev;
+    int nprob;
+    const int *mt_list;
+    const int *n_mt_dev;
+    int n_mt;
+    int nrt, nq, O;
+    int rb_per_prob;
+    const int *xrows;          // piece row of batch row r = xrows[xrow_off + r] (null: xrow_off + r)
+    const uint8_t *p8;         // [NP][prow][nq][128] permuted e4m3 codes
+    const uint32_t *s8;        // [NP][prow][nq] e8m0 bytes of the quad's 4 blocks
+    int prow;                  // rows per piece plane
+    const int *more;           // >= more_gen: some block needs all pieces (else two)
+    int more_gen;
+    const uint8_t *zero;
+    float *out;
+    int ldo;
+};
+
 // Numeric helpers shared by host and device.
 static inline int coli_ceil_div(int a, int b) { return (a + b - 1) / b; }

@@ -143,6 +143,31 @@ int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, i
                   "fragment prep");
 }
 
+// Many-row MXFP4 problems run the exact fp16-MFMA grouped GEMM by default.
+// COLI_HIP_MX=1 selects the block-scaled MFMA GEMM (gemm_mx.hip): faster,
+// but the hardware sums each 128-column block of e4m3 x e2m1 products with
+// about 2^-15 of the block's magnitude sum as error (measured), so results
+// carry ~3e-5 relative error (median) instead of fp32 accuracy.
+bool mx_gemm_enabled() {
+    const char *e = std::getenv("COLI_HIP_MX");
+    return e && e[0] == '1';
+}
+
+int make_frags8(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, const int *src_rows,
+                const int *nrows_dev) {
+    FragSet &f = ctx->frag[set];
+    const int nq = (K + 127) / 128, np = coli_mx_pieces();
+    if (!reserve(ctx, &f.p8, (size_t)np * nrows * nq * 128, 0) || !reserve(ctx, &f.s8, (size_t)np * nrows * nq * 4, 0))
+        return 0;
+    f.prow = nrows;
+    int *flag = (int *)ctx->flags.p + 8 + set;
+    f.gen8 = f.gen8 == 0x7fffffff ? 1 : f.gen8 + 1;
+    if (f.gen8 == 1 && !hip_ok(coli_launch_zero_i32(flag, 1, ctx->stream), "piece flag")) return 0;
+    return hip_ok(coli_launch_prep_fp8(x, ld, src_rows, nrows_dev, nrows, K, nq, nrows, (uint8_t *)f.p8.p,
+                                       (uint8_t *)f.s8.p, flag, f.gen8, ctx->stream),
+                  "fp8 activation pieces");
+}
+
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
@@ -197,6 +222,30 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
              const int *xrows_dev, float *out, int ldo) {
     if (n_mt <= 0) return 1;
     FragSet &f = ctx->frag[set];
+    if (kind == COLI_KIND_FP4 && mx_gemm_enabled()) {
+        ColiGemmMxArgs m;
+        std::memset(&m, 0, sizeof(m));
+        m.prob = probs_dev;
+        m.nprob_dev = nprob_dev;
+        m.nprob = nprob;
+        m.mt_list = mt_list_dev;
+        m.n_mt_dev = n_mt_dev;
+        m.n_mt = n_mt;
+        m.nrt = nrt;
+        m.nq = nq;
+        m.O = O;
+        m.rb_per_prob = (nrt + COLI_GM_WAVES * (dual ? 1 : 2) - 1) / (COLI_GM_WAVES * (dual ? 1 : 2));
+        m.xrows = xrows_dev;
+        m.p8 = (const uint8_t *)f.p8.p;
+        m.s8 = (const uint32_t *)f.s8.p;
+        m.prow = f.prow;
+        m.more = (const int *)ctx->flags.p + 8 + set;
+        m.more_gen = f.gen8;
+        m.zero = (const uint8_t *)ctx->zeros.p;
+        m.out = out;
+        m.ldo = ldo;
+        return hip_ok(coli_launch_gemm_mx(dual ? 1 : 0, &m, ctx->stream), "gemm launch");
+    }
     ColiGemmArgs a;
     std::memset(&a, 0, sizeof(a));
     a.prob = probs_dev;
@@ -264,9 +313,14 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
     if (need_gu && (!reserve(ctx, &ctx->g, (size_t)total * I * sizeof(float), 0) ||
                     !reserve(ctx, &ctx->u, (size_t)total * I * sizeof(float), 0)))
         return 0;
-    for (int o = 0; o < 2; o++)
-        if (need_x[o] && !make_frags(ctx, frag_set_of(o ? COLI_KIND_FP4 : 0, false), x_dev, D, total, D, !o))
+    // many-row MXFP4 members run the block-scaled MFMA GEMM on e4m3 pieces
+    const bool mx_gemm = max_rows > COLI_GEMM_MIN_ROWS && mx_gemm_enabled();
+    for (int o = 0; o < 2; o++) {
+        const int set = frag_set_of(o ? COLI_KIND_FP4 : 0, false);
+        if (need_x[o] && !((o && mx_gemm) ? make_frags8(ctx, set, x_dev, D, total, D)
+                                          : make_frags(ctx, set, x_dev, D, total, D, !o)))
             return 0;
+    }
 
     // descriptors: [dual by kind][split gate/up][down by kind]
     std::vector<ColiProb> probs;
@@ -364,8 +418,12 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
             return 0;
     }
     // down
-    for (int o = 0; o < 2; o++)
-        if (need_h[o] && !make_frags(ctx, frag_set_of(o ? COLI_KIND_FP4 : 0, true), h, I, total, I, !o)) return 0;
+    for (int o = 0; o < 2; o++) {
+        const int set = frag_set_of(o ? COLI_KIND_FP4 : 0, true);
+        if (need_h[o] &&
+            !((o && mx_gemm) ? make_frags8(ctx, set, h, I, total, I) : make_frags(ctx, set, h, I, total, I, !o)))
+            return 0;
+    }
     for (size_t l = 0; l < launches.size(); l++) {
         if (launches[l].first < down_first) continue;
         if (!launch(l, false)) return 0;

@@ -267,8 +267,10 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     const int fx = frag_set_of(m->kind, false), fh = frag_set_of(m->kind, true);
     const int int4 = m->kind != COLI_KIND_FP4;
     hipStream_t st = ctx->stream;
+    // many-row MXFP4 layers run the block-scaled MFMA GEMM on e4m3 pieces
+    const bool gemm = S > COLI_GEMM_MIN_ROWS, mx = gemm && m->kind == COLI_KIND_FP4 && mx_gemm_enabled();
     // 1. activation fragments, 2-3. router
-    if (!make_frags(ctx, fx, x_dev, c.D, S, c.D, int4)) return 0;
+    if (!(mx ? make_frags8(ctx, fx, x_dev, c.D, S, c.D) : make_frags(ctx, fx, x_dev, c.D, S, c.D, int4))) return 0;
     const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
     if (!nch || !hip_ok(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
                                                   c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, st),
@@ -280,7 +282,6 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
                        m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state);
     if (!hip_ok(hipGetLastError(), "moe union")) return 0;
     // 5. gate/up + SwiGLU over the union, 6. hidden fragments, 7. down
-    const bool gemm = S > COLI_GEMM_MIN_ROWS;
     const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
     if (gemm) {
         if (!run_gemm(ctx, m->kind, true, m->pdual, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_i, nq_d,
@@ -289,7 +290,9 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I)) {
         return 0;
     }
-    if (!make_frags(ctx, fh, m->h, c.I, rows, c.I, int4, nullptr, m->state + 1)) return 0;
+    if (!(mx ? make_frags8(ctx, fh, m->h, c.I, rows, c.I, nullptr, m->state + 1)
+             : make_frags(ctx, fh, m->h, c.I, rows, c.I, int4, nullptr, m->state + 1)))
+        return 0;
     if (gemm) {
         if (!run_gemm(ctx, m->kind, false, m->pdown, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_d, nq_i,
                       c.D, fh, nullptr, m->y, c.D))

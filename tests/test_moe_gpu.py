@@ -272,3 +272,32 @@ def test_expert_group_grouped_gemm(session, fmt, lo):
                 session.free(t)
     ref = group_reference(layer, x, [0, 1, 2], rows)
     assert rel_err(y, ref, group_mag(layer, x, [0, 1, 2], rows)).max() <= TOL
+
+
+@pytest.mark.parametrize("D,I,rows,lo", [(384, 256, [70, 3, 129], False), (384, 256, [70, 3, 129], True),
+                                         (2048, 512, [96, 40], True)])
+def test_expert_group_block_scaled_mfma(session, monkeypatch, D, I, rows, lo):
+    """The opt-in MXFP4 grouped GEMM on v_mfma_scale_f32_16x16x128_f8f6f4
+    (COLI_HIP_MX=1): activations as e4m3 pieces with e8m0 scales per 32
+    columns, weights and both block scales consumed by the hardware. Its
+    accuracy is bounded by the MFMA itself, which sums each 128-column block
+    of products with an error of about 2^-15 of the block's magnitude sum
+    (measured with exact fp8/fp4 operands): the bound checked here is 2e-4 of
+    the down projection's magnitude sum sum_k |h_k w_k|, against fp32-exact
+    parity of the default path (test_expert_group_grouped_gemm)."""
+    monkeypatch.setenv("COLI_HIP_MX", "1")
+    rng = np.random.default_rng(700 + D + 10 * lo)
+    layer = Layer(rng, 7, D, I, len(rows))
+    hs = layer.upload(session)
+    x = rng.standard_normal((sum(rows), D)).astype(np.float32) if lo else rand_x(rng, sum(rows), D)
+    try:
+        y = session.expert_group([h[0] for h in hs], [h[1] for h in hs], [h[2] for h in hs], rows, x)
+    finally:
+        for h in hs:
+            for t in h:
+                session.free(t)
+    members = list(range(len(rows)))
+    ref = group_reference(layer, x, members, rows)
+    mag = group_mag(layer, x, members, rows)
+    err = np.abs(y.astype(np.float64) - ref) / mag
+    assert err.max() <= 2e-4, f"block-scaled MFMA error {err.max():.3g} of the magnitude sum"
