@@ -379,7 +379,7 @@ def measured_traffic():
     """HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE runs (scaled by a calibration copy of known size); None when
     that profile is absent."""
-    path = os.path.join(ROOT, "profiles", "coli_gemv_tiles_dense_int4_traffic.json")
+    path = os.path.join(ROOT, "profiles", "coli_gemv_dense_int4_traffic.json")
     try:
         with open(path) as f:
             return int(json.load(f)["traffic_bytes_per_launch"])
@@ -429,7 +429,7 @@ def main():
         "frac_of_peak": round(r["value"] / PEAK_GBS, 3),
         "roofline": {"bound": "hbm", "achieved": round(r["kern_gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["kern_gbs"] / PEAK_GBS, 3), "traffic": measured_traffic(),
-                     "kernel": "coli_gemv_tiles", "avg_launch_us": round(r["kern_avg_us"], 2),
+                     "kernel": "coli_gemv_dma (B1, B4) + coli_gemv_tiles (B8, B16)", "avg_launch_us": round(r["kern_avg_us"], 2),
                      "avg_launch_bytes": int(r["kern_avg_bytes"])},
         "gemv_by_batch": r["by_batch"],
     }
