@@ -77,6 +77,7 @@ hipError_t coli_launch_repack(const ColiCudaTensor *t, const uint8_t *src_w, con
 hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const float *x, int ldx, float *y, int ldy,
                                   int S, hipStream_t st);
 hipError_t coli_launch_qdq_e4m3(const float *x, float *y, int S, int K, hipStream_t st);
+hipError_t coli_launch_qdq_i8(const float *x, float *y, int S, int K, hipStream_t st);
 int coli_router_chunks(int D);   // column chunks of the router partials
 hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E, float *part,
                                      hipStream_t st);

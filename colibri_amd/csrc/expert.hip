@@ -618,9 +618,12 @@ static int gemm_host(DevCtx *ctx, ColiCudaTensor *t, float *y, const float *x, i
     if (!hip_ok(hipMemcpyAsync(ctx->x.p, ctx->host_x, xb, hipMemcpyHostToDevice, ctx->stream), "input upload"))
         return 0;
     const float *xin = (const float *)ctx->x.p;
-    if (qdq) {
+    // qdq 1: e4m3 per 128 (native_quant contract); 2: int8 per 32 (matmul_mxfp4_i8)
+    if (qdq == 1 || (qdq == 2 && t->I % 32 == 0)) {
         if (!reserve(ctx, &ctx->qdq, xb, 0) ||
-            !hip_ok(coli_launch_qdq_e4m3(xin, (float *)ctx->qdq.p, S, t->I, ctx->stream), "activation qdq"))
+            !hip_ok(qdq == 1 ? coli_launch_qdq_e4m3(xin, (float *)ctx->qdq.p, S, t->I, ctx->stream)
+                             : coli_launch_qdq_i8(xin, (float *)ctx->qdq.p, S, t->I, ctx->stream),
+                    "activation qdq"))
             return 0;
         xin = (const float *)ctx->qdq.p;
     }
@@ -646,9 +649,8 @@ extern "C" int coli_cuda_matmul(ColiCudaTensor **tensor, float *y, const float *
     return gemm_host(ctx, t, y, x, S, 0);
 }
 
-extern "C" int coli_cuda_matmul_mxfp4(float *y, const float *x, const unsigned char *q4, const unsigned char *e8s,
-                                      int S, int I, int O) {
-    if (fault_injected()) return 0;
+static int matmul_mxfp4_stateless(float *y, const float *x, const unsigned char *q4, const unsigned char *e8s, int S,
+                                  int I, int O, int qdq) {
     if (S < 1 || I < 1 || O < 1 || !y || !x || !q4 || !e8s) return 0;
     DevCtx *ctx = find_ctx(0);
     if (!select_ctx(ctx)) return 0;
@@ -671,7 +673,44 @@ extern "C" int coli_cuda_matmul_mxfp4(float *y, const float *x, const unsigned c
         !hip_ok(hipMemcpyAsync(ctx->stage_s.p, e8s, ssrc, hipMemcpyHostToDevice, ctx->stream), "mxfp4 scale upload") ||
         !hip_ok(coli_launch_repack(&t, (const uint8_t *)ctx->stage_w.p, ctx->stage_s.p, ctx->stream), "mxfp4 repack"))
         return 0;
-    return gemm_host(ctx, &t, y, x, S, 0);
+    return gemm_host(ctx, &t, y, x, S, qdq);
+}
+
+extern "C" int coli_cuda_matmul_mxfp4(float *y, const float *x, const unsigned char *q4, const unsigned char *e8s,
+                                      int S, int I, int O) {
+    if (fault_injected()) return 0;
+    return matmul_mxfp4_stateless(y, x, q4, e8s, S, I, O, 0);
+}
+
+// matmul_mxfp4_i8 (c/quant.h:1441-1515): the same stateless call with the
+// activations quantized to int8 per 32 columns first (I % 32 != 0: the float
+// path, as the reference falls back).
+extern "C" int coli_hip_matmul_mxfp4_i8(float *y, const float *x, const unsigned char *q4, const unsigned char *e8s,
+                                        int S, int I, int O) {
+    if (fault_injected()) return 0;
+    return matmul_mxfp4_stateless(y, x, q4, e8s, S, I, O, 2);
+}
+
+// Resident-tensor variants of matmul_mxfp4_i8 (host and device buffers).
+extern "C" int coli_hip_fp4_matmul_i8(ColiCudaTensor *t, float *y, const float *x, int S) {
+    if (fault_injected()) return 0;
+    if (!t || t->kind != COLI_KIND_FP4 || !y || !x || S < 1) return 0;
+    DevCtx *ctx = find_ctx(t->device);
+    if (!select_ctx(ctx)) return 0;
+    return gemm_host(ctx, t, y, x, S, 2);
+}
+
+extern "C" int coli_hip_fp4_matmul_i8_dev(ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
+    if (fault_injected()) return 0;
+    if (!t || t->kind != COLI_KIND_FP4 || !y_dev || !x_dev || S < 1) return 0;
+    DevCtx *ctx = find_ctx(t->device);
+    if (!select_ctx(ctx)) return 0;
+    if (t->I % 32) return gemm_dev(ctx, t, y_dev, x_dev, S);
+    size_t xb = (size_t)S * t->I * sizeof(float);
+    if (!reserve(ctx, &ctx->qdq, xb, 0) ||
+        !hip_ok(coli_launch_qdq_i8(x_dev, (float *)ctx->qdq.p, S, t->I, ctx->stream), "activation qdq"))
+        return 0;
+    return gemm_dev(ctx, t, y_dev, (const float *)ctx->qdq.p, S);
 }
 
 extern "C" int coli_hip_fp4_matmul_qdq(ColiCudaTensor *t, float *y, const float *x, int S) {

@@ -583,6 +583,47 @@ __global__ __launch_bounds__(128) void coli_qdq_e4m3(const float *__restrict__ x
 }
 
 // ---------------------------------------------------------------------------
+// int8 activation quantize-dequantize per 32-column group (the activation
+// side of c/quant.h:1441-1515, matmul_mxfp4_i8): sc = max|x| / 127 floored
+// at 1e-20, q = nearest-even integer of x * (1 / sc) clamped to +-127, and
+// the GEMV then reads q * sc. Division, reciprocal and rounding are the
+// correctly rounded IEEE operations the reference uses, so q is bit-exact;
+// q * sc differs from the reference's post-dot scaling by one rounding per
+// element (2^-24 relative).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void coli_qdq_i8(const float *__restrict__ x, float *__restrict__ y, int S, int K) {
+    const int ng = K / 32;
+    const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (long)S * ng) return;
+    const float *xg = x + t * 32;
+    float v[32];
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+        const floatx4 a = *GPTR(floatx4, xg + i);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[i + j] = a[j];
+            am = fmaxf(am, fabsf(a[j]));
+        }
+    }
+    float sc = __fdiv_rn(am, 127.0f);
+    if (sc < 1e-20f) sc = 1e-20f;
+    const float inv = __fdiv_rn(1.0f, sc);
+    float *yg = y + t * 32;
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+        floatx4 o;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float q = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(__fmul_rn(v[i + j], inv))));
+            o[j] = __fmul_rn(q, sc);
+        }
+        *(floatx4 *)(yg + i) = o;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side launchers (called from backend_hip.hip)
 // ---------------------------------------------------------------------------
 struct ColiGemvPlan {
@@ -683,5 +724,12 @@ extern "C" hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const floa
 
 extern "C" hipError_t coli_launch_qdq_e4m3(const float *x, float *y, int S, int K, hipStream_t st) {
     hipLaunchKernelGGL(coli_qdq_e4m3, dim3((K + 127) / 128, S), dim3(128), 0, st, x, y, K);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t coli_launch_qdq_i8(const float *x, float *y, int S, int K, hipStream_t st) {
+    if (K % 32 || S <= 0) return K % 32 ? hipErrorInvalidValue : hipSuccess;
+    const long n = (long)S * (K / 32);
+    hipLaunchKernelGGL(coli_qdq_i8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, S, K);
     return hipGetLastError();
 }

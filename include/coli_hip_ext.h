@@ -44,6 +44,21 @@ int coli_hip_fp4_matmul_qdq(ColiCudaTensor *tensor, float *y, const float *x, in
 /* Same, device pointers, asynchronous on the backend stream. */
 int coli_hip_fp4_matmul_qdq_dev(ColiCudaTensor *tensor, float *y_dev, const float *x_dev, int S);
 
+/* MXFP4 with int8 activations: replaces matmul_mxfp4_i8 (c/quant.h:1441-1515,
+ * the K3 IDOT path selected by K3_IDOT=1, c/kimi_k3.c). Each activation row
+ * is quantized per 32 columns to int8 (sc = max|x| / 127, q = rint(x / sc)
+ * clamped to +-127, bit-exact with the reference) and multiplied with the
+ * MXFP4 weights; I % 32 != 0 falls back to the float path as the reference
+ * does. Stateless like coli_cuda_matmul_mxfp4 (host q4 [O][I/2], e8
+ * [O][I/32]). Returns 1 / 0 (y untouched on failure). */
+int coli_hip_matmul_mxfp4_i8(float *y, const float *x, const unsigned char *q4,
+                             const unsigned char *e8s, int S, int I, int O);
+
+/* Same on a resident MXFP4 tensor: host pointers (synchronous) / device
+ * pointers (asynchronous on the backend stream). */
+int coli_hip_fp4_matmul_i8(ColiCudaTensor *tensor, float *y, const float *x, int S);
+int coli_hip_fp4_matmul_i8_dev(ColiCudaTensor *tensor, float *y_dev, const float *x_dev, int S);
+
 /* ---- fused MoE layer (router -> union -> experts -> SwiGLU -> scatter) ---- */
 typedef struct ColiHipMoe ColiHipMoe;
 

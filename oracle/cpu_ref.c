@@ -300,6 +300,70 @@ int cref_fp4_matmul_batch(float *y, const uint8_t *q4, const uint8_t *e8,
     return 0;
 }
 
+/* MXFP4 with int8 activations (c/quant.h:1441-1515, the K3 IDOT path), AVX2
+ * association: each row's 32-column groups are quantized to int8 with
+ * sc = max|x| / 127 (floored at 1e-20), q = lrint(x * (1 / sc)) clamped to
+ * +-127; the group's integer dot with the doubled e2m1 codes is kept as 8
+ * int32 partials of 4 adjacent columns (maddubs + madd), each converted and
+ * fused into its lane accumulator with the group scale
+ * (mx4_scale(e8) * 0.5f) * sc, and the 8 lanes are summed as hsum256.
+ * I % 32 != 0 falls back to matmul_mxfp4, as the reference does. */
+void cref_matmul_mxfp4_i8(float *y, const float *x, const uint8_t *q4,
+                          const uint8_t *e8, int S, int I, int O) {
+    static const int lut2[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+    if (I % 32) {
+        cref_matmul_mxfp4(y, x, q4, e8, S, I, O);
+        return;
+    }
+    int rb = I / 2, ng = I / 32;
+    int8_t *xq = (int8_t *)malloc((size_t)S * I);
+    float *xsc = (float *)malloc((size_t)S * ng * sizeof(float));
+    if (!xq || !xsc) {
+        free(xq);
+        free(xsc);
+        return;
+    }
+    for (int s = 0; s < S; s++)
+        for (int g = 0; g < ng; g++) {
+            const float *xg = x + (int64_t)s * I + g * 32;
+            float am = 0.0f;
+            for (int i = 0; i < 32; i++) {
+                float a = fabsf(xg[i]);
+                if (a > am) am = a;
+            }
+            float sc = am / 127.f;
+            if (sc < 1e-20f) sc = 1e-20f;
+            xsc[(int64_t)s * ng + g] = sc;
+            float inv = 1.f / sc;
+            for (int i = 0; i < 32; i++) {
+                int v = (int)lrintf(xg[i] * inv);
+                if (v > 127) v = 127;
+                if (v < -127) v = -127;
+                xq[(int64_t)s * I + g * 32 + i] = (int8_t)v;
+            }
+        }
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++) {
+        const uint8_t *w = q4 + (int64_t)o * rb;
+        const uint8_t *scl = e8 + (int64_t)o * ng;
+        for (int s = 0; s < S; s++) {
+            const int8_t *xr = xq + (int64_t)s * I;
+            float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int g = 0; g < ng; g++) {
+                float sc = cref_mx4_scale(scl[g]) * 0.5f * xsc[(int64_t)s * ng + g];
+                for (int j = 0; j < 8; j++) {
+                    int32_t lane = 0;
+                    for (int i = 4 * j; i < 4 * j + 4; i++) lane += lut2[nib_at(w, g * 32 + i)] * xr[g * 32 + i];
+                    acc[j] = fmaf((float)lane, sc, acc[j]);
+                }
+            }
+            y[(int64_t)s * O + o] = hsum8(acc);
+        }
+    }
+    free(xq);
+    free(xsc);
+}
+
 /* 16-row interleave: packed[(tile*cols/2 + col)*16 + lane]
  * (c/deepseek_v4.c:10975-10993). */
 int cref_fp4_pack_rows16(uint8_t *pdata, uint8_t *pscales, const uint8_t *q4,

@@ -23,6 +23,11 @@
  *       + brute force.
  *   cref_matmul_mxfp4: bitwise vs oracle/_ref matmul_mxfp4; all-16-codes
  *       exactness (c/tests/test_mxfp4_cuda.cu:106-132); e8 edges 0/127/255.
+ *   cref_matmul_mxfp4_i8: bitwise vs tests/golden/golden_mxfp4_i8.npz and
+ *       oracle/_ref matmul_mxfp4_i8; the int8 quantization checked against
+ *       its definition (|q| <= 127, q = nearest integer of x / sc, the
+ *       group maximum maps to +-127); float64 dequantized product within
+ *       the quantization bound; I % 32 != 0 equals matmul_mxfp4.
  *   cref_fp4_matvec / cref_fp4_matmul_batch: fp4 matvec KAT = 128.0
  *       (test_native_quant.c:76-88) + bitwise vs oracle/_ref.
  *   cref_fp4_pack_rows16 / cref_fp4_matvec_rows16: bitwise vs oracle/_ref
@@ -62,6 +67,8 @@ void cref_matmul_i4(float *y, const float *x, const uint8_t *q4,
                     const float *scale, int S, int I, int O);
 void cref_matmul_mxfp4(float *y, const float *x, const uint8_t *q4,
                        const uint8_t *e8, int S, int I, int O);
+void cref_matmul_mxfp4_i8(float *y, const float *x, const uint8_t *q4,
+                          const uint8_t *e8, int S, int I, int O);
 /* native_quant contract: e4m3 QDQ of each activation row (block 128), then
  * the fmt=7 GEMV. Returns 0 on success, -1 on invalid shape (cols%128). */
 int cref_fp4_matmul_batch(float *y, const uint8_t *q4, const uint8_t *e8,

@@ -69,6 +69,7 @@ class Cref(_Lib):
         self._i4g = self.fn("matmul_i4_grouped", [_f, _f, _u8, _f, _i, _i, _i, _i])
         self._i4 = self.fn("matmul_i4", [_f, _f, _u8, _f, _i, _i, _i])
         self._mx = self.fn("matmul_mxfp4", [_f, _f, _u8, _u8, _i, _i, _i])
+        self._mx8 = self.fn("matmul_mxfp4_i8", [_f, _f, _u8, _u8, _i, _i, _i])
         self._fp4b = self.fn("fp4_matmul_batch", [_f, _u8, _u8, _i, _i, _f, _i], _i)
         self._pack16 = self.fn("fp4_pack_rows16", [_u8, _u8, _u8, _u8, _i, _i], _i)
         self._mv16 = self.fn("fp4_matvec_rows16", [_f, _u8, _u8, _i, _i, _f], _i)
@@ -108,6 +109,12 @@ class Cref(_Lib):
         S = x.shape[0]
         y = np.empty((S, O), np.float32)
         self._mx(f32p(y), f32p(x), u8p(q4), u8p(e8), S, I, O)
+        return y
+
+    def matmul_mxfp4_i8(self, x, q4, e8, O, I):
+        S = x.shape[0]
+        y = np.empty((S, O), np.float32)
+        self._mx8(f32p(y), f32p(x), u8p(q4), u8p(e8), S, I, O)
         return y
 
     def fp4_matmul_batch(self, x, q4, e8, O, I):
@@ -165,6 +172,7 @@ class Ref(_Lib):
         self._i4g = self.fn("ref_matmul_i4_grouped", [_f, _f, _u8, _f, _i, _i, _i, _i])
         self._i4 = self.fn("ref_matmul_i4", [_f, _f, _u8, _f, _i, _i, _i])
         self._mx = self.fn("ref_matmul_mxfp4", [_f, _f, _u8, _u8, _i, _i, _i])
+        self._mx8 = self.fn("ref_matmul_mxfp4_i8", [_f, _f, _u8, _u8, _i, _i, _i])
         self._f32 = self.fn("ref_matmul_f32", [_f, _f, _f, _i, _i, _i])
         self._qdq = self.fn("coli_fp8_activation_qdq_ref", [_f, _u8, _f, C.c_size_t, C.c_size_t], _i)
         self.e2m1 = self.fn("coli_e2m1_decode", [C.c_uint8], C.c_float)
@@ -189,6 +197,12 @@ class Ref(_Lib):
         S = x.shape[0]
         y = np.empty((S, O), np.float32)
         self._mx(f32p(y), f32p(x), u8p(q4), u8p(e8), S, I, O)
+        return y
+
+    def matmul_mxfp4_i8(self, x, q4, e8, O, I):
+        S = x.shape[0]
+        y = np.empty((S, O), np.float32)
+        self._mx8(f32p(y), f32p(x), u8p(q4), u8p(e8), S, I, O)
         return y
 
     def matmul_f32(self, x, W):

@@ -205,6 +205,29 @@ def test_fp4_native_quant_contract(session, S):
     check(y, ref, magnitude(xq, deq_mxfp4(q4, e8, I)))
 
 
+@pytest.mark.parametrize("S,I,O", [(1, 512, 64), (4, 2048, 256), (16, 256, 33), (3, 100, 9)])
+def test_matmul_mxfp4_i8(session, S, I, O):
+    """coli_hip_matmul_mxfp4_i8 (stateless) and coli_hip_fp4_matmul_i8
+    (resident) against the oracle's matmul_mxfp4_i8 (c/quant.h:1441-1515,
+    int8 activations per 32 columns; I % 32 != 0 is the float path)."""
+    rng = np.random.default_rng(900 + S * I + O)
+    q4, e8 = rand_mxfp4(rng, O, I, 110, 139)
+    x = (rng.standard_normal((S, I)) * 2).astype(np.float32)
+    x[0, :min(I, 32)] = 0.0          # one all-zero group (scale floor)
+    from colibri_amd.backend import f32p, u8p
+    ref = cref.matmul_mxfp4_i8(x, q4, e8, O, I)
+    y = np.zeros((S, O), np.float32)
+    assert session.b.hip_matmul_mxfp4_i8(f32p(y), f32p(x), u8p(q4), u8p(e8), S, I, O)
+    check(y, ref, magnitude(x, deq_mxfp4(q4, e8, I)))
+    h = session.upload_mxfp4(q4, e8, I, O)
+    y2 = np.zeros((S, O), np.float32)
+    try:
+        assert session.b.hip_fp4_matmul_i8(h, f32p(y2), f32p(x), S)
+    finally:
+        session.free(h)
+    assert np.array_equal(y, y2)
+
+
 def test_fp4_matvec_kat(session):
     """weights 0x44 (+2.0, +2.0), scale 0x7e (0.5), x = 1 over 128 columns gives
     exactly 128.0 (c/tests/test_native_quant.c:76-88)."""

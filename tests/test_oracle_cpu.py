@@ -321,3 +321,80 @@ def test_swiglu_closed_form():
     g64 = g.astype(np.float64)
     ref = g64 / (1 + np.exp(-g64)) * u
     assert np.allclose(h, ref, rtol=1e-6, atol=1e-30)
+
+
+# -- matmul_mxfp4_i8 (c/quant.h:1441-1515, the K3 IDOT path) --------------------
+
+GOLDEN_I8 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_mxfp4_i8.npz")
+
+
+def i8_quantize64(x):
+    """The int8 quantization of matmul_mxfp4_i8, per its definition: per row
+    and 32-column group, sc = max|x| / 127 (f32, floored at 1e-20), q = the
+    nearest integer (ties to even) of x * f32(1 / sc), clamped to +-127."""
+    S, I = x.shape
+    g = x.reshape(S, I // 32, 32)
+    sc = (np.abs(g).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    sc = np.maximum(sc, np.float32(1e-20))
+    inv = (np.float32(1.0) / sc).astype(np.float32)
+    q = np.clip(np.rint((g * inv[:, :, None]).astype(np.float32)), -127, 127)
+    return q, sc
+
+
+def test_golden_mxfp4_i8():
+    gold = np.load(GOLDEN_I8, allow_pickle=False)
+    n = 0
+    while f"c{n}_shape" in gold.files:
+        S, I, O = gold[f"c{n}_shape"]
+        y = cref.matmul_mxfp4_i8(gold[f"c{n}_x"], gold[f"c{n}_q4"], gold[f"c{n}_e8"], O, I)
+        assert np.array_equal(bits(y), bits(gold[f"c{n}_y"])), (S, I, O)
+        n += 1
+    assert n >= 5
+
+
+@pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built (needs the reference tree)")
+def test_mxfp4_i8_vs_compiled_reference():
+    ref = Ref()
+    rng = np.random.default_rng(808)
+    for t in range(30):
+        S = int(rng.integers(1, 17))
+        I = int(rng.choice([32, 64, 96, 256, 512, 100]))
+        O = int(rng.integers(1, 20))
+        x = rng.standard_normal((S, I)).astype(np.float32) * np.float32(10.0 ** rng.uniform(-3, 3))
+        q4, e8 = rand_mxfp4(rng, O, I, 100, 140)
+        assert np.array_equal(bits(cref.matmul_mxfp4_i8(x, q4, e8, O, I)),
+                              bits(ref.matmul_mxfp4_i8(x, q4, e8, O, I))), (S, I, O)
+
+
+def test_mxfp4_i8_quantized_dot_math():
+    """Against float64 on the quantized operands: the result is the exact
+    integer dot of each group with the doubled e2m1 codes times the group
+    scale, so y64 = sum_g sc_g * sum_k q_k w_k agrees to f32 rounding; and on
+    activations that are already k * s (integers with the group maximum at
+    127) the quantization is the identity."""
+    rng = np.random.default_rng(809)
+    S, I, O = 4, 256, 24
+    q4, e8 = rand_mxfp4(rng, O, I, 115, 130)
+    wd = deq_mxfp4(q4, e8, I)
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    q, sc = i8_quantize64(x)
+    assert np.abs(q).max() == 127
+    xq = (q * sc[:, :, None].astype(np.float64)).reshape(S, I)
+    y64 = xq @ wd.T
+    assert rel_err(cref.matmul_mxfp4_i8(x, q4, e8, O, I), y64, magnitude(xq, wd), 1.0).max() <= 2e-6
+    # quantization error of the int8 grid itself: within half a step per element
+    assert np.all(np.abs(xq.reshape(S, I // 32, 32) - x.reshape(S, I // 32, 32)) <= 0.5 * sc[:, :, None] * 1.0001)
+    # identity on the grid
+    k = rng.integers(-127, 128, (S, I)).astype(np.float64)
+    k.reshape(S, I // 32, 32)[:, :, 0] = 127
+    s = 2.0 ** rng.integers(-6, 3, (S, I // 32))
+    xg = (k.reshape(S, I // 32, 32) * s[:, :, None]).reshape(S, I).astype(np.float32)
+    qg, _ = i8_quantize64(xg)
+    assert np.array_equal(qg.reshape(S, I), k)
+
+
+def test_mxfp4_i8_ragged_falls_back():
+    rng = np.random.default_rng(810)
+    x = rand_x(rng, 2, 100)
+    q4, e8 = rand_mxfp4(rng, 5, 100)
+    assert np.array_equal(bits(cref.matmul_mxfp4_i8(x, q4, e8, 5, 100)), bits(cref.matmul_mxfp4(x, q4, e8, 5, 100)))
