@@ -35,7 +35,7 @@ _tpp = C.POINTER(C.c_void_p)    # ColiCudaTensor**
 class ColiHipMoeConfig(C.Structure):
     _fields_ = [("D", C.c_int), ("I", C.c_int), ("E", C.c_int), ("K", C.c_int),
                 ("route_mode", C.c_int), ("norm_topk", C.c_int), ("topp", C.c_float),
-                ("routed_scale", C.c_float), ("has_shared", C.c_int)]
+                ("routed_scale", C.c_float), ("has_shared", C.c_int), ("swiglu_limit", C.c_float)]
 
 
 def declared_symbols():

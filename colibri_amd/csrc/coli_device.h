@@ -107,6 +107,24 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
+// SwiGLU of the DUAL epilogues: silu(g) * u (c/backend_cuda.cu:618-624), or
+// with limit > 0 the DeepSeek-V4 form (c/deepseek_v4.c:1434-1448): gate
+// clamped from above and up to +-limit, g * sigmoid(g) * u with the
+// two-branch stable sigmoid (c/deepseek_v4.c:1102-1109).
+__device__ __forceinline__ float swiglu_out(float g, float u, float limit) {
+    if (!(limit > 0.0f)) return silu_mul(g, u);
+    g = fminf(g, limit);
+    u = fmaxf(-limit, fminf(u, limit));
+    float sg;
+    if (g >= 0.0f) {
+        sg = 1.0f / (1.0f + expf(-g));
+    } else {
+        const float e = expf(g);
+        sg = e / (1.0f + e);
+    }
+    return g * sg * u;
+}
+
 // Output of one lane for batch row `brow` of the problem: output row
 // rt*16 + (lane & 15) of every live tile, scaled back by the row's 2^E; for
 // DUAL, silu(gate) * up of the paired tiles.
@@ -125,7 +143,7 @@ __device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiP
         if (o >= a.O) continue;
         if constexpr (DUAL) {
             float gv = ldexpf(v[r], E), uv = ldexpf(v[r + RT], E);
-            orow[o] = silu_mul(gv, uv);
+            orow[o] = swiglu_out(gv, uv, a.swiglu_limit);
         } else {
             orow[o] = ldexpf(v[r], E);
         }

@@ -119,11 +119,11 @@ int make_frags8(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, 
 // inline problem) reading fragment set `set`.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
-             const ColiProb *inline_prob = nullptr);
+             const ColiProb *inline_prob = nullptr, float swiglu_limit = 0.0f);
 // One grouped GEMM over a device work list of (problem << 16 | 64-row tile).
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
-             const int *xrows_dev, float *out, int ldo);
+             const int *xrows_dev, float *out, int ldo, float swiglu_limit = 0.0f);
 
 // Router logits of S rows into `part`; returns the number of column-chunk
 // partials the selection must add (1 when the batch went through one GEMM),

@@ -75,6 +75,7 @@ struct ColiGemvArgs {
     const _Float16 *zero;     // >= COLI_ZERO_BYTES of zeros: inactive batch lanes, dead tiles
     float *out;
     int ldo;
+    float swiglu_limit;       // > 0: DeepSeek-V4 clamped SwiGLU in the DUAL epilogue
     float *partial;           // split-K partials: [instance][split][R][NB4][64]
     int *split_cnt;           // split-K arrival counters, one per instance; zero between launches
 };
@@ -103,6 +104,7 @@ struct ColiGemmArgs {
     const uint8_t *zero;
     float *out;
     int ldo;
+    float swiglu_limit;       // > 0: DeepSeek-V4 clamped SwiGLU in the DUAL epilogue
 };
 
 // Grouped MXFP4 GEMM on the block-scaled MFMA (gemm_mx.hip): activations as
@@ -125,6 +127,7 @@ struct ColiGemmMxArgs {
     const uint8_t *zero;
     float *out;
     int ldo;
+    float swiglu_limit;       // > 0: DeepSeek-V4 clamped SwiGLU in the DUAL epilogue
 };
 
 // Numeric helpers shared by host and device.

@@ -171,7 +171,7 @@ int make_frags8(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, 
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
-             const ColiProb *inline_prob) {
+             const ColiProb *inline_prob, float swiglu_limit) {
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
     GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
@@ -207,6 +207,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.zero = (const _Float16 *)ctx->zeros.p;
     a.out = out;
     a.ldo = ldo;
+    a.swiglu_limit = swiglu_limit;
     a.partial = (float *)ctx->partial.p;
     a.split_cnt = (int *)ctx->split_cnt.p;
     if (pl.dma) return hip_ok(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.PD, max_rows, ctx->stream),
@@ -219,7 +220,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
 // probs_dev.
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
-             const int *xrows_dev, float *out, int ldo) {
+             const int *xrows_dev, float *out, int ldo, float swiglu_limit) {
     if (n_mt <= 0) return 1;
     FragSet &f = ctx->frag[set];
     if (kind == COLI_KIND_FP4 && mx_gemm_enabled()) {
@@ -244,6 +245,7 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
         m.zero = (const uint8_t *)ctx->zeros.p;
         m.out = out;
         m.ldo = ldo;
+        m.swiglu_limit = swiglu_limit;
         return hip_ok(coli_launch_gemm_mx(dual ? 1 : 0, &m, ctx->stream), "gemm launch");
     }
     ColiGemmArgs a;
@@ -269,6 +271,7 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.zero = (const uint8_t *)ctx->zeros.p;
     a.out = out;
     a.ldo = ldo;
+    a.swiglu_limit = swiglu_limit;
     return hip_ok(coli_launch_gemm(kind, dual ? 1 : 0, &a, ctx->stream), "gemm launch");
 }
 

@@ -185,7 +185,8 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
                 if (!live[r]) continue;
                 const int o = rt[r] * 16 + (lane & 15);
                 if (o >= a.O) continue;
-                if constexpr (DUAL) orow[o] = silu_mul(ldexpf(acc[0][m][i], E), ldexpf(acc[1][m][i], E));
+                if constexpr (DUAL)
+                    orow[o] = swiglu_out(ldexpf(acc[0][m][i], E), ldexpf(acc[1][m][i], E), a.swiglu_limit);
                 else orow[o] = ldexpf(acc[r][m][i], E);
             }
         }

@@ -320,7 +320,7 @@ __device__ __forceinline__ void gemm_mx_body(const ColiGemmMxArgs &a, uint8_t *l
                 if (!live[r]) continue;
                 const int o = rt[r] * 16 + (lane & 15);
                 if (o >= a.O) continue;
-                if constexpr (DUAL) orow[o] = silu_mul(acc[0][m][i], acc[1][m][i]);
+                if constexpr (DUAL) orow[o] = swiglu_out(acc[0][m][i], acc[1][m][i], a.swiglu_limit);
                 else orow[o] = acc[r][m][i];
             }
         }

@@ -184,7 +184,7 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
     if (!out || !cfg || !router_w || !gates || !ups || !downs) return 0;
     const ColiHipMoeConfig c = *cfg;
     if (c.D < 1 || c.I < 1 || c.E < 1 || c.E > 1024 || c.K < 1 || c.K > 64 || c.K > c.E || c.route_mode < 0 ||
-        c.route_mode > 2)
+        c.route_mode > 3 || !(c.swiglu_limit >= 0.0f))
         return 0;
     if (c.has_shared && (!sg || !su || !sd)) return 0;
     DevCtx *ctx = find_ctx(device);
@@ -285,9 +285,10 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
     if (gemm) {
         if (!run_gemm(ctx, m->kind, true, m->pdual, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_i, nq_d,
-                      c.I, fx, m->xrows, m->h, c.I))
+                      c.I, fx, m->xrows, m->h, c.I, c.swiglu_limit))
             return 0;
-    } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I)) {
+    } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I,
+                         nullptr, c.swiglu_limit)) {
         return 0;
     }
     if (!(mx ? make_frags8(ctx, fh, m->h, c.I, rows, c.I, nullptr, m->state + 1)

@@ -152,6 +152,9 @@ extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const flo
 //   mode 2: as mode 1 for the selection; weights renormalized over the K
 //           with +1e-20; TOPP keeps until cum >= topp and renormalizes the
 //           kept set (c/kimi_k3.c:1337-1370); routed_scale applied after.
+//   mode 3: DeepSeek-V4 (c/deepseek_v4.c:1368-1432): p = sqrt(softplus(z))
+//           (stable form), choice = p + bias, weights p / sum over the K x
+//           routed_scale; a non-positive sum selects nothing (keff 0).
 // The reference selects by K rounds of an argmax with strict '>' (highest
 // value, lowest index on ties; NaN and values <= -1e30 never chosen; a round
 // with nothing left picks index kk, c/route_trace.h:383-393). The same rounds
@@ -310,6 +313,16 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
             cv[j] = v;
             pv[j] = v;
         }
+    } else if (mode == 3) {
+        // DeepSeek-V4: sqrt of the stable softplus (c/deepseek_v4.c:1368-1392)
+#pragma unroll
+        for (int j = 0; j < JM; j++) {
+            const float z = lg[j];
+            const float v = sqrtf(fmaxf(z, 0.0f) + log1pf(expf(-fabsf(z))));
+            if (j < nmine) p[lane + 64 * j] = v;
+            cv[j] = v + bs[j];
+            pv[j] = v;
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < JM; j++) {
@@ -399,6 +412,12 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
         }
         if (norm_topk) my_w /= wsum(act && slot < ke ? my_w : 0.0f) + 1e-20f;
         if (slot < ke) my_w *= routed_scale;
+    } else if (mode == 3) {
+        // score / sum of the selected scores * route scale; a non-positive sum
+        // (an error in coli_v4_route) selects nothing
+        const float total = wsum(my_w);
+        if (!(total > 0.0f)) ke = 0;
+        else my_w = my_w / total * routed_scale;
     } else {
         my_w /= wsum(my_w) + 1e-20f;
         if (cut) {

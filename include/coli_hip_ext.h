@@ -67,11 +67,14 @@ typedef struct {
     int route_mode;        /* 0 softmax then top-k (c/olmoe.c:666-681)
                               1 sigmoid, choice = sigmoid + bias (c/colibri.c:3978-4126)
                               2 sigmoid + bias select, weights renormalized over the
-                                selection (c/kimi_k3.c:1337-1356) */
+                                selection (c/kimi_k3.c:1337-1356)
+                              3 DeepSeek-V4: sqrt(softplus) + bias select, weights
+                                score / sum x routed_scale (c/deepseek_v4.c:1368-1432) */
     int norm_topk;
     float topp;            /* 0 disables */
     float routed_scale;    /* 1.0 for none */
     int has_shared;        /* one always-on expert, added after the routed sum */
+    float swiglu_limit;    /* > 0: DeepSeek-V4 clamped SwiGLU (c/deepseek_v4.c:1434-1448) */
 } ColiHipMoeConfig;
 
 /* Router weights f32 [E, D] (+ bias [E] or NULL) are copied to the device;

@@ -441,7 +441,36 @@ void cref_route(const float *logits, const float *bias, int S, int E, int K,
         int *ix = idx + (int64_t)s * K;
         float *wx = w + (int64_t)s * K;
         int ke = K;
-        if (mode == 0) {
+        if (mode == 3) {
+            /* DeepSeek-V4 (coli_v4_route, c/deepseek_v4.c:1368-1432): score =
+             * sqrt(softplus(z)) (stable form), selection = score + bias,
+             * top-K by strict > (the first unselected expert seeds each
+             * round, so the lowest index wins ties), weight = score /
+             * sum of the selected scores * route_scale. A non-positive sum
+             * is an error there; here the row selects nothing (keff 0). */
+            unsigned char *taken = (unsigned char *)calloc((size_t)E, 1);
+            for (int e = 0; e < E; e++) {
+                float v = z[e];
+                p[e] = sqrtf(fmaxf(v, 0.0f) + log1pf(expf(-fabsf(v))));
+                c[e] = p[e] + (bias ? bias[e] : 0.0f);
+            }
+            for (int kk = 0; kk < K; kk++) {
+                int best = -1;
+                for (int e = 0; e < E; e++)
+                    if (!taken[e] && (best < 0 || c[e] > c[best])) best = e;
+                ix[kk] = best;
+                taken[best] = 1;
+            }
+            free(taken);
+            float total = 0.0f;
+            for (int kk = 0; kk < K; kk++) total += p[ix[kk]];
+            if (!(total > 0.0f)) {
+                ke = 0;
+                for (int kk = 0; kk < K; kk++) wx[kk] = 0.0f;
+            } else {
+                for (int kk = 0; kk < K; kk++) wx[kk] = p[ix[kk]] / total * routed_scale;
+            }
+        } else if (mode == 0) {
             /* softmax_row, c/olmoe.c:246-250 */
             float m = -1e30f, sum = 0.0f;
             for (int e = 0; e < E; e++) if (z[e] > m) m = z[e];
@@ -535,6 +564,30 @@ void cref_swiglu(float *h, const float *g, const float *u, size_t n) {
     for (size_t i = 0; i < n; i++) {
         float v = g[i];
         h[i] = (v / (1.0f + expf(-v))) * u[i];
+    }
+}
+
+/* DeepSeek-V4 SwiGLU (coli_v4_swiglu, c/deepseek_v4.c:1434-1448): with
+ * limit > 0 the gate is clamped from above and the up value to +-limit;
+ * h = g * sigmoid(g) * u with the two-branch stable sigmoid of
+ * c/deepseek_v4.c:1102-1109. */
+static float sigmoid_stable_ref(float v) {
+    if (v >= 0.0f) {
+        float decay = expf(-v);
+        return 1.0f / (1.0f + decay);
+    }
+    float growth = expf(v);
+    return growth / (1.0f + growth);
+}
+
+void cref_swiglu_v4(float *h, const float *g, const float *u, size_t n, float limit) {
+    for (size_t i = 0; i < n; i++) {
+        float gv = g[i], uv = u[i];
+        if (limit > 0.0f) {
+            gv = fminf(gv, limit);
+            uv = fmaxf(-limit, fminf(uv, limit));
+        }
+        h[i] = gv * sigmoid_stable_ref(gv) * uv;
     }
 }
 

@@ -33,6 +33,9 @@
  *   cref_fp4_pack_rows16 / cref_fp4_matvec_rows16: bitwise vs oracle/_ref
  *       + permutation invariant rows16(W) == row-major(W) up to the
  *       no-FMA order (c/deepseek_v4.c:11059-11062).
+ *   cref_route mode 3 (DeepSeek-V4 sqrt-softplus) and cref_swiglu_v4:
+ *       bitwise vs oracle/_ref coli_v4_route / coli_v4_swiglu and
+ *       tests/golden/golden_v4.npz; score and clamp closed forms.
  *   cref_route_*: brute force (full stable sort of all E) + NaN fallback
  *       (c/tests/test_router_nan.c:37-75 semantics).
  *   cref_expert_union: set invariant + first-seen order.
@@ -100,6 +103,7 @@ int cref_expert_union(const int *idx, const float *w, const int *keff, int S, in
 
 /* h = silu(g) * u, the exact expression of backend_cuda.cu:417-423 / 618-624 */
 void cref_swiglu(float *h, const float *g, const float *u, size_t n);
+void cref_swiglu_v4(float *h, const float *g, const float *u, size_t n, float limit);
 
 /* One MoE layer, decode rows x[S,D] -> out[S,D].
  * fmt 4: int4 group-scaled (scales f32 [O, I/gs]); fmt 7: MXFP4 (e8 bytes);

@@ -34,6 +34,9 @@ def make_router_inputs(rng, S, D, E, K, mode, gap=1e-4, bias=False, zipf=None):
                 sc = sc / sc.sum()
                 # selection is monotone in z; require the gap in logit space
                 srt = np.sort(z)[::-1]
+            elif mode == 3:
+                sc = np.sqrt(np.logaddexp(0.0, z)) + (b if b is not None else 0)
+                srt = np.sort(sc)[::-1]
             else:
                 sc = 1.0 / (1.0 + np.exp(-z)) + (b if b is not None else 0)
                 srt = np.sort(sc)[::-1]
@@ -48,8 +51,9 @@ def make_router_inputs(rng, S, D, E, K, mode, gap=1e-4, bias=False, zipf=None):
 class Layer:
     """Expert weights of one synthetic MoE layer in source layout."""
 
-    def __init__(self, rng, fmt, D, I, E, shared=False):
+    def __init__(self, rng, fmt, D, I, E, shared=False, swiglu_limit=0.0):
         self.fmt, self.D, self.I, self.E = fmt, D, I, E
+        self.swiglu_limit = swiglu_limit   # > 0: DeepSeek-V4 clamped SwiGLU
         self.experts = [self._expert(rng) for _ in range(E)]
         self.shared = self._expert(rng) if shared else None
 
@@ -79,7 +83,7 @@ class Layer:
         g, u, d = self.experts[e] if e >= 0 else self.shared
         gv = self.gemv(g, x, self.I, self.D)
         uv = self.gemv(u, x, self.I, self.D)
-        h = cref.swiglu(gv, uv)
+        h = cref.swiglu_v4(gv, uv, self.swiglu_limit) if self.swiglu_limit > 0 else cref.swiglu(gv, uv)
         return h, self.gemv(d, h, self.D, self.I)
 
     def upload(self, session):

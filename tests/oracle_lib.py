@@ -78,6 +78,7 @@ class Cref(_Lib):
         self._union = self.fn("expert_union", [_i32, _f, _i32, _i, _i, _i, _i32, _i32,
                                                _i32, _i32, _f], _i)
         self._swiglu = self.fn("swiglu", [_f, _f, _f, C.c_size_t])
+        self._swiglu_v4 = self.fn("swiglu_v4", [_f, _f, _f, C.c_size_t, C.c_float])
 
     def qdq(self, x, block=128):
         x = np.ascontiguousarray(x, np.float32)
@@ -163,6 +164,13 @@ class Cref(_Lib):
         self._swiglu(f32p(h), f32p(g), f32p(u), g.size)
         return h
 
+    def swiglu_v4(self, g, u, limit):
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        h = np.empty_like(g)
+        self._swiglu_v4(f32p(h), f32p(g), f32p(u), g.size, limit)
+        return h
+
 
 class Ref(_Lib):
     """The reference's own CPU kernels, compiled from its sources."""
@@ -180,6 +188,28 @@ class Ref(_Lib):
         self.e4m3_dec = self.fn("coli_e4m3fn_decode", [C.c_uint8], C.c_float)
         self.e4m3_enc = self.fn("coli_e4m3fn_encode", [C.c_float], C.c_uint8)
         self.bf16_round = self.fn("coli_bf16_round", [C.c_float], C.c_float)
+        self._v4route = self.fn("coli_v4_route", [_f, _i32, _f, _f, _f, _i32, _i, _i, _i, C.c_float], _i)
+        self._v4swiglu = self.fn("coli_v4_swiglu", [_f, _f, _f, _i, C.c_float], _i)
+
+    def v4_route(self, logits, K, bias=None, route_scale=1.0):
+        """coli_v4_route on given logits: hidden = [1.0] and a one-column gate
+        make the reference's own dot product return each logit exactly."""
+        logits = np.ascontiguousarray(logits, np.float32)
+        E = logits.size
+        one = np.ones(1, np.float32)
+        w = np.zeros(K, np.float32)
+        idx = np.zeros(K, np.int32)
+        b = np.ascontiguousarray(bias, np.float32) if bias is not None else None
+        rc = self._v4route(f32p(w), i32p(idx), f32p(one), f32p(logits), f32p(b) if b is not None else None,
+                           None, E, 1, K, route_scale)
+        return rc, idx, w
+
+    def v4_swiglu(self, g, u, limit):
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        h = np.empty_like(g)
+        assert self._v4swiglu(f32p(h), f32p(g), f32p(u), g.size, limit) == 0
+        return h
 
     def matmul_i4_grouped(self, x, q4, sc, O, I, gs):
         S = x.shape[0]

@@ -162,7 +162,7 @@ def make_moe(session, layer, W, b, K, mode, norm_topk=0, topp=0.0, routed_scale=
     u, ua = tensor_array([h[1] for h in routed])
     d, da = tensor_array([h[2] for h in routed])
     cfg = ColiHipMoeConfig(layer.D, layer.I, E, K, mode, norm_topk, topp, routed_scale,
-                           1 if layer.shared else 0)
+                           1 if layer.shared else 0, layer.swiglu_limit)
     m = C.c_void_p()
     Wc = np.ascontiguousarray(W)
     bc = np.ascontiguousarray(b) if b is not None else None
@@ -301,3 +301,33 @@ def test_expert_group_block_scaled_mfma(session, monkeypatch, D, I, rows, lo):
     mag = group_mag(layer, x, members, rows)
     err = np.abs(y.astype(np.float64) - ref) / mag
     assert err.max() <= 2e-4, f"block-scaled MFMA error {err.max():.3g} of the magnitude sum"
+
+
+@pytest.mark.parametrize("fmt,S,shared,limit", [(7, 1, True, 2.0), (4, 5, False, 2.0), (7, 16, True, 0.0),
+                                                (7, 40, False, 2.0)])
+def test_moe_layer_deepseek_v4(session, fmt, S, shared, limit):
+    """DeepSeek-V4 routing (route mode 3: sqrt-softplus score + bias select,
+    weights score / sum x route_scale, c/deepseek_v4.c:1368-1432) and the V4
+    clamped SwiGLU (c/deepseek_v4.c:1434-1448) through the fused layer; S = 40
+    runs the grouped GEMM."""
+    rng = np.random.default_rng(400 + fmt * 10 + S)
+    D, I, E, K = 512, 256, 32, 4
+    layer = Layer(rng, fmt, D, I, E, shared=shared, swiglu_limit=limit)
+    x, W, b = make_router_inputs(rng, S, D, E, K, 3, bias=True)
+    m, hs = make_moe(session, layer, W, b, K, 3, routed_scale=2.5)
+    out = np.zeros((S, D), np.float32)
+    idx = np.zeros((S, K), np.int32)
+    w = np.zeros((S, K), np.float32)
+    keff = np.zeros(S, np.int32)
+    try:
+        assert session.b.hip_moe_forward(m, f32p(x), f32p(out), S, i32p(idx), f32p(w), i32p(keff))
+    finally:
+        session.b.hip_moe_free(m)
+        for h in hs:
+            for t in h:
+                session.free(t)
+    ri, rw, rk, ref, mag = moe_reference(layer, x, W, b, K, 3, routed_scale=2.5)
+    assert np.array_equal(keff, rk)
+    assert np.array_equal(idx, ri), "router top-K indices must be bit-exact"
+    assert np.allclose(w, rw, rtol=1e-5, atol=1e-7)
+    assert rel_err(out, ref, mag).max() <= TOL

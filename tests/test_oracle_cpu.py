@@ -398,3 +398,64 @@ def test_mxfp4_i8_ragged_falls_back():
     x = rand_x(rng, 2, 100)
     q4, e8 = rand_mxfp4(rng, 5, 100)
     assert np.array_equal(bits(cref.matmul_mxfp4_i8(x, q4, e8, 5, 100)), bits(cref.matmul_mxfp4(x, q4, e8, 5, 100)))
+
+
+# -- DeepSeek-V4 router and SwiGLU (c/deepseek_v4.c:1368-1448) -------------------
+
+GOLDEN_V4 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_v4.npz")
+
+
+def test_golden_v4_route_and_swiglu():
+    gold = np.load(GOLDEN_V4, allow_pickle=False)
+    n = 0
+    while f"r{n}_meta" in gold.files:
+        E, K, has_b = (int(v) for v in gold[f"r{n}_meta"])
+        b = gold[f"r{n}_b"] if has_b else None
+        idx, w, keff = cref.route(gold[f"r{n}_z"][None, :], K, 3, bias=b, routed_scale=float(gold[f"r{n}_scale"][0]))
+        assert np.array_equal(idx[0], gold[f"r{n}_idx"]), n
+        assert np.array_equal(bits(w[0]), bits(gold[f"r{n}_w"])), n
+        assert keff[0] == K
+        n += 1
+    assert n >= 4
+    for k in range(3):
+        h = cref.swiglu_v4(gold["sw_g"], gold["sw_u"], float(gold[f"sw{k}_limit"][0]))
+        assert np.array_equal(bits(h), bits(gold[f"sw{k}_h"])), k
+
+
+@pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built (needs the reference tree)")
+def test_v4_vs_compiled_reference():
+    ref = Ref()
+    rng = np.random.default_rng(811)
+    for t in range(40):
+        E = int(rng.integers(8, 400))
+        K = int(rng.integers(1, min(E, 16) + 1))
+        z = (rng.standard_normal(E) * float(rng.uniform(0.1, 20))).astype(np.float32)
+        b = (rng.standard_normal(E) * 0.1).astype(np.float32) if t % 2 else None
+        rc, ridx, rw = ref.v4_route(z, K, b, 2.0)
+        idx, w, _ = cref.route(z[None, :], K, 3, bias=b, routed_scale=2.0)
+        assert rc == 0 and np.array_equal(idx[0], ridx) and np.array_equal(bits(w[0]), bits(rw)), t
+    g = (rng.standard_normal(5000) * 8).astype(np.float32)
+    u = (rng.standard_normal(5000) * 8).astype(np.float32)
+    for limit in (0.0, 0.5, 3.0, 10.0):
+        assert np.array_equal(bits(cref.swiglu_v4(g, u, limit)), bits(ref.v4_swiglu(g, u, limit)))
+
+
+def test_v4_route_math():
+    """Against float64: score = sqrt(log(1 + e^z)), selection by score + bias
+    (a full stable sort gives the same top-K under a clear gap), weights =
+    score / sum * scale; clamps of the V4 SwiGLU."""
+    rng = np.random.default_rng(812)
+    E, K = 96, 8
+    z = (rng.standard_normal(E) * 4).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    sc = np.sqrt(np.logaddexp(0.0, z.astype(np.float64)))
+    sel = sc + b
+    order = np.argsort(-sel, kind="stable")[:K]
+    idx, w, keff = cref.route(z[None, :], K, 3, bias=b, routed_scale=1.5)
+    assert list(idx[0]) == list(order)
+    assert np.allclose(w[0], sc[order] / sc[order].sum() * 1.5, rtol=2e-6)
+    g = np.array([-3.0, 0.5, 2.0, 9.0], np.float32)
+    u = np.array([-9.0, -0.5, 3.0, 0.25], np.float32)
+    h = cref.swiglu_v4(g, u, 1.0).astype(np.float64)
+    gc, uc = np.minimum(g, 1.0).astype(np.float64), np.clip(u, -1.0, 1.0).astype(np.float64)
+    assert np.allclose(h, gc / (1 + np.exp(-gc)) * uc, rtol=1e-6)
