@@ -43,6 +43,32 @@ __device__ __forceinline__ ColiProb uniform_prob(const ColiProb &p) {
 }
 
 
+// Maximum over each 16-lane row, on the VALU (DPP: swap neighbours, swap
+// pairs, mirror halves of 8, mirror halves of 16).
+__device__ __forceinline__ float dpp_max16(float v) {
+    auto step = [](float x, int ctrl) {
+        const int o = ctrl == 0xB1   ? __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false)
+                      : ctrl == 0x4E ? __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false)
+                      : ctrl == 0x141 ? __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false)
+                                      : __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false);
+        return fmaxf(x, __int_as_float(o));
+    };
+    v = step(v, 0xB1);    // quad_perm [1, 0, 3, 2]
+    v = step(v, 0x4E);    // quad_perm [2, 3, 0, 1]
+    v = step(v, 0x141);   // row_half_mirror
+    return step(v, 0x140);  // row_mirror
+}
+
+// Maximum over the wave: rows by DPP, then across rows with the two lane-swap
+// permutes (lane l meets l ^ 16, then l ^ 32).
+__device__ __forceinline__ float wave_max64(float v) {
+    v = dpp_max16(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 template <int KIND>
 __device__ __forceinline__ half8v unpack_b(uint32_t w) {
     if constexpr (KIND == COLI_KIND_FP4) {

@@ -21,6 +21,13 @@ struct FragSet {
     DevBuf p8, s8;    // e4m3 pieces + e8m0 scales for the MXFP4 GEMM (coli_prep_fp8)
     int prow = 0;     // rows per piece plane
     int gen8 = 0;     // generation of the last piece prep (flag slot 8 + set)
+    // The rows the set was last asked for (make_frags): the prep is deferred
+    // until a kernel needs fragments (flush_frags); a GEMV that converts f32
+    // activations itself reads px directly and never needs it.
+    bool pending = false;
+    const float *px = nullptr;
+    int pld = 0, pnrows = 0, pK = 0, pint4 = 0;
+    const int *psrc = nullptr, *pnrows_dev = nullptr;
 };
 
 struct DevCtx {
@@ -62,7 +69,7 @@ int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scale
 extern "C" {
 hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, int dual, int W, int max_rows,
                             hipStream_t st);
-hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual, int PD, int max_rows,
+hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual, int W, int PD, int max_rows,
                                 hipStream_t st);
 hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, const int *nrows_dev,
                                  int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
@@ -106,9 +113,12 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
 
 // Activation fragments of rows x[0..nrows) (or src_rows[r]; nrows_dev: live
 // count on the device) of width K into fragment set `set` (0/1: inputs of the
-// int4 / fp4 order, 2/3: hidden rows).
+// int4 / fp4 order, 2/3: hidden rows). Records the request; the prep runs
+// when a kernel first needs the fragments (flush_frags). x must hold its
+// values until then.
 int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
                const int *src_rows = nullptr, const int *nrows_dev = nullptr);
+int flush_frags(DevCtx *ctx, int set);
 int frag_set_of(int kind, bool hidden);
 // Activation pieces of the MXFP4 grouped GEMM (e4m3 + e8m0 per 32 columns)
 // of the same rows, into fragment set `set`.

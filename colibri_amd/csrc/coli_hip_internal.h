@@ -72,6 +72,8 @@ struct ColiGemvArgs {
     const int *xexp;          // per fragment row
     const int *haslo;         // == lo_gen when some lo part of this fragment set is non-zero
     int lo_gen;
+    const float *xf;          // non-null (coli_gemv_dma only): f32 activations, row r = xf + xrows-mapped r * ldx
+    int ldx;
     const _Float16 *zero;     // >= COLI_ZERO_BYTES of zeros: inactive batch lanes, dead tiles
     float *out;
     int ldo;

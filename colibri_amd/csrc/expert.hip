@@ -129,6 +129,25 @@ static int ngp_of(int K) { return (K + 127) / 128 * 4; }
 int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
                const int *src_rows, const int *nrows_dev) {
     FragSet &f = ctx->frag[set];
+    if (!x || nrows < 0 || K < 1 || ld < K) return 0;
+    f.pending = true;
+    f.px = x;
+    f.pld = ld;
+    f.pnrows = nrows;
+    f.pK = K;
+    f.pint4 = int4_order;
+    f.psrc = src_rows;
+    f.pnrows_dev = nrows_dev;
+    return 1;
+}
+
+int flush_frags(DevCtx *ctx, int set) {
+    FragSet &f = ctx->frag[set];
+    if (!f.pending) return 1;
+    f.pending = false;
+    const float *x = f.px;
+    const int ld = f.pld, nrows = f.pnrows, K = f.pK, int4_order = f.pint4;
+    const int *src_rows = f.psrc, *nrows_dev = f.pnrows_dev;
     int ngp = ngp_of(K);
     size_t halves = (size_t)nrows * ngp * 32;
     if (!reserve(ctx, &f.hi, halves * 2, 0) || !reserve(ctx, &f.lo, halves * 2, 0) ||
@@ -168,6 +187,13 @@ int make_frags8(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, 
                   "fp8 activation pieces");
 }
 
+// COLI_HIP_XF32=0 keeps the fragment prep for every GEMV (the LDS-ring
+// kernel then reads prepared fragments, as the tiled one always does).
+static bool xf32_enabled() {
+    const char *e = std::getenv("COLI_HIP_XF32");
+    return !(e && e[0] == '0');
+}
+
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
@@ -183,6 +209,22 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     FragSet &f = ctx->frag[set];
     ColiGemvArgs a;
     std::memset(&a, 0, sizeof(a));
+    // Up to 32768 activations (rows x K) on the LDS-ring kernel are read as
+    // f32 and converted in the kernel, which saves the prep launch; beyond,
+    // every workgroup staging the f32 rows costs more than the prep (the
+    // activations are re-read by every workgroup, at twice the bytes of the
+    // hi fragments).
+    if (pl.dma && max_rows <= 4 && (long)max_rows * nq * 128 <= 32768 && f.px && !f.psrc && f.pK == nq * 128 &&
+        f.pld % 4 == 0 && (uintptr_t)f.px % 16 == 0 && xf32_enabled()) {
+        a.xf = f.px;
+        a.ldx = f.pld;
+        // one row tile over a long K: sixteen waves, twice the per-quad
+        // conversion chains in flight per CU
+        if (pl.R == 1 && !dual && nq >= 64 && 16L * pl.PD * dma_slot_bytes(kind, 1, max_rows) <= 160 * 1024)
+            pl.W = 16;
+    } else if (!flush_frags(ctx, set)) {
+        return 0;
+    }
     a.prob = probs_dev;
     if (inline_prob) {
         a.prob = nullptr;
@@ -210,7 +252,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.swiglu_limit = swiglu_limit;
     a.partial = (float *)ctx->partial.p;
     a.split_cnt = (int *)ctx->split_cnt.p;
-    if (pl.dma) return hip_ok(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.PD, max_rows, ctx->stream),
+    if (pl.dma) return hip_ok(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.W, pl.PD, max_rows, ctx->stream),
                               "gemv launch");
     return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
 }
@@ -223,6 +265,7 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
              const int *xrows_dev, float *out, int ldo, float swiglu_limit) {
     if (n_mt <= 0) return 1;
     FragSet &f = ctx->frag[set];
+    if (!(kind == COLI_KIND_FP4 && mx_gemm_enabled()) && !flush_frags(ctx, set)) return 0;
     if (kind == COLI_KIND_FP4 && mx_gemm_enabled()) {
         ColiGemmMxArgs m;
         std::memset(&m, 0, sizeof(m));

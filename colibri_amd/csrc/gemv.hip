@@ -31,6 +31,9 @@
 
 #include <math.h>
 
+#include <algorithm>
+#include <cstdlib>
+
 #include "coli_device.h"
 
 // ---------------------------------------------------------------------------
@@ -110,16 +113,23 @@ __global__ void coli_repack_scales_e8(const uint8_t *__restrict__ src, int O, in
 // ---------------------------------------------------------------------------
 // For fragment row r (source row src_row[r] of x, f32 [.., ldx]; src_row[r]
 // < 0 marks an unused slot):
-//   E = exponent with max|x| * 2^-E in [0.5, 1) (0 for an all-zero row),
+//   E = exponent with max|x| * 2^-E in [2^14, 2^15) (0 for an all-zero row):
+//   the top of the fp16 range, so hi and lo stay normal for every value
+//   within 2^-18 of the row maximum (scaled to [0.5, 1) instead, every value
+//   below 2^-14 of the maximum turned subnormal and most of its contribution
+//   was lost in measurement),
 //   hi = fp16(x * 2^-E * m), lo = fp16(x * 2^-E * m - hi), m = 1/16 on the
 //   high-nibble columns of the int4 order, else 1.
 // Layout per row: [ngp groups][4 kslices][8 halves]; slot t of kslice s of
 // group g holds column 32g + 8s + perm[t], perm = {0,2,4,6,1,3,5,7} (int4)
 // or identity (fp4), matching the B-operand order built in the GEMV.
-// One 256-thread block per fragment row: the row is read once (up to 8 slots
-// of 8 columns per thread stay in registers between the maximum and the
-// conversion; longer rows re-read the rest), reduced to its maximum, then
-// converted. Whether any lo part is non-zero is published as `gen` into
+// nchunk 256-thread blocks per row (block = row * nchunk + chunk). Every block of a row reads the
+// whole row and reduces it to its maximum (the chunks re-read it from cache),
+// then converts only its own share: thread t's slots are t + 256 i, and block
+// c converts those with i % chunks == c. Up to 8 slots of 8 columns per
+// thread stay in registers between the maximum and the conversion; longer
+// rows re-read the rest. Splitting a row over blocks shortens the serial
+// conversion and store tail that one block per row would carry. Whether any lo part is non-zero is published as `gen` into
 // *haslo with an atomic max: the GEMV treats any flag >= its generation as
 // "lo present", so the flag never needs clearing and stays correct when a
 // captured graph replays an old generation.
@@ -129,9 +139,9 @@ __global__ __launch_bounds__(256) void coli_prep_frag(const float *__restrict__ 
                                                       const int *__restrict__ nrows_dev, int K, int ngp,
                                                       int int4_order, _Float16 *__restrict__ hi,
                                                       _Float16 *__restrict__ lo, int *__restrict__ exp2out,
-                                                      int *__restrict__ haslo, int gen, int vec,
+                                                      int *__restrict__ haslo, int gen, int vec, int nchunk,
                                                       const float *__restrict__ zero) {
-    const int r = blockIdx.x;
+    const int r = blockIdx.x / nchunk, chunk = blockIdx.x - r * nchunk;
     if (nrows_dev && r >= *nrows_dev) return;
     const int srow = src_row ? src_row[r] : r;
     if (srow < 0) return;
@@ -170,8 +180,11 @@ __global__ __launch_bounds__(256) void coli_prep_frag(const float *__restrict__ 
     __syncthreads();
     m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     int E = 0;
-    if (m > 0.0f && isfinite(m)) frexpf(m, &E);
-    if (threadIdx.x == 0) exp2out[r] = E;
+    if (m > 0.0f && isfinite(m)) {
+        frexpf(m, &E);
+        E -= 15;
+    }
+    if (threadIdx.x == 0 && chunk == 0) exp2out[r] = E;
     bool any = false;
     auto convert = [&](int slot, const float (&u)[8]) {
         if (slot >= nslot) return;
@@ -190,8 +203,11 @@ __global__ __launch_bounds__(256) void coli_prep_frag(const float *__restrict__ 
         *(half8v *)(lo + base) = (half8v){l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
     };
 #pragma unroll
-    for (int i = 0; i < COLI_PREP_SLOTS; i++) convert(threadIdx.x + 256 * i, v[i]);
-    for (int slot = threadIdx.x + 256 * COLI_PREP_SLOTS; slot < nslot; slot += 256) {
+    for (int i = 0; i < COLI_PREP_SLOTS; i++)
+        if (i % nchunk == chunk) convert(threadIdx.x + 256 * i, v[i]);
+    for (int i = COLI_PREP_SLOTS; 256 * i < nslot; i++) {
+        if (i % nchunk != chunk) continue;
+        const int slot = threadIdx.x + 256 * i;
         float u[8];
         load_slot(slot, u);
         convert(slot, u);
@@ -675,6 +691,7 @@ extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, i
                                        hipStream_t st) {
     int nb4 = max_rows <= 1 ? 1 : (max_rows <= 2 ? 2 : 4);
     if (!a->prob && (a->nprob != 1 || a->nprob_dev)) return hipErrorInvalidValue;   // inline problem: exactly one
+    if (a->xf) return hipErrorInvalidValue;   // this kernel reads prepared fragments only
     long items = (long)a->nprob * a->n_bt * a->rb_per_prob * a->splits;
     int blocks = (int)items;
     if (blocks <= 0) return hipSuccess;
@@ -693,8 +710,14 @@ extern "C" hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *
                                             hipStream_t st) {
     if (nrows <= 0) return hipSuccess;
     const int vec = ((uintptr_t)x % 16 == 0) && (ldx % 4 == 0) && (K % 8 == 0);
-    hipLaunchKernelGGL(coli_prep_frag, dim3(nrows), dim3(256), 0, st, x, ldx, src_row, nrows_dev, K, ngp, int4_order,
-                       hi, lo, exp2out, haslo, gen, vec, (const float *)zero);
+    // chunks per row: one per 256 slots (2048 columns), fewer when many rows
+    // already fill the chip
+    int nchunk = (ngp * 4 + 255) / 256;
+    const char *e = std::getenv("COLI_HIP_PREP_CHUNKS");
+    if (e) nchunk = std::max(1, std::min(nchunk, std::atoi(e)));
+    else if (nrows >= 64) nchunk = 1;
+    hipLaunchKernelGGL(coli_prep_frag, dim3((unsigned)(nrows * nchunk)), dim3(256), 0, st, x, ldx, src_row, nrows_dev,
+                       K, ngp, int4_order, hi, lo, exp2out, haslo, gen, vec, nchunk, (const float *)zero);
     return hipGetLastError();
 }
 

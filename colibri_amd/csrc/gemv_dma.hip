@@ -27,6 +27,17 @@
 // sixteen lanes of one k-slice read sixteen different bank groups (the
 // A-operand reads are free of bank conflicts). The ring always reserves room
 // for the lo fragments; they are fetched only when the fragment set has any.
+//
+// F32 (one to four batch rows, K a multiple of 128): no fragment prep at
+// all. The stage's activations arrive as f32 (the same NXR x 512 bytes the
+// hi + lo fragments would take) and each wave converts them in place before
+// its MFMAs: the exponent is taken per 128-column quad and batch row (E with
+// max|x| * 2^-E in [2^14, 2^15) over the quad, 0 for an all-zero quad), hi and lo
+// are split as in coli_prep_frag, and the quad's partial sum, over its four
+// groups, is scaled by 2^E into the accumulator. The lo MFMAs of a quad run
+// only when one of its lo parts is non-zero (a wave-uniform branch). Per-quad
+// exponents keep at least the precision of one exponent per row; the sums
+// differ from the fragment path in rounding only.
 #include "coli_hip_internal.h"
 
 #include <math.h>
@@ -39,6 +50,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 // LDS written by the DMA is invisible to the compiler's memory model: read it
 // through volatile pointers so no read is folded or reordered across a wait.
 #define LDS_RD(T, p) (*(const volatile __attribute__((address_space(3))) T *)(lds_void *)(p))
+#define LDS_WR(T, p, v) (*(volatile __attribute__((address_space(3))) T *)(lds_void *)(p) = (v))
 
 // Scale bytes of one tile quad: 16 rows x 4 groups of fp16 / f32 / e8m0.
 template <int KIND> struct ScaleGeom {
@@ -77,20 +89,87 @@ struct DmaGeom {
     static constexpr int kXOff = kScaleOff + kScaleInst * 256;
     static constexpr int kXInst = NXR == 1 ? 1 : NXR / 4;   // DMA instructions per fragment half
     static constexpr int kXBytes = NXR * 256;
-    static constexpr int kSlot = kXOff + 2 * kXBytes;     // room for hi + lo
+    static constexpr int kSlot = kXOff + 2 * kXBytes;     // room for hi + lo (= NXR rows of 128 f32)
+    static constexpr int kF32Inst = NXR == 1 ? 2 : NXR / 2;  // f32 DMA: 256 B (one row) / 1 KiB (two rows)
     static constexpr int loads(bool lo) { return R + kScaleInst + kXInst * (lo ? 2 : 1); }
+    static constexpr int loads_f32() { return R + kScaleInst + kF32Inst; }
 };
 
+// In-place conversion of one stage's f32 activations (NXR rows x 128, row
+// major at x) into hi / lo fragments at x / x + NXR * 256, laid out as the
+// fragment DMA would have left them. Returns 2^E of the lane's quad row in
+// *scale (NXR == 1: the one row; NXR == 4: row lane / 16) and whether any lo
+// part of the wave is non-zero. Every lane reads all its values before any
+// lane writes (one wave, LDS in order).
+template <int NXR, bool INT4>
+__device__ __forceinline__ bool f32_to_frags(uint8_t *x, int lane, int *E_out) {
+    if constexpr (NXR == 1) {
+        // lane: chunk c = lane / 4, fragment slots 2u, 2u + 1 (u = lane % 4)
+        const int c = lane >> 2, u = lane & 3;
+        const int col = 8 * c + (INT4 ? (u < 2 ? 4 * u : 4 * (u - 2) + 1) : 2 * u);
+        const int step = INT4 ? 2 : 1;
+        const float v0 = LDS_RD(float, x + col * 4), v1 = LDS_RD(float, x + (col + step) * 4);
+        const float m = wave_max64(fmaxf(fabsf(v0), fabsf(v1)));
+        int E = 0;
+        if (m > 0.0f && isfinite(m)) {
+            frexpf(m, &E);
+            E -= 15;
+        }
+        const float mul = (INT4 && u >= 2) ? 0.0625f : 1.0f;
+        const float y0 = ldexpf(v0, -E) * mul, y1 = ldexpf(v1, -E) * mul;
+        const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+        const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
+        LDS_WR(half2v, x + c * 16 + u * 4, ((half2v){h0, h1}));
+        LDS_WR(half2v, x + 256 + c * 16 + u * 4, ((half2v){l0, l1}));
+        *E_out = E;
+        return __builtin_amdgcn_ballot_w64(l0 != (_Float16)0.0f || l1 != (_Float16)0.0f) != 0;
+    } else if constexpr (NXR == 4) {
+        // lane: row rr = lane / 16, chunk c = lane % 16 (columns 8c .. 8c + 7)
+        const int rr = lane >> 4, c = lane & 15;
+        const floatx4 a = LDS_RD(floatx4, x + rr * 512 + c * 32), b = LDS_RD(floatx4, x + rr * 512 + c * 32 + 16);
+        const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        float m = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) m = fmaxf(m, fabsf(v[t]));
+        m = dpp_max16(m);
+        int E = 0;
+        if (m > 0.0f && isfinite(m)) {
+            frexpf(m, &E);
+            E -= 15;
+        }
+        half8v h, l;
+        bool any = false;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int off = INT4 ? (t < 4 ? 2 * t : 2 * (t - 4) + 1) : t;
+            float y = ldexpf(v[off], -E);
+            if (INT4 && (off & 1)) y *= 0.0625f;
+            h[t] = (_Float16)y;
+            l[t] = (_Float16)(y - (float)h[t]);
+            any |= l[t] != (_Float16)0.0f;
+        }
+        const int dst = (rr * 16 + (c ^ rr)) * 16;
+        LDS_WR(half8v, x + dst, h);
+        LDS_WR(half8v, x + NXR * 256 + dst, l);
+        *E_out = E;
+        return __builtin_amdgcn_ballot_w64(any) != 0;
+    } else {
+        *E_out = 0;   // not instantiated by a launch (F32 requires NXR 1 or 4)
+        return false;
+    }
+}
+
 // INL: the single problem a.prob0 (3-D grid: row block, 1, batch tile).
-template <int KIND, int R, bool DUAL, int NB4, int W, int PD, int NXR, bool INL>
+template <int KIND, int R, bool DUAL, int NB4, int W, int PD, int NXR, bool INL, bool F32>
 __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
     using G = DmaGeom<KIND, R, NXR>;
+    static_assert(!F32 || NXR == 1 || NXR == 4, "f32 activations: one or four rows per stage");
     constexpr bool XF = NXR > 1;
     constexpr int RT = DUAL ? R / 2 : R;
     constexpr int RING = W * PD * G::kSlot;
     constexpr int RED = W * R * NB4 * 64 * 4;
     static_assert(RING <= 160 * 1024 && RED <= 160 * 1024, "LDS budget");
-    static_assert((PD - 1) * G::loads(true) <= 63, "vmcnt range");
+    static_assert((PD - 1) * (F32 ? G::loads_f32() : G::loads(true)) <= 63, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[RING > RED ? RING : RED];
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -146,6 +225,19 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
         xsrc_hi[k] = (const uint8_t *)a.xhi + off;
         xsrc_lo[k] = (const uint8_t *)a.xlo + off;
     }
+    // f32 activations: instruction k fetches row 0, columns 64k + lane
+    // (NXR 1), or rows 2k + lane / 32, columns 4 (lane % 32) .. + 3 (NXR 4)
+    const uint8_t *xsrc_f[G::kF32Inst];
+    if constexpr (F32) {
+#pragma unroll
+        for (int k = 0; k < G::kF32Inst; k++) {
+            const int brow = NXR == 1 ? 0 : min(2 * k + (lane >> 5), nb - 1);
+            const int br = pr.xrow_off + 16 * bt + brow;
+            const int fr = a.xrows ? a.xrows[br] : br;
+            const int col = NXR == 1 ? 64 * k + lane : 4 * (lane & 31);
+            xsrc_f[k] = (const uint8_t *)(a.xf + (size_t)fr * a.ldx + col);
+        }
+    }
     uint8_t *ring = lds + wave * PD * G::kSlot;
     // the ring is written behind the compiler's back: let it escape, so the
     // "memory" clobbers of the waits below force fresh reads
@@ -174,6 +266,18 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
             }
             __builtin_amdgcn_global_load_lds((const void *)(base + qo + (lane % LPT) * 4),
                                              (lds_void *)(dst + G::kScaleOff + k * 256), 4, 0, 0);
+        }
+        if constexpr (F32) {
+#pragma unroll
+            for (int k = 0; k < G::kF32Inst; k++) {
+                if constexpr (NXR == 1)
+                    __builtin_amdgcn_global_load_lds((const void *)(xsrc_f[k] + (size_t)q * 512),
+                                                     (lds_void *)(dst + G::kXOff + k * 256), 4, 0, 0);
+                else
+                    __builtin_amdgcn_global_load_lds((const void *)(xsrc_f[k] + (size_t)q * 512),
+                                                     (lds_void *)(dst + G::kXOff + k * 1024), 16, 0, 0);
+            }
+            return;
         }
         const size_t xo = (size_t)q * 256;
         auto xdma = [&](const uint8_t *src, int off) {
@@ -229,6 +333,72 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
         }
     };
 
+    // F32: convert the stage, then the quad's partial sum over its four groups
+    // is scaled by 2^E of its batch row into the accumulator
+    auto compute_f32 = [&](int slot) {
+        uint8_t *src = ring + slot * G::kSlot;
+        int Eq;
+        const bool lo = f32_to_frags<NXR, KIND != COLI_KIND_FP4>(src + G::kXOff, lane, &Eq);
+        int Ei[NB4];
+#pragma unroll
+        for (int i = 0; i < NB4; i++)
+            Ei[i] = NXR == 1 ? __builtin_amdgcn_readfirstlane(Eq) : __builtin_amdgcn_readlane(Eq, 16 * i);
+        u32x4 w[R];
+        ScaleRegs<KIND> sc[R];
+        half8v xh[4], xl[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) xh[j] = LDS_RD(half8v, src + G::kXOff + xaddr(j));
+        if (lo) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) xl[j] = LDS_RD(half8v, src + G::kXOff + G::kXBytes + xaddr(j));
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = LDS_RD(u32x4, src + r * COLI_TILE_BYTES + lane * 16);
+            scale_from_lds<KIND>(sc[r], src + G::kScaleOff + r * ScaleGeom<KIND>::kBytes, lane & 15);
+        }
+        floatx4 t[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) t[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const half8v bw = unpack_b<KIND>(w[r][j]);
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if (lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
+                const float scl = sc[r].get(j);
+#pragma unroll
+                for (int i = 0; i < NB4; i++) t[r][i] = fmaf(d[i], scl, t[r][i]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < NB4; i++) acc[r][i] += ldexpf(t[r][i], Ei[i]);
+    };
+
+    auto run_f32 = [&]() {
+        constexpr int L = G::loads_f32();
+#pragma unroll
+        for (int s = 0; s < PD - 1; s++)
+            if (s < nit) issue(s, s, false);
+        for (int it0 = 0; it0 < nit; it0 += PD) {
+#pragma unroll
+            for (int u = 0; u < PD; u++) {
+                const int it = it0 + u;
+                if (it >= nit) break;
+                if (it + PD - 1 < nit) {
+                    issue(it + PD - 1, (u + PD - 1) % PD, false);
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PD - 1) * L) : "memory");
+                } else {
+                    dma_wait_tail<L, PD>(nit - 1 - it);
+                }
+                compute_f32(u);
+            }
+        }
+    };
+
     auto run = [&](auto lo_tag) {
         constexpr bool LO = decltype(lo_tag)::value;
         constexpr int L = G::loads(LO);
@@ -250,12 +420,13 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
             }
         }
     };
-    if (*a.haslo >= a.lo_gen) run(std::true_type{});   // >=: stays correct under graph replay
+    if constexpr (F32) run_f32();
+    else if (*a.haslo >= a.lo_gen) run(std::true_type{});   // >=: stays correct under graph replay
     else run(std::false_type{});
 
     // exponent of the batch row this wave finishes
     int E_out = 0;
-    if (wave < NB4) {
+    if (!F32 && wave < NB4) {
         const int brow = ks * 4 + wave;
         if (brow < nb) {
             const int br = pr.xrow_off + 16 * bt + brow;
@@ -287,62 +458,82 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
-template <int KIND, int R, bool DUAL, int NB4, int PD, int NXR>
-static hipError_t launch_dma4(const ColiGemvArgs &a, int blocks, hipStream_t st) {
-    constexpr int W = 8;
+template <int KIND, int R, bool DUAL, int NB4, int PD, int NXR, bool F32, int W>
+static hipError_t launch_dma6(const ColiGemvArgs &a, int blocks, hipStream_t st) {
     if constexpr (W * PD * DmaGeom<KIND, R, NXR>::kSlot > 160 * 1024) {
         return hipErrorInvalidConfiguration;
     } else {
         if (!a.prob)
-            hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, true>), dim3(a.rb_per_prob, 1, a.n_bt),
-                               dim3(64 * W), 0, st, a);
+            hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, true, F32>),
+                               dim3(a.rb_per_prob, 1, a.n_bt), dim3(64 * W), 0, st, a);
         else
-            hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, false>), dim3(blocks), dim3(64 * W), 0,
-                               st, a);
+            hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, false, F32>), dim3(blocks),
+                               dim3(64 * W), 0, st, a);
         return hipGetLastError();
     }
 }
 
+// W = 16 (one row tile, long K): twice the waves per CU to cover the
+// latency of each wave's serial per-quad chain.
+template <int KIND, int R, bool DUAL, int NB4, int PD, int NXR, bool F32>
+static hipError_t launch_dma5(const ColiGemvArgs &a, int W, int blocks, hipStream_t st) {
+    if constexpr (R == 1 && !DUAL) {
+        if (W == 16) return launch_dma6<KIND, R, DUAL, NB4, PD, NXR, F32, 16>(a, blocks, st);
+    }
+    return launch_dma6<KIND, R, DUAL, NB4, PD, NXR, F32, 8>(a, blocks, st);
+}
+
+template <int KIND, int R, bool DUAL, int NB4, int PD, int NXR>
+static hipError_t launch_dma4(const ColiGemvArgs &a, int W, int blocks, hipStream_t st) {
+    if constexpr (NXR == 1 || NXR == 4) {
+        if (a.xf) return launch_dma5<KIND, R, DUAL, NB4, PD, NXR, true>(a, W, blocks, st);
+    }
+    return launch_dma5<KIND, R, DUAL, NB4, PD, NXR, false>(a, W, blocks, st);
+}
+
 template <int KIND, int R, bool DUAL, int NB4, int NXR>
-static hipError_t launch_dma3(const ColiGemvArgs &a, int PD, int blocks, hipStream_t st) {
-    if (PD == 2) return launch_dma4<KIND, R, DUAL, NB4, 2, NXR>(a, blocks, st);
-    return launch_dma4<KIND, R, DUAL, NB4, 3, NXR>(a, blocks, st);
+static hipError_t launch_dma3(const ColiGemvArgs &a, int W, int PD, int blocks, hipStream_t st) {
+    if (PD == 2) return launch_dma4<KIND, R, DUAL, NB4, 2, NXR>(a, W, blocks, st);
+    return launch_dma4<KIND, R, DUAL, NB4, 3, NXR>(a, W, blocks, st);
 }
 
 template <int KIND, int R, bool DUAL>
-static hipError_t launch_dma2(const ColiGemvArgs &a, int max_rows, int PD, int blocks, hipStream_t st) {
-    if (max_rows <= 1) return launch_dma3<KIND, R, DUAL, 1, 1>(a, PD, blocks, st);
-    if (max_rows <= 2) return launch_dma3<KIND, R, DUAL, 2, 4>(a, PD, blocks, st);
-    if (max_rows <= 4) return launch_dma3<KIND, R, DUAL, 4, 4>(a, PD, blocks, st);
-    if (max_rows <= 8) return launch_dma3<KIND, R, DUAL, 4, 8>(a, PD, blocks, st);
-    return launch_dma3<KIND, R, DUAL, 4, 16>(a, PD, blocks, st);
+static hipError_t launch_dma2(const ColiGemvArgs &a, int W, int max_rows, int PD, int blocks, hipStream_t st) {
+    if (max_rows <= 1) return launch_dma3<KIND, R, DUAL, 1, 1>(a, W, PD, blocks, st);
+    if (max_rows <= 2) return launch_dma3<KIND, R, DUAL, 2, 4>(a, W, PD, blocks, st);
+    if (max_rows <= 4) return launch_dma3<KIND, R, DUAL, 4, 4>(a, W, PD, blocks, st);
+    if (max_rows <= 8) return launch_dma3<KIND, R, DUAL, 4, 8>(a, W, PD, blocks, st);
+    return launch_dma3<KIND, R, DUAL, 4, 16>(a, W, PD, blocks, st);
 }
 
 template <int KIND>
-static hipError_t launch_dma1(const ColiGemvArgs &a, int R, bool dual, int max_rows, int PD, int blocks,
+static hipError_t launch_dma1(const ColiGemvArgs &a, int R, bool dual, int W, int max_rows, int PD, int blocks,
                               hipStream_t st) {
     if (dual) {
-        if (R == 4) return launch_dma2<KIND, 4, true>(a, max_rows, PD, blocks, st);
-        return launch_dma2<KIND, 2, true>(a, max_rows, PD, blocks, st);
+        if (R == 4) return launch_dma2<KIND, 4, true>(a, W, max_rows, PD, blocks, st);
+        return launch_dma2<KIND, 2, true>(a, W, max_rows, PD, blocks, st);
     }
-    if (R == 4) return launch_dma2<KIND, 4, false>(a, max_rows, PD, blocks, st);
-    if (R == 2) return launch_dma2<KIND, 2, false>(a, max_rows, PD, blocks, st);
-    return launch_dma2<KIND, 1, false>(a, max_rows, PD, blocks, st);
+    if (R == 4) return launch_dma2<KIND, 4, false>(a, W, max_rows, PD, blocks, st);
+    if (R == 2) return launch_dma2<KIND, 2, false>(a, W, max_rows, PD, blocks, st);
+    return launch_dma2<KIND, 1, false>(a, W, max_rows, PD, blocks, st);
 }
 
 // Returns hipErrorInvalidConfiguration for a decomposition the ring cannot
 // hold (the caller then uses coli_gemv_tiles).
-extern "C" hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual, int PD, int max_rows,
+extern "C" hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual, int W, int PD, int max_rows,
                                            hipStream_t st) {
-    if (a->splits != 1 || max_rows < 1 || max_rows > 16) return hipErrorInvalidValue;
+    if (a->splits != 1 || max_rows < 1 || max_rows > 16 || (W != 8 && W != 16)) return hipErrorInvalidValue;
+    // f32 activations: up to four rows, rows of whole quads, 16-byte aligned
+    if (a->xf && (max_rows > 4 || a->ldx < a->nq * 128 || a->ldx % 4 || (uintptr_t)a->xf % 16))
+        return hipErrorInvalidValue;
     if (!a->prob && (a->nprob != 1 || a->nprob_dev)) return hipErrorInvalidValue;
     const long items = (long)a->nprob * a->n_bt * a->rb_per_prob;
     if (items <= 0) return hipSuccess;
     const int blocks = (int)items;
     switch (kind) {
-    case COLI_KIND_I4_H: return launch_dma1<COLI_KIND_I4_H>(*a, R, dual, max_rows, PD, blocks, st);
-    case COLI_KIND_I4_F: return launch_dma1<COLI_KIND_I4_F>(*a, R, dual, max_rows, PD, blocks, st);
-    case COLI_KIND_FP4: return launch_dma1<COLI_KIND_FP4>(*a, R, dual, max_rows, PD, blocks, st);
+    case COLI_KIND_I4_H: return launch_dma1<COLI_KIND_I4_H>(*a, R, dual, W, max_rows, PD, blocks, st);
+    case COLI_KIND_I4_F: return launch_dma1<COLI_KIND_I4_F>(*a, R, dual, W, max_rows, PD, blocks, st);
+    case COLI_KIND_FP4: return launch_dma1<COLI_KIND_FP4>(*a, R, dual, W, max_rows, PD, blocks, st);
     default: return hipErrorInvalidValue;
     }
 }

@@ -242,3 +242,78 @@ def test_fp4_matvec_kat(session):
     finally:
         session.free(h)
     assert y[0, 0] == 128.0
+
+
+def wild_x(rng, S, I):
+    """Activations that stress the per-quad exponent of the f32 path: full
+    f32 mantissas (lo parts), quads scaled by 2^-24 .. 2^20, an all-zero
+    quad, subnormals and one quad holding a single large value."""
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    nq = (I + 127) // 128
+    for s in range(S):
+        for q in range(nq):
+            x[s, 128 * q:128 * (q + 1)] *= np.float32(2.0 ** int(rng.integers(-24, 21)))
+    if nq > 1:
+        x[:, 128:256] = 0.0
+    x[0, :16] = np.float32(1e-40)
+    if nq > 2:
+        x[-1, 256:384] = 0.0
+        x[-1, 300] = 3.0e4
+    return x
+
+
+def outlier_x(rng, S, I):
+    """Gaussian rows with a few massive activations (up to 1e6 x typical):
+    with the fragments scaled to [0.5, 1) of the row maximum instead of the
+    top of the fp16 range, the typical values turned subnormal and these rows
+    failed the tolerance."""
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    amp = [1e2, 3e4, 1e6, 5e3]
+    for s in range(S):
+        x[s, 7] = amp[s % 4]
+        x[s, (131 * s + 300) % I] = -amp[(s + 1) % 4] / 3
+    return x
+
+
+# Both GEMV kernels and both activation paths of the LDS-ring kernel (f32
+# rows converted in the kernel, per-quad exponents; or prepared fragments,
+# per-row exponents) on the same inputs. The extreme per-quad ranges of
+# wild_x (2^44 across a row) are for the per-quad path only.
+@pytest.mark.parametrize("mode", [("dma", "1"), ("dma", "0"), ("tiles", "1")])
+@pytest.mark.parametrize("fmt", ["i4h", "i4f", "mx"])
+@pytest.mark.parametrize("S", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("O,I,xkind", [(256, 1024, "bf16"), (96, 768, "wild"), (128, 640, "outlier"),
+                                       (40, 384, "f32"), (48, 200, "f32")])
+def test_gemv_kernel_paths(session, monkeypatch, mode, fmt, S, O, I, xkind):
+    if xkind == "wild" and (mode != ("dma", "1") or S > 4):
+        pytest.skip("per-row exponent: a 2^44 range inside one row is beyond the fragment path")
+    monkeypatch.setenv("COLI_HIP_GEMV", mode[0])
+    monkeypatch.setenv("COLI_HIP_XF32", mode[1])
+    rng = np.random.default_rng(S * 1000 + O + I)
+    if xkind == "bf16":
+        x = rand_x(rng, S, I)
+    elif xkind == "wild":
+        x = wild_x(rng, S, I)
+    elif xkind == "outlier":
+        x = outlier_x(rng, S, I)
+    else:
+        x = rng.standard_normal((S, I)).astype(np.float32)
+    if fmt == "mx":
+        q4, e8 = rand_mxfp4(rng, O, I)
+        h = session.upload_mxfp4(q4, e8, I, O)
+        ref = cref.matmul_mxfp4(x, q4, e8, O, I)
+        mag = magnitude(x, deq_mxfp4(q4, e8, I))
+        fmtc, gs = 7, 32
+    else:
+        q4, sc = rand_i4(rng, O, I, 32, fp16_scales=fmt == "i4h")
+        h = session.upload(q4, sc, 4, I, O, 32)
+        ref = cref.matmul_i4_grouped(x, q4, sc, O, I, 32)
+        mag = magnitude(x, deq_i4(q4, sc, I, 32))
+        fmtc, gs = 4, 32
+    try:
+        y = session.matmul(h, x, fmtc, I, O, gs)
+        y2 = session.matmul(h, x, fmtc, I, O, gs)
+    finally:
+        session.free(h)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    check(y, ref, mag)
