@@ -104,9 +104,12 @@ int coli_hip_moe_last_union(ColiHipMoe *moe, int *nu, int *uniq);
 
 /* ---- plumbing for benchmarks and tests ----------------------------------- */
 /* coli_cuda_pipe_gemm in two halves, so a timer can bracket the GEMV kernel
- * alone: prep builds the activation fragments of x_dev[S, I] for the
- * tensor's storage kind; run launches the GEMV y_dev[S, O] on them. A run
- * must follow the prep of the same kind of tensor and the same S. */
+ * alone: prep names the activations x_dev[S, I] for the tensor's storage
+ * kind (no launch); run launches the GEMV y_dev[S, O]. The first run after a
+ * prep also launches the fragment build when its kernel needs fragments (the
+ * LDS-ring kernel of up to 32768 activations reads x_dev itself), so x_dev
+ * must hold its values until the runs are issued. A run must follow the prep
+ * of the same kind of tensor and the same S. */
 int coli_hip_gemm_prep_dev(ColiCudaTensor *tensor, const float *x_dev, int S);
 int coli_hip_gemm_run_dev(ColiCudaTensor *tensor, float *y_dev, int S);
 /* Fill n bytes of device memory with uniform pseudo-random bytes (seeded,
