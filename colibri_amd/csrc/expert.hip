@@ -225,6 +225,16 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     } else if (!flush_frags(ctx, set)) {
         return 0;
     }
+    // ring depth override (tuning; deeper rings measured slower: fewer
+    // workgroups fit a CU): the deeper of 2, 3 that fits
+    if (const char *e = std::getenv("COLI_HIP_DMA_PD"); e && pl.dma) {
+        const int want = std::atoi(e);
+        for (int PD : {3, 2})
+            if (PD <= want && (long)pl.W * PD * dma_slot_bytes(kind, pl.R, max_rows) <= 160 * 1024) {
+                pl.PD = PD;
+                break;
+            }
+    }
     a.prob = probs_dev;
     if (inline_prob) {
         a.prob = nullptr;

@@ -74,6 +74,7 @@ __device__ __forceinline__ void dma_wait_tail(int pend) {
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(k * L) : "memory");       \
         return;                                                            \
     }
+    if constexpr (PD > 5) { COLI_WT(4) }
     if constexpr (PD > 4) { COLI_WT(3) }
     if constexpr (PD > 3) { COLI_WT(2) }
     if constexpr (PD > 2) { COLI_WT(1) }
@@ -460,7 +461,8 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
 // ---------------------------------------------------------------------------
 template <int KIND, int R, bool DUAL, int NB4, int PD, int NXR, bool F32, int W>
 static hipError_t launch_dma6(const ColiGemvArgs &a, int blocks, hipStream_t st) {
-    if constexpr (W * PD * DmaGeom<KIND, R, NXR>::kSlot > 160 * 1024) {
+    using G = DmaGeom<KIND, R, NXR>;
+    if constexpr (W * PD * G::kSlot > 160 * 1024 || (PD - 1) * (F32 ? G::loads_f32() : G::loads(true)) > 63) {
         return hipErrorInvalidConfiguration;
     } else {
         if (!a.prob)

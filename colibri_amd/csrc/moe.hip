@@ -21,6 +21,7 @@
 // returns to the host between stages, and no stage allocates once the layer
 // has run at a given S.
 #include "coli_hip_host.h"
+#include "coli_route.h"
 
 #include "coli_backend_abi.h"
 #include "coli_hip_ext.h"
@@ -47,6 +48,7 @@ struct ColiHipMoe {
     int *state = nullptr;     // [0] problems, [1] packed rows, [2] union size, [3] GEMM row tiles
     int *uniq = nullptr, *xrows = nullptr, *slotrow = nullptr, *mt = nullptr;
     ColiProb *pdual = nullptr, *pdown = nullptr;
+    int *route_cnt = nullptr;   // arrival counter of coli_moe_route (zero between launches)
 };
 
 // ---------------------------------------------------------------------------
@@ -60,14 +62,14 @@ struct ColiHipMoe {
 // addresses rows through slotrow).
 // Also emits the GEMM work list (expert << 16 | 64-row tile) in union order.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void coli_moe_union(const int *__restrict__ idx, const int *__restrict__ keff,
-                                                       int S, int K, int E, int has_shared,
-                                                       const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
-                                                       ColiProb *__restrict__ pdown, int *__restrict__ uniq,
-                                                       int *__restrict__ xrows, int *__restrict__ slotrow,
-                                                       int *__restrict__ mt, int *__restrict__ state) {
+// The body runs on any block size; sm: (7 E + 5) ints of LDS. idx / keff may
+// point to LDS.
+__device__ __forceinline__ void moe_union_body(const int *idx, const int *keff, int S, int K, int E, int has_shared,
+                                               const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
+                                               ColiProb *__restrict__ pdown, int *__restrict__ uniq,
+                                               int *__restrict__ xrows, int *__restrict__ slotrow,
+                                               int *__restrict__ mt, int *__restrict__ state, int *sm) {
     // first [E] | cnt [E] | cur [E] | rank [E] | order [E + 1] | off [E + 2] | toff [E + 2]
-    extern __shared__ int sm[];
     int *first = sm, *cnt = first + E, *cur = cnt + E, *rank = cur + E, *order = rank + E, *off = order + E + 1,
         *toff = off + E + 2;
     __shared__ int s_nu;
@@ -150,6 +152,61 @@ __global__ __launch_bounds__(1024) void coli_moe_union(const int *__restrict__ i
     }
 }
 
+__global__ __launch_bounds__(1024) void coli_moe_union(const int *__restrict__ idx, const int *__restrict__ keff,
+                                                       int S, int K, int E, int has_shared,
+                                                       const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
+                                                       ColiProb *__restrict__ pdown, int *__restrict__ uniq,
+                                                       int *__restrict__ xrows, int *__restrict__ slotrow,
+                                                       int *__restrict__ mt, int *__restrict__ state) {
+    extern __shared__ int sm[];
+    moe_union_body(idx, keff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, sm);
+}
+
+// ---------------------------------------------------------------------------
+// Decode routing in one launch (S <= 16, up to 128 workgroups): router partial logits, top-K
+// selection and union. Every workgroup computes the partials of 4 experts x
+// one 512-column chunk and publishes them as agent-scope atomics (coherent
+// across the XCDs' L2s), waits for its stores, then counts its arrival; the
+// last workgroup to arrive runs the selection of every row (one wave per row,
+// the partials read back as agent-scope atomics) and the union, and resets
+// the counter for the next launch. No workgroup waits for another. Same
+// arithmetic, order and results as the three separate kernels.
+// ---------------------------------------------------------------------------
+template <int SMAX, int JM>
+__global__ __launch_bounds__(256) void coli_moe_route(const float *__restrict__ x, int S, const float *__restrict__ W,
+                                                      int D, int E, float *__restrict__ part, int nch,
+                                                      const float *__restrict__ bias, int K, int mode, float topp,
+                                                      int norm_topk, float routed_scale, int *__restrict__ idx,
+                                                      float *__restrict__ wsel, int *__restrict__ keff,
+                                                      int *__restrict__ counter, int has_shared,
+                                                      const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
+                                                      ColiProb *__restrict__ pdown, int *__restrict__ uniq,
+                                                      int *__restrict__ xrows, int *__restrict__ slotrow,
+                                                      int *__restrict__ mt, int *__restrict__ state) {
+    extern __shared__ int sm[];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int neb = (E + 3) / 4;
+    const int eb = blockIdx.x % neb, ch = blockIdx.x / neb;
+    router_partial_wave<SMAX, true>(x, S, W, D, E, part, (size_t)S * E, eb * 4 + wave, ch, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == (int)gridDim.x - 1;
+        if (s_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // LDS: slots [S K] | keff [S] | selection weights [4 E] floats, then the union's (7 E + 5) ints
+    int *sidx = sm, *skeff = sm + S * K, *work = skeff + S;
+    for (int s = wave; s < S; s += 4)
+        select_row<JM, true>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
+                             (float *)work + (size_t)wave * E, s, lane, sidx, skeff);
+    __syncthreads();
+    moe_union_body(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, work);
+}
+
 // out[t, d] = sum_{kk < keff[t]} w[t, kk] * y[slotrow[t, kk], d]  (+ y[shared row of t])
 __global__ void coli_moe_combine(const float *__restrict__ y, int D, const float *__restrict__ w,
                                  const int *__restrict__ keff, const int *__restrict__ slotrow, int K,
@@ -171,7 +228,7 @@ extern "C" void coli_hip_moe_free(ColiHipMoe *m) {
         (void)hipStreamSynchronize(ctx->stream);
     }
     void *bufs[] = {m->rw, m->rb, m->tab, m->logits, m->wsel, m->h, m->y, m->idx, m->keff, m->state,
-                    m->uniq, m->xrows, m->slotrow, m->mt, m->pdual, m->pdown};
+                    m->uniq, m->xrows, m->slotrow, m->mt, m->pdual, m->pdown, m->route_cnt};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     delete m;
@@ -212,7 +269,9 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
              hip_ok(hipMemcpy(m->rw, router_w, rwb, hipMemcpyHostToDevice), "router weights upload") &&
              hip_ok(hipMalloc((void **)&m->tab, tab.size() * sizeof(ColiProb)), "expert table") &&
              hip_ok(hipMemcpy(m->tab, tab.data(), tab.size() * sizeof(ColiProb), hipMemcpyHostToDevice),
-                    "expert table upload");
+                    "expert table upload") &&
+             hip_ok(hipMalloc((void **)&m->route_cnt, sizeof(int)), "routing counter") &&
+             hip_ok(hipMemset(m->route_cnt, 0, sizeof(int)), "routing counter clear");
     if (ok && router_bias)
         ok = hip_ok(hipMalloc((void **)&m->rb, (size_t)c.E * sizeof(float)), "router bias") &&
              hip_ok(hipMemcpy(m->rb, router_bias, (size_t)c.E * sizeof(float), hipMemcpyHostToDevice),
@@ -256,6 +315,44 @@ static int moe_reserve(DevCtx *ctx, ColiHipMoe *m, int S) {
     return 1;
 }
 
+// COLI_HIP_FUSED_ROUTE=0 runs the router, selection and union as three
+// launches at every S.
+static bool fused_route_disabled() {
+    const char *e = std::getenv("COLI_HIP_FUSED_ROUTE");
+    return e && e[0] == '0';
+}
+
+static int launch_route(ColiHipMoe *m, const float *x_dev, int S, hipStream_t st) {
+    const ColiHipMoeConfig &c = m->cfg;
+    const int nch = coli_router_chunks(c.D), neb = (c.E + 3) / 4;
+    const size_t work = std::max((size_t)4 * c.E * sizeof(float), (size_t)(7 * c.E + 5) * sizeof(int));
+    const size_t shm = (size_t)(S * c.K + S) * sizeof(int) + work;
+    const int jm = c.E <= 64 ? 1 : c.E <= 128 ? 2 : c.E <= 256 ? 4 : c.E <= 512 ? 8 : 16;
+    const dim3 grid((unsigned)(neb * nch)), block(256);
+#define COLI_ROUTE_ARGS                                                                                         \
+    x_dev, S, m->rw, c.D, c.E, m->logits, nch, m->rb, c.K, c.route_mode, c.topp, c.norm_topk, c.routed_scale, \
+        m->idx, m->wsel, m->keff, m->route_cnt, c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows,  \
+        m->slotrow, m->mt, m->state
+#define COLI_ROUTE_JM(SM)                                                                                    \
+    switch (jm) {                                                                                            \
+    case 1: hipLaunchKernelGGL((coli_moe_route<SM, 1>), grid, block, shm, st, COLI_ROUTE_ARGS); break;       \
+    case 2: hipLaunchKernelGGL((coli_moe_route<SM, 2>), grid, block, shm, st, COLI_ROUTE_ARGS); break;       \
+    case 4: hipLaunchKernelGGL((coli_moe_route<SM, 4>), grid, block, shm, st, COLI_ROUTE_ARGS); break;       \
+    case 8: hipLaunchKernelGGL((coli_moe_route<SM, 8>), grid, block, shm, st, COLI_ROUTE_ARGS); break;       \
+    default: hipLaunchKernelGGL((coli_moe_route<SM, 16>), grid, block, shm, st, COLI_ROUTE_ARGS); break;     \
+    }
+    if (S == 1) {
+        COLI_ROUTE_JM(1)
+    } else if (S <= 4) {
+        COLI_ROUTE_JM(4)
+    } else {
+        COLI_ROUTE_JM(16)
+    }
+#undef COLI_ROUTE_JM
+#undef COLI_ROUTE_ARGS
+    return hip_ok(hipGetLastError(), "moe routing");
+}
+
 extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float *out_dev, int S) {
     if (fault_injected()) return 0;
     if (!m || !x_dev || !out_dev || S < 1 || S > COLI_MOE_MAX_ROWS || S * m->cfg.K > COLI_MOE_MAX_SEL) return 0;
@@ -271,16 +368,24 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     const bool gemm = S > COLI_GEMM_MIN_ROWS, mx = gemm && m->kind == COLI_KIND_FP4 && mx_gemm_enabled();
     // 1. activation fragments, 2-3. router
     if (!(mx ? make_frags8(ctx, fx, x_dev, c.D, S, c.D) : make_frags(ctx, fx, x_dev, c.D, S, c.D, int4))) return 0;
-    const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
-    if (!nch || !hip_ok(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
-                                                  c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, st),
-                        "moe router select"))
-        return 0;
-    // 4. union
-    const size_t ush = (size_t)(7 * c.E + 5) * sizeof(int);
-    hipLaunchKernelGGL(coli_moe_union, dim3(1), dim3(1024), ush, st, m->idx, m->keff, S, c.K, c.E, c.has_shared,
-                       m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state);
-    if (!hip_ok(hipGetLastError(), "moe union")) return 0;
+    // One launch when few workgroups arrive: every arrival is an atomic on
+    // one counter, and hundreds of them serialize (measured: 896 arrivals
+    // cost more than the two launches they save).
+    if (S <= 16 && (long)((c.E + 3) / 4) * coli_router_chunks(c.D) <= 128 && !fused_route_disabled()) {
+        // 2-4. router, selection and union in one launch
+        if (!launch_route(m, x_dev, S, st)) return 0;
+    } else {
+        const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
+        if (!nch || !hip_ok(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
+                                                      c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, st),
+                            "moe router select"))
+            return 0;
+        // 4. union
+        const size_t ush = (size_t)(7 * c.E + 5) * sizeof(int);
+        hipLaunchKernelGGL(coli_moe_union, dim3(1), dim3(1024), ush, st, m->idx, m->keff, S, c.K, c.E, c.has_shared,
+                           m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state);
+        if (!hip_ok(hipGetLastError(), "moe union")) return 0;
+    }
     // 5. gate/up + SwiGLU over the union, 6. hidden fragments, 7. down
     const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
     if (gemm) {

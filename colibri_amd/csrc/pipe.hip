@@ -60,16 +60,8 @@ __global__ void coli_sum_slots(float *dst, const float *slots, int n, int D) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// Router logits: logits[s, e] = sum_d x[s, d] * W[e, d], f32 (the router GEMV
-// of c/colibri.c:3978 / c/olmoe.c:648), in two fixed-order halves so the
-// 4-byte router weights stream from every CU at once:
-//  * coli_router_partial: one wave per (expert, 512-column chunk); lane l
-//    covers columns 4l..4l+3 of each 256-column step, then a fixed butterfly
-//    gives part[chunk][s][e];
-//  * the selection kernel adds the chunks in chunk order while it reads them.
-// ---------------------------------------------------------------------------
-#define COLI_ROUTER_CHUNK 512
+#include "coli_route.h"
+
 template <int SMAX>
 __global__ __launch_bounds__(256) void coli_router_partial(const float *__restrict__ x, int S,
                                                            const float *__restrict__ W, int D, int E,
@@ -77,44 +69,7 @@ __global__ __launch_bounds__(256) void coli_router_partial(const float *__restri
     // readfirstlane: the wave index is wave-uniform, so everything derived from it
     // (tile indices, validity, base pointers) stays in scalar registers.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int e = blockIdx.x * 4 + wave, ch = blockIdx.y;
-    if (e >= E) return;
-    const float *wr = W + (size_t)e * D;
-    float acc[SMAX];
-#pragma unroll
-    for (int s = 0; s < SMAX; s++) acc[s] = 0.0f;
-#pragma unroll
-    for (int step = 0; step < COLI_ROUTER_CHUNK / 256; step++) {
-        const int d = ch * COLI_ROUTER_CHUNK + step * 256 + lane * 4;
-        if (d >= D) break;
-        if ((D & 3) == 0) {
-            const float4 wv = *(const float4 *)(wr + d);
-#pragma unroll
-            for (int s = 0; s < SMAX; s++) {
-                if (s >= S) break;
-                const float4 xv = *(const float4 *)(x + (size_t)s * D + d);
-                float a = xv.x * wv.x;
-                a = fmaf(xv.y, wv.y, a);
-                a = fmaf(xv.z, wv.z, a);
-                acc[s] += fmaf(xv.w, wv.w, a);
-            }
-        } else {
-            for (int t = 0; t < 4 && d + t < D; t++) {
-                const float wv = wr[d + t];
-#pragma unroll
-                for (int s = 0; s < SMAX; s++)
-                    if (s < S) acc[s] = fmaf(x[(size_t)s * D + d + t], wv, acc[s]);
-            }
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < SMAX; s++) {
-        if (s >= S) break;
-        float v = acc[s];
-#pragma unroll
-        for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0) part[(size_t)ch * chstride + (size_t)s * E + e] = v;
-    }
+    router_partial_wave<SMAX, false>(x, S, W, D, E, part, chstride, blockIdx.x * 4 + wave, blockIdx.y, lane);
 }
 
 extern "C" int coli_router_chunks(int D) { return (D + COLI_ROUTER_CHUNK - 1) / COLI_ROUTER_CHUNK; }
@@ -139,114 +94,6 @@ extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const flo
     return hipGetLastError();
 }
 
-// ---------------------------------------------------------------------------
-// Top-K selection, one 64-lane wave per token row (E <= 1024, K <= 64). The
-// logits are the sum of the router's column-chunk partials, added in chunk
-// order.
-//   mode 0: p = softmax(z) (max-subtracted, c/olmoe.c:246-250), select on p,
-//           weight p, optional norm over K without epsilon (c/olmoe.c:681).
-//   mode 1: p = sigmoid(z), choice = p + bias, select on choice, weight p,
-//           TOPP (sort by weight, tot = 1e-20 + sum, keep until cum >=
-//           topp * tot), norm_topk (sum + 1e-20), x routed_scale
-//           (c/backend_cuda.cu:2169-2194, c/colibri.c:3982-4126).
-//   mode 2: as mode 1 for the selection; weights renormalized over the K
-//           with +1e-20; TOPP keeps until cum >= topp and renormalizes the
-//           kept set (c/kimi_k3.c:1337-1370); routed_scale applied after.
-//   mode 3: DeepSeek-V4 (c/deepseek_v4.c:1368-1432): p = sqrt(softplus(z))
-//           (stable form), choice = p + bias, weights p / sum over the K x
-//           routed_scale; a non-positive sum selects nothing (keff 0).
-// The reference selects by K rounds of an argmax with strict '>' (highest
-// value, lowest index on ties; NaN and values <= -1e30 never chosen; a round
-// with nothing left picks index kk, c/route_trace.h:383-393). The same rounds
-// run here across the wave: each is a 64-lane argmax over order-preserving
-// keys, which leaves the chosen expert and its weight in lane kk; the
-// post-processing (normalization, TOPP ranks and cumulative sums) then runs
-// with one slot per lane.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool valid_score(float v) { return v == v && v > -1e30f; }
-
-// Wave-wide reductions without LDS round trips: a butterfly inside each
-// 16-lane row through DPP lane moves (quad_perm xor 1, xor 2, then row
-// rotations by 4 and 8), then the four row results read into scalar registers
-// and combined in row order. Every lane returns the same value; the
-// combination order is fixed, so results are reproducible.
-template <int CTRL>
-__device__ __forceinline__ int dpp_mov(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-#define COLI_DPP_XOR1 0xB1    // quad_perm [1, 0, 3, 2]
-#define COLI_DPP_XOR2 0x4E    // quad_perm [2, 3, 0, 1]
-#define COLI_DPP_ROR4 0x124   // row_ror:4
-#define COLI_DPP_ROR8 0x128   // row_ror:8
-
-template <typename Op>
-__device__ __forceinline__ float wave_reduce(float v, Op op) {
-    v = op(v, __int_as_float(dpp_mov<COLI_DPP_XOR1>(__float_as_int(v))));
-    v = op(v, __int_as_float(dpp_mov<COLI_DPP_XOR2>(__float_as_int(v))));
-    v = op(v, __int_as_float(dpp_mov<COLI_DPP_ROR4>(__float_as_int(v))));
-    v = op(v, __int_as_float(dpp_mov<COLI_DPP_ROR8>(__float_as_int(v))));
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return op(op(op(r0, r1), r2), r3);
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    return wave_reduce(v, [](float a, float b) { return a + b; });
-}
-__device__ __forceinline__ float wave_max(float v) {
-    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-    v += dpp_mov<COLI_DPP_XOR1>(v);
-    v += dpp_mov<COLI_DPP_XOR2>(v);
-    v += dpp_mov<COLI_DPP_ROR4>(v);
-    v += dpp_mov<COLI_DPP_ROR8>(v);
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
-           __builtin_amdgcn_readlane(v, 48);
-}
-__device__ __forceinline__ int wave_min_i(int v) {
-    v = min(v, dpp_mov<COLI_DPP_XOR1>(v));
-    v = min(v, dpp_mov<COLI_DPP_XOR2>(v));
-    v = min(v, dpp_mov<COLI_DPP_ROR4>(v));
-    v = min(v, dpp_mov<COLI_DPP_ROR8>(v));
-    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
-}
-// Argmax over (key, then lowest index) carrying a payload; uniform result.
-__device__ __forceinline__ void wave_argmax(unsigned &k, int &e, float &w) {
-    auto step = [&](unsigned ok, int oe, float ow) {
-        if (ok > k || (ok == k && oe < e)) {
-            k = ok;
-            e = oe;
-            w = ow;
-        }
-    };
-#define COLI_ARGMAX_STEP(CTRL) \
-    step((unsigned)dpp_mov<CTRL>((int)k), dpp_mov<CTRL>(e), __int_as_float(dpp_mov<CTRL>(__float_as_int(w))))
-    COLI_ARGMAX_STEP(COLI_DPP_XOR1);
-    COLI_ARGMAX_STEP(COLI_DPP_XOR2);
-    COLI_ARGMAX_STEP(COLI_DPP_ROR4);
-    COLI_ARGMAX_STEP(COLI_DPP_ROR8);
-#undef COLI_ARGMAX_STEP
-    unsigned rk[4];
-    int re[4];
-    float rw[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        rk[r] = (unsigned)__builtin_amdgcn_readlane((int)k, 16 * r);
-        re[r] = __builtin_amdgcn_readlane(e, 16 * r);
-        rw[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 16 * r));
-    }
-    k = rk[0];
-    e = re[0];
-    w = rw[0];
-#pragma unroll
-    for (int r = 1; r < 4; r++) step(rk[r], re[r], rw[r]);
-}
-
-#define COLI_SEL_BATCH 4   // experts per lane whose chunk partials are loaded together (JM >= 4)
-#define COLI_SEL_MAXCH 16  // chunk partials held in registers (more are added from memory)
 template <int JM>
 __global__ __launch_bounds__(256) void coli_router_select(const float *__restrict__ part, int nch,
                                                           const float *__restrict__ bias, int S, int E, int K,
@@ -254,188 +101,9 @@ __global__ __launch_bounds__(256) void coli_router_select(const float *__restric
                                                           float routed_scale, int *__restrict__ idx,
                                                           float *__restrict__ wout, int *__restrict__ keff) {
     extern __shared__ float sh[];
-    // readfirstlane: the wave index is wave-uniform, so everything derived from it
-    // (tile indices, validity, base pointers) stays in scalar registers.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int s = blockIdx.x * 4 + wave;
-    float *p = sh + (size_t)wave * E;                 // [E] weight source (fallback slots read it)
-    const bool live = s < S;
-    const size_t chstride = (size_t)S * E;
-    const float *z0 = part + (size_t)(live ? s : 0) * E;
-    // Lane l owns experts e = l + 64 j (E <= 1024: j < 16). Their chunk
-    // partials (and bias) are all requested before the first add: every load
-    // is unconditional (indices clamped into range, the extra values masked
-    // in the sum), so none waits for another. Logits are summed in chunk order.
-    constexpr int CB = COLI_SEL_BATCH < JM ? COLI_SEL_BATCH : JM, CH = COLI_SEL_MAXCH;
-    const int nmine = (E - lane + 63) / 64;   // this lane's experts
-    const int jmax = (E + 63) / 64;           // wave-uniform bound
-    float lg[JM] = {}, bs[JM] = {};
-#pragma unroll
-    for (int j0 = 0; j0 < JM; j0 += CB) {
-        if (j0 >= jmax) continue;
-        float t[CB][CH];
-        int ee[CB];
-#pragma unroll
-        for (int jj = 0; jj < CB; jj++) {
-            ee[jj] = min(lane + 64 * (j0 + jj), E - 1);
-#pragma unroll
-            for (int ch = 0; ch < CH; ch++) t[jj][ch] = z0[(size_t)min(ch, nch - 1) * chstride + ee[jj]];
-            bs[j0 + jj] = bias ? bias[ee[jj]] : 0.0f;
-        }
-#pragma unroll
-        for (int jj = 0; jj < CB; jj++) {
-            float v = t[jj][0];
-#pragma unroll
-            for (int ch = 1; ch < CH; ch++) v += ch < nch ? t[jj][ch] : 0.0f;
-            for (int ch = CH; ch < nch; ch++) v += z0[(size_t)ch * chstride + ee[jj]];
-            lg[j0 + jj] = v;
-        }
-    }
-    // weight source pv (also in LDS, for the fallback slots) and selection score cv
-    float cv[JM], pv[JM];
-    if (mode == 0) {
-        float m = -1e30f;
-#pragma unroll
-        for (int j = 0; j < JM; j++)
-            if (j < nmine) m = fmaxf(m, lg[j]);
-        m = wave_max(m);
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < JM; j++) {
-            lg[j] = j < nmine ? expf(lg[j] - m) : 0.0f;
-            sum += lg[j];
-        }
-        sum = wave_sum(sum);
-#pragma unroll
-        for (int j = 0; j < JM; j++) {
-            const float v = lg[j] / sum;
-            if (j < nmine) p[lane + 64 * j] = v;
-            cv[j] = v;
-            pv[j] = v;
-        }
-    } else if (mode == 3) {
-        // DeepSeek-V4: sqrt of the stable softplus (c/deepseek_v4.c:1368-1392)
-#pragma unroll
-        for (int j = 0; j < JM; j++) {
-            const float z = lg[j];
-            const float v = sqrtf(fmaxf(z, 0.0f) + log1pf(expf(-fabsf(z))));
-            if (j < nmine) p[lane + 64 * j] = v;
-            cv[j] = v + bs[j];
-            pv[j] = v;
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < JM; j++) {
-            const float v = 1.0f / (1.0f + expf(-lg[j]));
-            if (j < nmine) p[lane + 64 * j] = v;
-            cv[j] = v + bs[j];
-            pv[j] = v;
-        }
-    }
-    if (!live) return;
-    // Order-preserving keys: a valid score maps to a key > 0, an invalid one
-    // (NaN, or <= -1e30) to 0; +0 and -0 share a key, as they compare equal.
-    int nvalid = 0;
-    unsigned key[JM];
-#pragma unroll
-    for (int j = 0; j < JM; j++) {
-        unsigned k = 0;
-        if (j < nmine) {
-            float v = cv[j];
-            if (valid_score(v)) {
-                if (v == 0.0f) v = 0.0f;
-                const unsigned b = __float_as_uint(v);
-                k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-            }
-        }
-        key[j] = k;
-        nvalid += k != 0;
-    }
-    nvalid = wave_sum_i(nvalid);
-    const int want = nvalid < K ? nvalid : K;
-    // K rounds of a wave-wide argmax (largest key, then lowest expert index):
-    // round kk yields the expert of rank kk (and its weight source), which its
-    // owner lane then retires; lane kk keeps slot kk.
-    int my_e = 0;
-    float my_w = 0.0f;
-    for (int kk = 0; kk < want; kk++) {
-        unsigned bk = 0;
-        int be = 0x7fffffff;
-        float bw = 0.0f;
-#pragma unroll
-        for (int j = 0; j < JM; j++)
-            if (key[j] > bk) {   // strict: the lower index (smaller j) wins a tie
-                bk = key[j];
-                be = lane + 64 * j;
-                bw = pv[j];
-            }
-        wave_argmax(bk, be, bw);
-#pragma unroll
-        for (int j = 0; j < JM; j++)
-            if (lane + 64 * j == be) key[j] = 0;
-        if (lane == kk) {
-            my_e = be;
-            my_w = bw;
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // p[] written by all lanes
-    const bool act = lane < K;
-    if (act && lane >= want) {   // fewer valid scores than K: experts 0, 1, ... fill the rest
-        my_e = lane < E ? lane : 0;
-        my_w = p[my_e];
-    }
-    if (!act) my_w = 0.0f;
-    auto wsum = [](float v) { return wave_sum(v); };
-    // rank of this slot when sorted by weight, descending and stable (ties
-    // keep slot order), and the inclusive cumulative weight in that order
-    auto sort_rank = [&](int &rank, float &cum) {
-        rank = 0;
-        cum = 0.0f;
-        for (int j = 0; j < K; j++) {
-            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
-            const bool before = wj > my_w || (wj == my_w && j < lane);
-            rank += before ? 1 : 0;
-            cum += (before || j == lane) ? wj : 0.0f;
-        }
-    };
-    int slot = lane, ke = K;
-    const bool cut = topp > 0.0f && topp < 1.0f;
-    if (mode == 0) {
-        if (norm_topk) my_w /= wsum(my_w);
-    } else if (mode == 1) {
-        if (cut) {
-            float cum;
-            sort_rank(slot, cum);
-            const float tot = 1e-20f + wsum(my_w);
-            const int first = wave_min_i(act && cum >= topp * tot ? slot : K - 1);
-            ke = first + 1;
-        }
-        if (norm_topk) my_w /= wsum(act && slot < ke ? my_w : 0.0f) + 1e-20f;
-        if (slot < ke) my_w *= routed_scale;
-    } else if (mode == 3) {
-        // score / sum of the selected scores * route scale; a non-positive sum
-        // (an error in coli_v4_route) selects nothing
-        const float total = wsum(my_w);
-        if (!(total > 0.0f)) ke = 0;
-        else my_w = my_w / total * routed_scale;
-    } else {
-        my_w /= wsum(my_w) + 1e-20f;
-        if (cut) {
-            float cum;
-            sort_rank(slot, cum);
-            const int keep = wave_min_i(act && cum >= topp ? slot + 1 : K);
-            if (keep < K) {
-                my_w /= wsum(act && slot < keep ? my_w : 0.0f) + 1e-20f;
-                ke = keep;
-            }
-        }
-        if (routed_scale != 1.0f && slot < ke) my_w *= routed_scale;
-    }
-    if (act) {
-        idx[(size_t)s * K + slot] = my_e;
-        wout[(size_t)s * K + slot] = slot < ke ? my_w : 0.0f;
-    }
-    if (lane == 0) keff[s] = ke;
+    select_row<JM, false>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wout, keff,
+                          sh + (size_t)wave * E, blockIdx.x * 4 + wave, lane, nullptr, nullptr);
 }
 
 extern "C" hipError_t coli_launch_router_select(const float *part, int nch, const float *bias, int S, int E,

@@ -331,3 +331,39 @@ def test_moe_layer_deepseek_v4(session, fmt, S, shared, limit):
     assert np.array_equal(idx, ri), "router top-K indices must be bit-exact"
     assert np.allclose(w, rw, rtol=1e-5, atol=1e-7)
     assert rel_err(out, ref, mag).max() <= TOL
+
+
+# Decode routing in one launch (router partials, selection and union; the
+# last workgroup to arrive selects) against the three separate launches:
+# bitwise equal outputs, slots and weights, over several calls in a row (the
+# arrival counter resets itself) and several column chunks.
+@pytest.mark.parametrize("mode,S,E", [(0, 1, 64), (1, 4, 32), (2, 7, 256), (3, 16, 128), (2, 16, 256)])
+def test_moe_fused_routing_bitwise(session, monkeypatch, mode, S, E):
+    rng = np.random.default_rng(500 + mode * 7 + S + E)
+    D, I, K = 1536, 256, 8 if E >= 64 else 4
+    layer = Layer(rng, 4, D, I, E, shared=mode == 2)
+    runs = {}
+    for fused in ("1", "0"):
+        monkeypatch.setenv("COLI_HIP_FUSED_ROUTE", fused)
+        m, hs = make_moe(session, layer, *make_router_inputs(np.random.default_rng(7), S, D, E, K, mode,
+                                                             bias=(mode != 0))[1:], K, mode,
+                         norm_topk=1 if mode == 1 else 0, routed_scale=2.5 if mode == 1 else 1.0)
+        got = []
+        try:
+            for call in range(3):
+                x = np.random.default_rng(call).standard_normal((S, D)).astype(np.float32)
+                out = np.zeros((S, D), np.float32)
+                idx = np.zeros((S, K), np.int32)
+                w = np.zeros((S, K), np.float32)
+                keff = np.zeros(S, np.int32)
+                assert session.b.hip_moe_forward(m, f32p(x), f32p(out), S, i32p(idx), f32p(w), i32p(keff))
+                got.append((out, idx, w, keff))
+        finally:
+            session.b.hip_moe_free(m)
+            for h in hs:
+                for t in h:
+                    session.free(t)
+        runs[fused] = got
+    for a, b in zip(runs["1"], runs["0"]):
+        for u, v in zip(a, b):
+            assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
