@@ -49,13 +49,18 @@ def make_router_inputs(rng, S, D, E, K, mode, gap=1e-4, bias=False, zipf=None):
 
 
 class Layer:
-    """Expert weights of one synthetic MoE layer in source layout."""
+    """Expert weights of one synthetic MoE layer in source layout.
+    distinct: number of distinct weight sets, expert e using set e % distinct
+    (full-size layers without full-size host and device memory)."""
 
-    def __init__(self, rng, fmt, D, I, E, shared=False, swiglu_limit=0.0):
+    def __init__(self, rng, fmt, D, I, E, shared=False, swiglu_limit=0.0, distinct=None):
         self.fmt, self.D, self.I, self.E = fmt, D, I, E
         self.swiglu_limit = swiglu_limit   # > 0: DeepSeek-V4 clamped SwiGLU
-        self.experts = [self._expert(rng) for _ in range(E)]
+        n = E if distinct is None else min(E, distinct)
+        sets = [self._expert(rng) for _ in range(n)]
+        self.experts = [sets[e % n] for e in range(E)]
         self.shared = self._expert(rng) if shared else None
+        self._deq = {}
 
     def _expert(self, rng):
         D, I = self.D, self.I
@@ -76,8 +81,11 @@ class Layer:
         return cref.matmul_mxfp4(x, q, s, O, I)
 
     def deq(self, mat, I):
-        q, s = mat
-        return deq_i4(q, s, I, 32) if self.fmt == 4 else deq_mxfp4(q, s, I)
+        key = id(mat[0])
+        if key not in self._deq:
+            q, s = mat
+            self._deq[key] = np.abs(deq_i4(q, s, I, 32) if self.fmt == 4 else deq_mxfp4(q, s, I)).T.copy()
+        return self._deq[key]
 
     def expert_forward(self, e, x):
         g, u, d = self.experts[e] if e >= 0 else self.shared
@@ -87,10 +95,16 @@ class Layer:
         return h, self.gemv(d, h, self.D, self.I)
 
     def upload(self, session):
-        hs = []
-        for (g, u, d) in self.experts + ([self.shared] if self.shared else []):
-            hs.append(tuple(self._up(session, m, O, I) for m, O, I in
-                            ((g, self.I, self.D), (u, self.I, self.D), (d, self.D, self.I))))
+        """Device handles per expert (+ shared); experts sharing a weight set
+        share its handles (free them with free_handles)."""
+        hs, done = [], {}
+        for trip in self.experts + ([self.shared] if self.shared else []):
+            key = id(trip)
+            if key not in done:
+                g, u, d = trip
+                done[key] = tuple(self._up(session, m, O, I) for m, O, I in
+                                  ((g, self.I, self.D), (u, self.I, self.D), (d, self.D, self.I)))
+            hs.append(done[key])
         return hs
 
     def _up(self, session, m, O, I):
@@ -118,5 +132,15 @@ def moe_reference(layer, x, W, b, K, mode, norm_topk=0, topp=0.0, routed_scale=1
             h, y = layer.expert_forward(e, xs)
             dm = layer.experts[e][2] if e >= 0 else layer.shared[2]
             out[s] += wk * y[0].astype(np.float64)
-            mag[s] += abs(wk) * (np.abs(h[0].astype(np.float64)) @ np.abs(layer.deq(dm, layer.I)).T)
+            mag[s] += abs(wk) * (np.abs(h[0].astype(np.float64)) @ layer.deq(dm, layer.I))
     return idx, w, keff, out, mag
+
+
+def free_handles(session, hs):
+    """Free every distinct device handle of Layer.upload once."""
+    seen = set()
+    for trip in hs:
+        for t in trip:
+            if t is not None and id(t) not in seen:
+                seen.add(id(t))
+                session.free(t)

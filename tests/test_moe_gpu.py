@@ -28,7 +28,7 @@ def group_mag(layer, x, members, rows):
     for e, r in zip(members, rows):
         for s in range(r):
             h, _ = layer.expert_forward(e, x[off + s:off + s + 1])
-            mags.append(np.abs(h[0]).astype(np.float64) @ np.abs(layer.deq(layer.experts[e][2], layer.I)).T)
+            mags.append(np.abs(h[0]).astype(np.float64) @ layer.deq(layer.experts[e][2], layer.I))
         off += r
     return np.stack(mags)
 
@@ -120,7 +120,7 @@ def test_resident_issue_take(session):
     for e in range(4):
         h, y = layer.expert_forward(e, x)
         ref += w[e] * y[0]
-        mag += w[e] * (np.abs(h[0]).astype(np.float64) @ np.abs(layer.deq(layer.experts[e][2], I)).T)
+        mag += w[e] * (np.abs(h[0]).astype(np.float64) @ layer.deq(layer.experts[e][2], I))
     assert rel_err(out, ref, mag).max() <= TOL
 
 
