@@ -104,13 +104,20 @@ static bool plan_dma(const DevCtx *ctx, GemvLaunchPlan &p, int kind, int nprob, 
     int RT = 1;
     if (tiles >= 2 * cus) RT = 2;
     if (!dual && tiles >= 2 * cus && max_rows > 8) RT = 4;
-    if (dual) RT = std::min(RT, 2);
+    // dual (gate + up): one row-tile pair per wave (measured: DSV3 B1 layer
+    // 77.2 -> 71.5 us, OLMoE 32.4 -> 31.5 us against two pairs)
+    if (dual) RT = 1;
+    int W = 8;
+    // tuning overrides: row tiles per wave, waves per group (dual only)
+    if (const char *e = std::getenv("COLI_HIP_DMA_RT")) RT = std::max(1, std::min(dual ? 2 : 4, std::atoi(e)));
+    if (const char *e = std::getenv("COLI_HIP_DMA_W"))
+        if (dual && max_rows <= 1) W = std::atoi(e) == 4 ? 4 : 8;
     for (; RT >= 1; RT /= 2) {
         const int R = dual ? 2 * RT : RT;
         for (int PD = (R == 1 ? 3 : 2); PD >= 2; PD--) {
-            if (8L * PD * dma_slot_bytes(kind, R, max_rows) <= 160 * 1024) {
+            if ((long)W * PD * dma_slot_bytes(kind, R, max_rows) <= 160 * 1024) {
                 p.R = R;
-                p.W = 8;
+                p.W = W;
                 p.PD = PD;
                 p.dma = 1;
                 p.rbpp = (nrt + RT - 1) / RT;

@@ -482,6 +482,9 @@ static hipError_t launch_dma5(const ColiGemvArgs &a, int W, int blocks, hipStrea
     if constexpr (R == 1 && !DUAL) {
         if (W == 16) return launch_dma6<KIND, R, DUAL, NB4, PD, NXR, F32, 16>(a, blocks, st);
     }
+    if constexpr (DUAL && NXR == 1) {
+        if (W == 4) return launch_dma6<KIND, R, DUAL, NB4, PD, NXR, F32, 4>(a, blocks, st);
+    }
     return launch_dma6<KIND, R, DUAL, NB4, PD, NXR, F32, 8>(a, blocks, st);
 }
 
@@ -524,7 +527,7 @@ static hipError_t launch_dma1(const ColiGemvArgs &a, int R, bool dual, int W, in
 // hold (the caller then uses coli_gemv_tiles).
 extern "C" hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual, int W, int PD, int max_rows,
                                            hipStream_t st) {
-    if (a->splits != 1 || max_rows < 1 || max_rows > 16 || (W != 8 && W != 16)) return hipErrorInvalidValue;
+    if (a->splits != 1 || max_rows < 1 || max_rows > 16 || (W != 4 && W != 8 && W != 16)) return hipErrorInvalidValue;
     // f32 activations: up to four rows, rows of whole quads, 16-byte aligned
     if (a->xf && (max_rows > 4 || a->ldx < a->nq * 128 || a->ldx % 4 || (uintptr_t)a->xf % 16))
         return hipErrorInvalidValue;
