@@ -177,17 +177,18 @@ __device__ __forceinline__ void wave_argmax(unsigned &k, int &e, float &w) {
 #define COLI_SEL_BATCH 4   // experts per lane whose chunk partials are loaded together (JM >= 4)
 #define COLI_SEL_MAXCH 16  // chunk partials held in registers (more are added from memory)
 // Selection of token row s by one wave; p: [E] floats of LDS for this wave.
-// ATOMIC: the partials are read as agent-scope atomics (written inside the
-// same launch by other workgroups). sidx / skeff (optional): copies of the
+// ATOMIC: idx / wout / keff are written as agent-scope atomics (read back by
+// another workgroup of the same launch); LD_ATOMIC: the partials are read as
+// agent-scope atomics (written by other workgroups of the same launch). sidx / skeff (optional): copies of the
 // row's slots and keff for a reader in the same workgroup.
-template <int JM, bool ATOMIC>
+template <int JM, bool ATOMIC, bool LD_ATOMIC = ATOMIC>
 __device__ __forceinline__ void select_row(const float *__restrict__ part, int nch, const float *__restrict__ bias,
                                            int S, int E, int K, int mode, float topp, int norm_topk,
                                            float routed_scale, int *__restrict__ idx, float *__restrict__ wout,
                                            int *__restrict__ keff, float *p, int s, int lane, int *sidx,
                                            int *skeff) {
     auto ld = [](const float *q) {
-        if constexpr (ATOMIC) return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (LD_ATOMIC) return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else return *q;
     };
     const bool live = s < S;
@@ -363,12 +364,19 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
         if (routed_scale != 1.0f && slot < ke) my_w *= routed_scale;
     }
     if (act) {
-        idx[(size_t)s * K + slot] = my_e;
-        wout[(size_t)s * K + slot] = slot < ke ? my_w : 0.0f;
+        if constexpr (ATOMIC) {   // read back by another workgroup of the same launch
+            __hip_atomic_store(idx + (size_t)s * K + slot, my_e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(wout + (size_t)s * K + slot, slot < ke ? my_w : 0.0f, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            idx[(size_t)s * K + slot] = my_e;
+            wout[(size_t)s * K + slot] = slot < ke ? my_w : 0.0f;
+        }
         if (sidx) sidx[s * K + slot] = my_e;
     }
     if (lane == 0) {
-        keff[s] = ke;
+        if constexpr (ATOMIC) __hip_atomic_store(keff + s, ke, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else keff[s] = ke;
         if (skeff) skeff[s] = ke;
     }
 }

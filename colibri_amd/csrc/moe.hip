@@ -163,6 +163,48 @@ __global__ __launch_bounds__(1024) void coli_moe_union(const int *__restrict__ i
 }
 
 // ---------------------------------------------------------------------------
+// Selection and union in one launch (partials from coli_router_partial): one
+// wave per row; each workgroup publishes its rows' slots as agent-scope
+// atomics, waits for its stores and counts its arrival; the last one to
+// arrive reads every row's slots back and builds the union. Same arithmetic
+// and results as coli_router_select followed by coli_moe_union.
+// ---------------------------------------------------------------------------
+template <int JM>
+__global__ __launch_bounds__(256) void coli_moe_select_union(const float *__restrict__ part, int nch,
+                                                             const float *__restrict__ bias, int S, int E, int K,
+                                                             int mode, float topp, int norm_topk, float routed_scale,
+                                                             int *__restrict__ idx, float *__restrict__ wsel,
+                                                             int *__restrict__ keff, int *__restrict__ counter,
+                                                             int has_shared, const ColiProb *__restrict__ tab,
+                                                             ColiProb *__restrict__ pdual, ColiProb *__restrict__ pdown,
+                                                             int *__restrict__ uniq, int *__restrict__ xrows,
+                                                             int *__restrict__ slotrow, int *__restrict__ mt,
+                                                             int *__restrict__ state) {
+    extern __shared__ int sm[];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // LDS: slots [S K] | keff [S] | selection weights [4 E] floats, then the union's (7 E + 5) ints
+    int *sidx = sm, *skeff = sm + S * K, *work = skeff + S;
+    select_row<JM, true, false>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
+                                (float *)work + (size_t)wave * E, blockIdx.x * 4 + wave, lane, nullptr, nullptr);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == (int)gridDim.x - 1;
+        if (s_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int i = threadIdx.x; i < S * K; i += blockDim.x)
+        sidx[i] = __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int t = threadIdx.x; t < S; t += blockDim.x)
+        skeff[t] = __hip_atomic_load(keff + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    moe_union_body(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, work);
+}
+
+// ---------------------------------------------------------------------------
 // Decode routing in one launch (S <= 16, up to 128 workgroups): router partial logits, top-K
 // selection and union. Every workgroup computes the partials of 4 experts x
 // one 512-column chunk and publishes them as agent-scope atomics (coherent
@@ -353,6 +395,27 @@ static int launch_route(ColiHipMoe *m, const float *x_dev, int S, hipStream_t st
     return hip_ok(hipGetLastError(), "moe routing");
 }
 
+static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
+    const ColiHipMoeConfig &c = m->cfg;
+    const size_t work = std::max((size_t)4 * c.E * sizeof(float), (size_t)(7 * c.E + 5) * sizeof(int));
+    const size_t shm = (size_t)(S * c.K + S) * sizeof(int) + work;
+    const int jm = c.E <= 64 ? 1 : c.E <= 128 ? 2 : c.E <= 256 ? 4 : c.E <= 512 ? 8 : 16;
+    const dim3 grid((unsigned)((S + 3) / 4)), block(256);
+#define COLI_SU(JM)                                                                                             \
+    hipLaunchKernelGGL((coli_moe_select_union<JM>), grid, block, shm, st, m->logits, nch, m->rb, S, c.E, c.K,     \
+                       c.route_mode, c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, m->route_cnt, \
+                       c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state)
+    switch (jm) {
+    case 1: COLI_SU(1); break;
+    case 2: COLI_SU(2); break;
+    case 4: COLI_SU(4); break;
+    case 8: COLI_SU(8); break;
+    default: COLI_SU(16); break;
+    }
+#undef COLI_SU
+    return hip_ok(hipGetLastError(), "moe selection + union");
+}
+
 extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float *out_dev, int S) {
     if (fault_injected()) return 0;
     if (!m || !x_dev || !out_dev || S < 1 || S > COLI_MOE_MAX_ROWS || S * m->cfg.K > COLI_MOE_MAX_SEL) return 0;
@@ -374,6 +437,10 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     if (S <= 16 && (long)((c.E + 3) / 4) * coli_router_chunks(c.D) <= 128 && !fused_route_disabled()) {
         // 2-4. router, selection and union in one launch
         if (!launch_route(m, x_dev, S, st)) return 0;
+    } else if (S <= 64 && !fused_route_disabled()) {
+        // 2. router partials, 3-4. selection and union in one launch
+        const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
+        if (!nch || !launch_select_union(m, nch, S, st)) return 0;
     } else {
         const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
         if (!nch || !hip_ok(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
