@@ -78,6 +78,7 @@ __device__ __forceinline__ void moe_union_body(const int *idx, const int *keff, 
         first[e] = 0x7fffffff;
         cnt[e] = 0;
         cur[e] = 0;
+        rank[e] = -1;
     }
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
@@ -88,40 +89,91 @@ __device__ __forceinline__ void moe_union_body(const int *idx, const int *keff, 
         }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        int r = -1;
-        if (cnt[e] > 0) {
-            const int fe = first[e];
-            r = 0;
-            for (int f = 0; f < E; f++) r += first[f] < fe;   // first[] of unused experts is INT_MAX
-            order[r] = e;
+    // Ranks straight from the selection positions, in chunks of one position
+    // per thread: position i is its expert's first when first[e] == i, and
+    // the expert's rank is the number of such positions before i (a ballot
+    // per wave and a prefix over the waves' counts; no scan over E).
+    {
+        __shared__ int s_wc[32];
+        const int w = threadIdx.x >> 6, ln = threadIdx.x & 63, nw = (blockDim.x + 63) >> 6;
+        int base = 0;
+        for (int c0 = 0; c0 < n; c0 += blockDim.x) {
+            const int i = c0 + threadIdx.x;
+            int e = -1;
+            bool f = false;
+            if (i < n) {
+                const int t = i / K, kk = i - t * K;
+                e = idx[i];
+                f = kk < keff[t] && e >= 0 && e < E && first[e] == i;
+            }
+            const unsigned long long m = __builtin_amdgcn_ballot_w64(f);
+            if (ln == 0) s_wc[w] = __popcll(m);
+            __syncthreads();
+            int pre = base, tot = 0;
+            for (int v = 0; v < nw; v++) {
+                pre += v < w ? s_wc[v] : 0;
+                tot += s_wc[v];
+            }
+            if (f) {
+                const int r = pre + __popcll(m & ((1ull << ln) - 1ull));
+                rank[e] = r;
+                order[r] = e;
+            }
+            base += tot;
+            __syncthreads();   // s_wc is rewritten by the next chunk
         }
-        rank[e] = r;
-    }
-    if (threadIdx.x < 64) {
-        int c = 0;
-        for (int e = threadIdx.x; e < E; e += 64) c += cnt[e] > 0;
-#pragma unroll
-        for (int o = 32; o; o >>= 1) c += __shfl_xor(c, o);
-        if (threadIdx.x == 0) s_nu = c;
+        if (threadIdx.x == 0) s_nu = base;
     }
     __syncthreads();
     const int nu = s_nu, np = nu + (has_shared ? 1 : 0);
     if (has_shared && threadIdx.x == 0) order[nu] = E;
     __syncthreads();
-    // packed offsets and GEMM tile offsets in union order (each slot sums the
-    // earlier counts itself: no serial scan)
-    for (int j = threadIdx.x; j <= np; j += blockDim.x) {
-        int o = 0, to = 0;
-        for (int q = 0; q < j; q++) {
-            const int c = order[q] == E ? S : cnt[order[q]];
-            o += c;
-            to += (c + COLI_GM_ROWS - 1) / COLI_GM_ROWS;
+    // packed offsets and GEMM tile offsets in union order: exclusive prefix
+    // sums over the problems, a wave scan per chunk of one problem per thread
+    // plus a prefix over the waves' totals
+    {
+        __shared__ int s_ws[32], s_wt[32];
+        const int w = threadIdx.x >> 6, ln = threadIdx.x & 63, nw = (blockDim.x + 63) >> 6;
+        int base_o = 0, base_t = 0;
+        for (int c0 = 0; c0 <= np; c0 += blockDim.x) {
+            const int j = c0 + threadIdx.x;
+            int c = 0, tl = 0;
+            if (j < np) {
+                c = order[j] == E ? S : cnt[order[j]];
+                tl = (c + COLI_GM_ROWS - 1) / COLI_GM_ROWS;
+            }
+            int xc = c, xt = tl;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int yc = __shfl_up(xc, o), yt = __shfl_up(xt, o);
+                if (ln >= o) {
+                    xc += yc;
+                    xt += yt;
+                }
+            }
+            if (ln == 63) {
+                s_ws[w] = xc;
+                s_wt[w] = xt;
+            }
+            __syncthreads();
+            int pc = base_o, pt = base_t, tc = 0, tt = 0;
+            for (int v = 0; v < nw; v++) {
+                if (v < w) {
+                    pc += s_ws[v];
+                    pt += s_wt[v];
+                }
+                tc += s_ws[v];
+                tt += s_wt[v];
+            }
+            if (j <= np) {
+                off[j] = pc + xc - c;
+                toff[j] = pt + xt - tl;
+            }
+            base_o += tc;
+            base_t += tt;
+            __syncthreads();   // s_ws / s_wt are rewritten by the next chunk
         }
-        off[j] = o;
-        toff[j] = to;
     }
-    __syncthreads();
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int t = i / K, kk = i - t * K, e = idx[i];
         if (kk < keff[t] && e >= 0 && e < E) {
@@ -186,7 +238,7 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
     // LDS: slots [S K] | keff [S] | selection weights [4 E] floats, then the union's (7 E + 5) ints
     int *sidx = sm, *skeff = sm + S * K, *work = skeff + S;
     select_row<JM, true, false>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
-                                (float *)work + (size_t)wave * E, blockIdx.x * 4 + wave, lane, nullptr, nullptr);
+                                (float *)work + (size_t)wave * E, blockIdx.x * 4 + wave, lane, sidx, skeff);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -196,10 +248,12 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
     }
     __syncthreads();
     if (!s_last) return;
+    // the other workgroups' rows (this one's are in LDS already)
+    const int own0 = blockIdx.x * 4, own1 = min(S, own0 + 4);
     for (int i = threadIdx.x; i < S * K; i += blockDim.x)
-        sidx[i] = __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (i / K < own0 || i / K >= own1) sidx[i] = __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int t = threadIdx.x; t < S; t += blockDim.x)
-        skeff[t] = __hip_atomic_load(keff + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t < own0 || t >= own1) skeff[t] = __hip_atomic_load(keff + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     moe_union_body(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, work);
 }
