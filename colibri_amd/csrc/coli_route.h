@@ -7,6 +7,8 @@
 
 #include <math.h>
 
+#include "coli_device.h"
+
 // ---------------------------------------------------------------------------
 // Router logits: logits[s, e] = sum_d x[s, d] * W[e, d], f32 (the router GEMV
 // of c/colibri.c:3978 / c/olmoe.c:648), in two fixed-order halves so the
@@ -176,6 +178,57 @@ __device__ __forceinline__ void wave_argmax(unsigned &k, int &e, float &w) {
 
 #define COLI_SEL_BATCH 4   // experts per lane whose chunk partials are loaded together (JM >= 4)
 #define COLI_SEL_MAXCH 16  // chunk partials held in registers (more are added from memory)
+// Partial logits of four experts (one per wave) over one 512-column chunk for
+// up to SMAX rows, with the rows' chunk staged once in LDS by the workgroup
+// (every wave reading them from L2 cost four times the traffic). The router
+// weights are requested before the staging. D % 4 == 0. All 256 threads of
+// the workgroup call it (it synchronizes).
+template <int SMAX, bool ATOMIC>
+__device__ __forceinline__ void router_partial_block(const float *__restrict__ x, int S, const float *__restrict__ W,
+                                                     int D, int E, float *__restrict__ part, size_t chstride,
+                                                     int e, int ch, int lane, floatx4 (*xs)[COLI_ROUTER_CHUNK / 4]) {
+    constexpr int NV = COLI_ROUTER_CHUNK / 4;   // float4 per row chunk
+    const int d0 = ch * COLI_ROUTER_CHUNK;
+    floatx4 wv[COLI_ROUTER_CHUNK / 256];
+#pragma unroll
+    for (int step = 0; step < COLI_ROUTER_CHUNK / 256; step++) {
+        const int d = d0 + step * 256 + lane * 4;
+        wv[step] = (e < E && d < D) ? *(const floatx4 *)(W + (size_t)e * D + d) : (floatx4){0.f, 0.f, 0.f, 0.f};
+    }
+    for (int v = threadIdx.x; v < SMAX * NV; v += blockDim.x) {
+        const int s = v / NV, c = v - s * NV, d = d0 + c * 4;
+        xs[s][c] = (s < S && d < D) ? *(const floatx4 *)(x + (size_t)s * D + d) : (floatx4){0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();
+    if (e >= E) return;
+    float acc[SMAX];
+#pragma unroll
+    for (int s = 0; s < SMAX; s++) acc[s] = 0.0f;
+#pragma unroll
+    for (int step = 0; step < COLI_ROUTER_CHUNK / 256; step++) {
+#pragma unroll
+        for (int s = 0; s < SMAX; s++) {
+            const floatx4 xv = xs[s][step * 64 + lane];
+            float a = xv[0] * wv[step][0];
+            a = fmaf(xv[1], wv[step][1], a);
+            a = fmaf(xv[2], wv[step][2], a);
+            acc[s] += fmaf(xv[3], wv[step][3], a);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < SMAX; s++) {
+        if (s >= S) break;
+        float v = acc[s];
+#pragma unroll
+        for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0) {
+            float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
+            if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else *dst = v;
+        }
+    }
+}
+
 // Selection of token row s by one wave; p: [E] floats of LDS for this wave.
 // ATOMIC: idx / wout / keff are written as agent-scope atomics (read back by
 // another workgroup of the same launch); LD_ATOMIC: the partials are read as

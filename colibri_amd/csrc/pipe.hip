@@ -69,6 +69,14 @@ __global__ __launch_bounds__(256) void coli_router_partial(const float *__restri
     // readfirstlane: the wave index is wave-uniform, so everything derived from it
     // (tile indices, validity, base pointers) stays in scalar registers.
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if constexpr (SMAX > 1) {
+        if ((D & 3) == 0) {
+            __shared__ floatx4 xs[SMAX][COLI_ROUTER_CHUNK / 4];
+            router_partial_block<SMAX, false>(x, S, W, D, E, part, chstride, blockIdx.x * 4 + wave, blockIdx.y, lane,
+                                              xs);
+            return;
+        }
+    }
     router_partial_wave<SMAX, false>(x, S, W, D, E, part, chstride, blockIdx.x * 4 + wave, blockIdx.y, lane);
 }
 
