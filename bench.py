@@ -389,6 +389,40 @@ def measured_traffic():
         return None
 
 
+def moe_layers(bench):
+    """The MoE-layer measurements of configs[0], [2], [3] and [4]."""
+    res = {
+        "configs[0]_olmoe_int4": bench.moe("olmoe", 4, 2048, 1024, 64, 8, 0, False, (1,), 10, False),
+        "configs[2]_dsv3_mxfp4": bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 16), 1, True),
+    }
+    # configs[3]: one verification step of 21 rows (16-node tree + 5-token
+    # draft) on the configs[2] layer shape, union GEMM vs 21 per-token passes
+    ver = {}
+    for fmt, tag in ((7, "mxfp4"), (4, "int4")):
+        r = bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True, steps=20)
+        r.update({k + "": v for k, v in bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True,
+                                                      steps=5, per_token=True).items() if k.startswith("B")})
+        ver[tag] = r
+    res["configs[3]_verification_21rows"] = ver
+    # configs[4]: Kimi-shaped prefill chunk, 512 tokens, 384 experts top-8,
+    # router logits ~N(0,1) with a Zipf(1.1) selection bias
+    res["configs[4]_kimi_prefill_512"] = {
+        tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+                       w_std=1.0 / math.sqrt(7168))
+        for fmt, tag in ((7, "mxfp4"), (4, "int4"))}
+    # the opt-in MXFP4 GEMM on the block-scaled MFMA (COLI_HIP_MX=1; not
+    # fp32-exact: the hardware's per-block summation error is ~2^-15 of the
+    # block's magnitude sum)
+    os.environ["COLI_HIP_MX"] = "1"
+    try:
+        res["configs[4]_kimi_prefill_512"]["mxfp4_block_scaled_mfma_optin"] = bench.moe(
+            "kimi", 7, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+            w_std=1.0 / math.sqrt(7168))
+    finally:
+        del os.environ["COLI_HIP_MX"]
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -398,6 +432,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-moe", action="store_true")
+    ap.add_argument("--skip-dense", action="store_true",
+                    help="run only the MoE-layer measurements (profiling aid; prints the moe_layer object)")
     ap.add_argument("--moe-steps", type=int, default=50)
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy 256 MiB device-to-device 4 times (the known-size reference that scales "
@@ -418,6 +454,10 @@ def main():
         bench.close()
         print(json.dumps({"copy_calib_bytes": nb, "copies": 4}))
         return
+    if args.skip_dense:
+        print(json.dumps({"moe_layer": moe_layers(bench)}))
+        bench.close()
+        return
     bench.dense()
     r = bench.dense_result
     out = {
@@ -436,35 +476,7 @@ def main():
         "gemv_by_batch": r["by_batch"],
     }
     if not args.skip_moe:
-        out["moe_layer"] = {
-            "configs[0]_olmoe_int4": bench.moe("olmoe", 4, 2048, 1024, 64, 8, 0, False, (1,), 10, False),
-            "configs[2]_dsv3_mxfp4": bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 16), 1, True),
-        }
-        # one verification step of 21 rows (16-node tree + 5-token
-        # draft) on the configs[2] layer shape, union GEMM vs 21 per-token passes
-        ver = {}
-        for fmt, tag in ((7, "mxfp4"), (4, "int4")):
-            r = bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True, steps=20)
-            r.update({k + "": v for k, v in bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True,
-                                                          steps=5, per_token=True).items() if k.startswith("B")})
-            ver[tag] = r
-        out["moe_layer"]["configs[3]_verification_21rows"] = ver
-        # Kimi-shaped prefill chunk, 512 tokens, 384 experts top-8,
-        # router logits ~N(0,1) with a Zipf(1.1) selection bias
-        out["moe_layer"]["configs[4]_kimi_prefill_512"] = {
-            tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
-                           w_std=1.0 / math.sqrt(7168))
-            for fmt, tag in ((7, "mxfp4"), (4, "int4"))}
-        # the opt-in MXFP4 GEMM on the block-scaled MFMA (COLI_HIP_MX=1; not
-        # fp32-exact: the hardware's per-block summation error is ~2^-15 of the
-        # block's magnitude sum)
-        os.environ["COLI_HIP_MX"] = "1"
-        try:
-            out["moe_layer"]["configs[4]_kimi_prefill_512"]["mxfp4_block_scaled_mfma_optin"] = bench.moe(
-                "kimi", 7, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
-                w_std=1.0 / math.sqrt(7168))
-        finally:
-            del os.environ["COLI_HIP_MX"]
+        out["moe_layer"] = moe_layers(bench)
     if not args.skip_cpu:
         out["cpu_baseline"] = bench.cpu_baseline()
     bench.close()

@@ -871,13 +871,14 @@ extern "C" int coli_cuda_expert_group_resident_take(int home_device, const int *
 }
 
 // ---------------------------------------------------------------------------
-// Router logits. Decode batches (<= 16 rows) use the chunked partial kernel
-// (pipe.hip); larger batches are a plain f32 GEMM, logits[S, E] = x W^T,
+// Router logits. Up to 64 rows use the chunked partial kernel (pipe.hip, in
+// passes of 16 rows; rocBLAS's sgemm took 60 us for 21 rows of the DSV3
+// router); larger batches are a plain f32 GEMM, logits[S, E] = x W^T,
 // which rocBLAS runs on the backend stream (col-major: C(E x S) = W^T(E x D)
 // x^T... i.e. op(A) = A^T with A = W as a D x E col-major matrix).
 // ---------------------------------------------------------------------------
 int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int E, float *part) {
-    if (S <= 16)
+    if (S <= 64)
         return hip_ok(coli_launch_router_logits(x, S, W, D, E, part, ctx->stream), "router logits")
                    ? coli_router_chunks(D)
                    : 0;
