@@ -39,12 +39,13 @@ __device__ __forceinline__ void router_partial_wave(const float *__restrict__ x,
             const float4 wv = *(const float4 *)(wr + d);
 #pragma unroll
             for (int s = 0; s < SMAX; s++) {
-                if (s >= S) break;
-                const float4 xv = *(const float4 *)(x + (size_t)s * D + d);
-                float a = xv.x * wv.x;
-                a = fmaf(xv.y, wv.y, a);
-                a = fmaf(xv.z, wv.z, a);
-                acc[s] += fmaf(xv.w, wv.w, a);
+                if (s < S) {
+                    const float4 xv = *(const float4 *)(x + (size_t)s * D + d);
+                    float a = xv.x * wv.x;
+                    a = fmaf(xv.y, wv.y, a);
+                    a = fmaf(xv.z, wv.z, a);
+                    acc[s] += fmaf(xv.w, wv.w, a);
+                }
             }
         } else {
             for (int t = 0; t < 4 && d + t < D; t++) {
@@ -57,14 +58,15 @@ __device__ __forceinline__ void router_partial_wave(const float *__restrict__ x,
     }
 #pragma unroll
     for (int s = 0; s < SMAX; s++) {
-        if (s >= S) break;
-        float v = acc[s];
+        if (s < S) {
+            float v = acc[s];
 #pragma unroll
-        for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0) {
-            float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
-            if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else *dst = v;
+            for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) {
+                float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
+                if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else *dst = v;
+            }
         }
     }
 }
@@ -217,14 +219,15 @@ __device__ __forceinline__ void router_partial_block(const float *__restrict__ x
     }
 #pragma unroll
     for (int s = 0; s < SMAX; s++) {
-        if (s >= S) break;
-        float v = acc[s];
+        if (s < S) {
+            float v = acc[s];
 #pragma unroll
-        for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0) {
-            float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
-            if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else *dst = v;
+            for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) {
+                float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
+                if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else *dst = v;
+            }
         }
     }
 }
