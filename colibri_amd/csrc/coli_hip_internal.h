@@ -74,6 +74,7 @@ struct ColiGemvArgs {
     int lo_gen;
     const float *xf;          // non-null (coli_gemv_dma only): f32 activations, row r = xf + xrows-mapped r * ldx
     int ldx;
+    int xstage;               // with xf and one row per problem: convert the row once per group into LDS
     const _Float16 *zero;     // >= COLI_ZERO_BYTES of zeros: inactive batch lanes, dead tiles
     float *out;
     int ldo;

@@ -201,6 +201,12 @@ static bool xf32_enabled() {
     return !(e && e[0] == '0');
 }
 
+// COLI_HIP_XSTAGE=0: one-row f32 GEMVs convert per stage and wave instead.
+static bool xstage_enabled() {
+    const char *e = std::getenv("COLI_HIP_XSTAGE");
+    return !(e && e[0] == '0');
+}
+
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
@@ -229,6 +235,12 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
         // conversion chains in flight per CU
         if (pl.R == 1 && !dual && nq >= 64 && 16L * pl.PD * dma_slot_bytes(kind, 1, max_rows) <= 160 * 1024)
             pl.W = 16;
+        // one row of one matrix: convert it once per group into LDS when the
+        // ring leaves room (for the MoE's many small problems the per-stage
+        // conversion measured faster)
+        if (max_rows <= 1 && inline_prob && xstage_enabled() &&
+            (long)pl.W * pl.PD * dma_slot_bytes(kind, pl.R, max_rows) + (long)nq * 516 <= 160 * 1024)
+            a.xstage = 1;
     } else if (!flush_frags(ctx, set)) {
         return 0;
     }

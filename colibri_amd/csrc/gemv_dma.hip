@@ -161,9 +161,14 @@ __device__ __forceinline__ bool f32_to_frags(uint8_t *x, int lane, int *E_out) {
 }
 
 // INL: the single problem a.prob0 (3-D grid: row block, 1, batch tile).
-template <int KIND, int R, bool DUAL, int NB4, int W, int PD, int NXR, bool INL, bool F32>
+// XS (with F32, one row): the workgroup converts its row once into LDS
+// (dynamic shared memory: hi [nq][256 B], lo [nq][256 B], exponents [nq]) while
+// its first weight stages are in flight; the stages then carry weights and
+// scales only.
+template <int KIND, int R, bool DUAL, int NB4, int W, int PD, int NXR, bool INL, bool F32, bool XS = false>
 __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
     using G = DmaGeom<KIND, R, NXR>;
+    static_assert(!XS || (F32 && NXR == 1), "staged activations: f32, one row");
     static_assert(!F32 || NXR == 1 || NXR == 4, "f32 activations: one or four rows per stage");
     constexpr bool XF = NXR > 1;
     constexpr int RT = DUAL ? R / 2 : R;
@@ -268,7 +273,9 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
             __builtin_amdgcn_global_load_lds((const void *)(base + qo + (lane % LPT) * 4),
                                              (lds_void *)(dst + G::kScaleOff + k * 256), 4, 0, 0);
         }
-        if constexpr (F32) {
+        if constexpr (XS) {
+            return;
+        } else if constexpr (F32) {
 #pragma unroll
             for (int k = 0; k < G::kF32Inst; k++) {
                 if constexpr (NXR == 1)
@@ -379,6 +386,107 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
             for (int i = 0; i < NB4; i++) acc[r][i] += ldexpf(t[r][i], Ei[i]);
     };
 
+    // XS: the staged row (set up below, before the loop)
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs_lds[];
+    auto compute_xs = [&](int slot, int q, bool lo) {
+        const uint8_t *src = ring + slot * G::kSlot;
+        const uint8_t *xq = xs_lds + q * 256 + ks * 16;
+        u32x4 w[R];
+        ScaleRegs<KIND> sc[R];
+        half8v xh[4], xl[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) xh[j] = *(const half8v *)(xq + j * 64);
+        if (lo) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) xl[j] = *(const half8v *)(xq + a.nq * 256 + j * 64);
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = LDS_RD(u32x4, src + r * COLI_TILE_BYTES + lane * 16);
+            scale_from_lds<KIND>(sc[r], src + G::kScaleOff + r * ScaleGeom<KIND>::kBytes, lane & 15);
+        }
+        floatx4 t[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) t[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const half8v bw = unpack_b<KIND>(w[r][j]);
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if (lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
+                const float scl = sc[r].get(j);
+#pragma unroll
+                for (int i = 0; i < NB4; i++) t[r][i] = fmaf(d[i], scl, t[r][i]);
+            }
+        }
+        const int Eq = ((const int *)(xs_lds + a.nq * 512))[q];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < NB4; i++) acc[r][i] += ldexpf(t[r][i], Eq);
+    };
+
+    auto run_xs = [&]() {
+        constexpr int L = G::loads(false) - G::kXInst;   // weights and scales only
+#pragma unroll
+        for (int s = 0; s < PD - 1; s++)
+            if (s < nit) issue(s, s, false);
+        // stage the row: thread t converts 8 columns (chunk) c = t + 64 W i
+        // of the row; a quad's sixteen chunks sit on sixteen consecutive lanes
+        const int ncc = a.nq * 16;
+        const float *xrow = (const float *)xsrc_f[0] - lane;   // row start (xsrc_f[0] = row + lane)
+        bool any = false;
+        for (int c0 = 0; c0 < ncc; c0 += 64 * W) {
+            const int c = c0 + threadIdx.x;
+            floatx4 v0 = (floatx4){0.f, 0.f, 0.f, 0.f}, v1 = v0;
+            if (c < ncc) {
+                v0 = *GPTR(floatx4, xrow + c * 8);
+                v1 = *GPTR(floatx4, xrow + c * 8 + 4);
+            }
+            float m = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) m = fmaxf(m, fmaxf(fabsf(v0[t]), fabsf(v1[t])));
+            m = dpp_max16(m);
+            int E = 0;
+            if (m > 0.0f && isfinite(m)) {
+                frexpf(m, &E);
+                E -= 15;
+            }
+            if (c < ncc) {
+                const float u[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                half8v h, l;
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const int off = KIND != COLI_KIND_FP4 ? (t < 4 ? 2 * t : 2 * (t - 4) + 1) : t;
+                    float y = ldexpf(u[off], -E);
+                    if (KIND != COLI_KIND_FP4 && (off & 1)) y *= 0.0625f;
+                    h[t] = (_Float16)y;
+                    l[t] = (_Float16)(y - (float)h[t]);
+                    any |= l[t] != (_Float16)0.0f;
+                }
+                *(half8v *)(xs_lds + c * 16) = h;
+                *(half8v *)(xs_lds + a.nq * 256 + c * 16) = l;
+                if ((c & 15) == 0) ((int *)(xs_lds + a.nq * 512))[c >> 4] = E;
+            }
+        }
+        const bool lo = __syncthreads_or(any);
+        for (int it0 = 0; it0 < nit; it0 += PD) {
+#pragma unroll
+            for (int u = 0; u < PD; u++) {
+                const int it = it0 + u;
+                if (it >= nit) break;
+                if (it + PD - 1 < nit) {
+                    issue(it + PD - 1, (u + PD - 1) % PD, false);
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PD - 1) * L) : "memory");
+                } else {
+                    dma_wait_tail<L, PD>(nit - 1 - it);
+                }
+                compute_xs(u, q_first + it * W, lo);
+            }
+        }
+    };
+
     auto run_f32 = [&]() {
         constexpr int L = G::loads_f32();
 #pragma unroll
@@ -421,7 +529,8 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
             }
         }
     };
-    if constexpr (F32) run_f32();
+    if constexpr (XS) run_xs();
+    else if constexpr (F32) run_f32();
     else if (*a.haslo >= a.lo_gen) run(std::true_type{});   // >=: stays correct under graph replay
     else run(std::false_type{});
 
@@ -465,6 +574,19 @@ static hipError_t launch_dma6(const ColiGemvArgs &a, int blocks, hipStream_t st)
     if constexpr (W * PD * G::kSlot > 160 * 1024 || (PD - 1) * (F32 ? G::loads_f32() : G::loads(true)) > 63) {
         return hipErrorInvalidConfiguration;
     } else {
+        if constexpr (F32 && NXR == 1) {
+            if (a.xstage) {   // the row staged once per workgroup
+                const size_t shm = (size_t)a.nq * 516;
+                if ((size_t)W * PD * G::kSlot + shm > 160 * 1024) return hipErrorInvalidConfiguration;
+                if (!a.prob)
+                    hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, true, F32, true>),
+                                       dim3(a.rb_per_prob, 1, a.n_bt), dim3(64 * W), shm, st, a);
+                else
+                    hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, false, F32, true>),
+                                       dim3(blocks), dim3(64 * W), shm, st, a);
+                return hipGetLastError();
+            }
+        }
         if (!a.prob)
             hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, true, F32>),
                                dim3(a.rb_per_prob, 1, a.n_bt), dim3(64 * W), 0, st, a);
