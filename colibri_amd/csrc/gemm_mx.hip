@@ -135,7 +135,9 @@ __global__ __launch_bounds__(256) void coli_prep_fp8(const float *__restrict__ x
             }
         }
     }
-    if (__builtin_amdgcn_ballot_w64(need) && (threadIdx.x & 63) == 0) atomicMax(more, gen);
+    if (__builtin_amdgcn_ballot_w64(need) && (threadIdx.x & 63) == 0 &&
+        __hip_atomic_load(more, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen)   // skip once raised
+        atomicMax(more, gen);
 }
 
 // 4x4 dword transpose across the four 16-lane rows: lane (c, g) ends with
