@@ -31,14 +31,15 @@ def _get(b, p, shape):
 
 
 # (200, 384): one group per row block; (128, 16384): long K split across
-# workgroups, whose arrival counters must be back at zero after every launch.
+# workgroups, whose arrival counters must be back at zero after every launch;
+# (4096, 4096): the LDS-ring kernel on f32 rows (one row: staged once per
+# workgroup; three rows: converted per stage).
 @pytest.mark.parametrize("fmt", [4, 7])
-@pytest.mark.parametrize("O,I", [(200, 384), (128, 16384)])
-def test_gemm_graph_replays_match_eager(session, fmt, O, I):
+@pytest.mark.parametrize("O,I,S", [(200, 384, 3), (128, 16384, 3), (4096, 4096, 1), (4096, 4096, 3)])
+def test_gemm_graph_replays_match_eager(session, fmt, O, I, S):
     b = session.b
     st = b.hip_stream(0)
-    rng = np.random.default_rng(50 + fmt + I)
-    S = 3
+    rng = np.random.default_rng(50 + fmt + I + S)
     if fmt == 4:
         q4, sc = rand_i4(rng, O, I, 32)
         h = session.upload(q4, sc, 4, I, O, 32)
@@ -73,11 +74,15 @@ def test_gemm_graph_replays_match_eager(session, fmt, O, I):
         session.free(h)
 
 
-def test_moe_graph_replays_match_eager(session):
+# (256, 16): routing in one launch; (1536, 256): router partials, then the
+# selection and union in one launch (both with arrival counters that must be
+# back at zero after every replay)
+@pytest.mark.parametrize("D,E", [(256, 16), (1536, 256)])
+def test_moe_graph_replays_match_eager(session, D, E):
     b = session.b
     st = b.hip_stream(0)
-    rng = np.random.default_rng(61)
-    D, I, E, K, S = 256, 128, 16, 4, 5
+    rng = np.random.default_rng(61 + E)
+    I, K, S = 128, 4, 5
     layer = Layer(rng, 7, D, I, E, shared=True)
     x, W, bias = make_router_inputs(rng, S, D, E, K, 1, bias=True)
     hs = layer.upload(session)
