@@ -374,6 +374,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     // INL launches a 3-D grid (row block, split, batch tile): no index
     // arithmetic on kernel arguments precedes the first loads.
     int p = 0, bt, rb, s;
+    ColiProb pdesc;
     if constexpr (INL) {
         rb = blockIdx.x;
         s = blockIdx.y;
@@ -384,6 +385,9 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
         const int items_per_p = a.n_bt * items_per_bt;
         p = item / items_per_p;
         if (p >= a.nprob) return;
+        // the descriptor (inside the array: p < nprob) and the live count are
+        // read together, one memory round trip before the weight loads
+        pdesc = a.prob[p];
         if (a.nprob_dev && p >= *a.nprob_dev) return;
         int rem = item - p * items_per_p;
         bt = rem / items_per_bt;
@@ -391,7 +395,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
         rb = rem / a.splits;
         s = rem - rb * a.splits;
     }
-    const ColiProb pr = uniform_prob(INL ? a.prob0 : a.prob[p]);
+    const ColiProb pr = uniform_prob(INL ? a.prob0 : pdesc);
     const int nb = min(16, pr.nrows - 16 * bt);
     if constexpr (!INL) {
         if (nb <= 0) return;

@@ -180,6 +180,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int p = 0, bt, rb;
+    ColiProb pdesc;
     if constexpr (INL) {
         rb = blockIdx.x;
         bt = blockIdx.z;
@@ -188,12 +189,15 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
         const int items_per_p = a.n_bt * a.rb_per_prob;
         p = item / items_per_p;
         if (p >= a.nprob) return;
+        // the descriptor (inside the array: p < nprob) and the live count are
+        // read together, one memory round trip before the weight loads
+        pdesc = a.prob[p];
         if (a.nprob_dev && p >= *a.nprob_dev) return;
         const int rem = item - p * items_per_p;
         bt = rem / a.rb_per_prob;
         rb = rem - bt * a.rb_per_prob;
     }
-    const ColiProb pr = uniform_prob(INL ? a.prob0 : a.prob[p]);
+    const ColiProb pr = uniform_prob(INL ? a.prob0 : pdesc);
     const int nb = min(16, pr.nrows - 16 * bt);
     if constexpr (!INL) {
         if (nb <= 0) return;
