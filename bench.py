@@ -389,6 +389,87 @@ def measured_traffic():
         return None
 
 
+def issue_take(bench, name, fmt, D, I, count=8, reps=200):
+    """Decode-time expert group (one row for each of `count` experts), the
+    reference's async split (c/backend_cuda.cu:1677-1812; the CPU share of a
+    layer runs between issue and take, c/colibri.c:4467-4531 and 4795):
+    host wall time of the sync call, of issue() and of take(), and of
+    issue -> host work of the sync call's length -> take, against the two
+    run back to back. Host buffers in and out, as the ABI has them."""
+    from colibri_amd.backend import f32p, i32p, tensor_array
+    b = bench.b
+    stage = bench.alloc(I * D // 2)
+    hs = []
+    seed = 7000
+    for e in range(count):
+        trip = []
+        for (O, II) in ((I, D), (I, D), (D, I)):
+            seed += 1
+            if fmt == 4:
+                trip.append(bench.tensor_i4(stage, O, II, fp16_scales(bench.rng, O, II // 32), seed))
+            else:
+                trip.append(bench.tensor_fp4(stage, O, II, bench.rng.integers(119, 124, (O, II // 32),
+                                                                               dtype=np.uint8), seed))
+        hs.append(trip)
+    g, ga = tensor_array([t[0] for t in hs])
+    u, ua = tensor_array([t[1] for t in hs])
+    d, da = tensor_array([t[2] for t in hs])
+    rows = np.ones(count, np.int32)
+    x = bf16_exact(bench.rng.standard_normal((count, D)).astype(np.float32))
+    y = np.zeros((count, D), np.float32)
+    pc = time.perf_counter
+
+    def sync():
+        if not b.cuda_expert_group(g, u, d, i32p(rows), count, f32p(y), f32p(x)):
+            raise RuntimeError("coli_cuda_expert_group failed")
+
+    def issue():
+        if not b.cuda_expert_group_issue(g, u, d, i32p(rows), count, f32p(x)):
+            raise RuntimeError("coli_cuda_expert_group_issue failed")
+
+    def take():
+        if not b.cuda_expert_group_take(0):
+            raise RuntimeError("coli_cuda_expert_group_take returned NULL")
+
+    def spin(sec):
+        t = pc() + sec
+        while pc() < t:
+            pass
+
+    for _ in range(10):
+        sync()
+        issue()
+        take()
+    t_sync, t_issue, t_take, t_ovl = [], [], [], []
+    for _ in range(reps):
+        t0 = pc()
+        sync()
+        t_sync.append(pc() - t0)
+    cpu = float(np.median(t_sync))
+    for _ in range(reps):
+        t0 = pc()
+        issue()
+        t1 = pc()
+        take()
+        t2 = pc()
+        t_issue.append(t1 - t0)
+        t_take.append(t2 - t1)
+    for _ in range(reps):
+        t0 = pc()
+        issue()
+        spin(cpu)
+        take()
+        t_ovl.append(pc() - t0)
+    for trip in hs:
+        for t in trip:
+            b.cuda_tensor_free(t)
+    med = lambda v: round(float(np.median(v)) * 1e6, 1)
+    return {"shape": f"{name}: {count} experts x 1 row, D={D}, I={I}, fmt={fmt}",
+            "sync_call_us": med(t_sync), "issue_us": med(t_issue), "take_after_issue_us": med(t_take),
+            "issue_hostwork_take_us": med(t_ovl), "hostwork_us": round(cpu * 1e6, 1),
+            "serial_us": round(2 * cpu * 1e6, 1)}
+
+
 def moe_layers(bench):
     """The MoE-layer measurements of configs[0], [2], [3] and [4]."""
     res = {
@@ -404,6 +485,9 @@ def moe_layers(bench):
                                                       steps=5, per_token=True).items() if k.startswith("B")})
         ver[tag] = r
     res["configs[3]_verification_21rows"] = ver
+    # the async issue/take split at decode, overlapped with host work
+    res["issue_take"] = {"olmoe_int4": issue_take(bench, "olmoe", 4, 2048, 1024),
+                         "dsv3_mxfp4": issue_take(bench, "dsv3", 7, 7168, 2048)}
     # Kimi-shaped prefill chunk, 512 tokens, 384 experts top-8,
     # router logits ~N(0,1) with a Zipf(1.1) selection bias
     res["configs[4]_kimi_prefill_512"] = {

@@ -366,8 +366,10 @@ struct Member {
 };
 
 // x_dev: [total, D] rows in member order; result y_dev: [total, D].
+// drained: the stream was synchronized since the last copy out of the
+// pinned descriptor staging was queued (it is not waited for again).
 static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, int D, int I, float *y_dev,
-                            const float *x_dev) {
+                            const float *x_dev, bool drained) {
     if (!reserve(ctx, &ctx->h, (size_t)total * I * sizeof(float), 0)) return 0;
     float *h = (float *)ctx->h.p;
 
@@ -454,7 +456,7 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
             !reserve(ctx, &ctx->prob, pb + mb, 0))
             return 0;
         // the pinned staging may still feed a queued copy of the previous call
-        if (!hip_ok(hipStreamSynchronize(ctx->stream), "descriptor staging")) return 0;
+        if (!drained && !hip_ok(hipStreamSynchronize(ctx->stream), "descriptor staging")) return 0;
         std::memcpy(ctx->host_prob, probs.data(), pb);
         if (mb) std::memcpy((char *)ctx->host_prob + pb, mt.data(), mb);
         if (!hip_ok(hipMemcpyAsync(ctx->prob.p, ctx->host_prob, pb + mb, hipMemcpyHostToDevice, ctx->stream),
@@ -554,7 +556,9 @@ static int group_stage_and_run(DevCtx *ctx, std::vector<Member> &mem, int count,
     if (!hip_ok(hipMemcpyAsync(ctx->x.p, ctx->host_x, xb, hipMemcpyHostToDevice, ctx->stream), "group input upload"))
         return 0;
     if (ev) (void)hipEventRecord(ev[1], ctx->stream);
-    if (!run_expert_group(ctx, mem.data(), count, total, D, I, (float *)ctx->y.p, (const float *)ctx->x.p)) return 0;
+    // the stream was drained above; what it holds since reads host_x only
+    if (!run_expert_group(ctx, mem.data(), count, total, D, I, (float *)ctx->y.p, (const float *)ctx->x.p, true))
+        return 0;
     if (ev) (void)hipEventRecord(ev[2], ctx->stream);
     if (!hip_ok(hipMemcpyAsync(ctx->host_y, ctx->y.p, xb, hipMemcpyDeviceToHost, ctx->stream),
                 "group output download"))
@@ -855,7 +859,7 @@ extern "C" int coli_cuda_expert_group_resident_issue(ColiCudaTensor *const *gate
                                                 (size_t)D * sizeof(float), ctx->stream);
         if (!hip_ok(e, "resident input")) return 0;
     }
-    if (!run_expert_group(ctx, mem.data(), count, total, D, I, (float *)ctx->y.p, xr)) return 0;
+    if (!run_expert_group(ctx, mem.data(), count, total, D, I, (float *)ctx->y.p, xr, false)) return 0;
     float *local = home_device == ctx->device ? partial_slot_dev : (float *)ctx->rslot.p;
     if (!hip_ok(coli_launch_weighted_sum_rows(local, (const float *)ctx->y.p, (const float *)ctx->rw.p, count, D,
                                               ctx->stream),
