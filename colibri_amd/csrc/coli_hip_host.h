@@ -95,6 +95,7 @@ hipError_t coli_launch_zero_i32(int *p, int n, hipStream_t st);
 hipError_t coli_launch_fill_random(void *dev, size_t n, unsigned long long seed, hipStream_t st);
 hipError_t coli_launch_silu_mul(float *gate, const float *up, size_t n, hipStream_t st);
 hipError_t coli_launch_silu_mul_to(float *h, const float *gate, const float *up, size_t n, hipStream_t st);
+hipError_t coli_launch_copy_f32(float *dst, const float *src, size_t n, hipStream_t st);
 hipError_t coli_launch_add_n(float *x, const float *t, size_t n, hipStream_t st);
 hipError_t coli_launch_rows_add(float *x, const float *partial, const int *rows, int nrows, int D,
                                 hipStream_t st);

@@ -148,6 +148,24 @@ extern "C" hipError_t coli_launch_silu_mul_to(float *h, const float *gate, const
     hipLaunchKernelGGL(coli_silu_mul_to, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, h, gate, up, n);
     return hipGetLastError();
 }
+// Copy n floats between buffers either side of PCIe (pinned host memory seen
+// through its device pointer): one launch instead of a DMA-engine copy.
+__global__ __launch_bounds__(256) void coli_copy_f32(float *__restrict__ dst, const float *__restrict__ src,
+                                                     size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (4 * i + 3 < n) {
+        *(floatx4 *)(dst + 4 * i) = *(const floatx4 *)(src + 4 * i);
+    } else {
+        for (size_t k = 4 * i; k < n; k++) dst[k] = src[k];
+    }
+}
+extern "C" hipError_t coli_launch_copy_f32(float *dst, const float *src, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    if ((uintptr_t)dst % 16 || (uintptr_t)src % 16) return hipErrorInvalidValue;
+    const size_t n4 = (n + 3) / 4;
+    hipLaunchKernelGGL(coli_copy_f32, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, dst, src, n);
+    return hipGetLastError();
+}
 extern "C" hipError_t coli_launch_add_n(float *x, const float *t, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(coli_add_n, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, t, n);
     return hipGetLastError();
