@@ -39,8 +39,13 @@
  *   cref_route_*: brute force (full stable sort of all E) + NaN fallback
  *       (c/tests/test_router_nan.c:37-75 semantics).
  *   cref_expert_union: set invariant + first-seen order.
- *   cref_swiglu / cref_moe_layer: closed form composition; checked against
- *       a float64 re-evaluation of the same composition in tests.
+ *   cref_swiglu: closed form.
+ *   cref_moe_layer: against the layer evaluated in float64 from dequantized
+ *       weights (full-sort router, silu * up, slot-order weighted sum, shared
+ *       expert weight 1) in fmt 4 / 7 / 17, route modes 0-3, with and
+ *       without the shared expert: indices exact, outputs within 2e-5 of
+ *       the magnitude sum (tests/test_oracle_cpu.py
+ *       test_moe_layer_vs_f64_composition).
  */
 #ifndef COLI_CPU_REF_H
 #define COLI_CPU_REF_H

@@ -78,6 +78,7 @@ class Cref(_Lib):
         self._union = self.fn("expert_union", [_i32, _f, _i32, _i, _i, _i, _i32, _i32,
                                                _i32, _i32, _f], _i)
         self._swiglu = self.fn("swiglu", [_f, _f, _f, C.c_size_t])
+        self._moe = self.fn("moe_layer", [C.c_void_p, _f, _i, _f, _i32, _f, _i32], _i)
         self._swiglu_v4 = self.fn("swiglu_v4", [_f, _f, _f, C.c_size_t, C.c_float])
 
     def qdq(self, x, block=128):
@@ -170,6 +171,44 @@ class Cref(_Lib):
         h = np.empty_like(g)
         self._swiglu_v4(f32p(h), f32p(g), f32p(u), g.size, limit)
         return h
+
+
+class CrefMoe(C.Structure):
+    """cpu_ref.h CrefMoe."""
+    _fields_ = [(n, C.c_int) for n in ("fmt", "D", "I", "E", "K", "gs", "route_mode", "norm_topk",
+                                      "has_shared")] + \
+        [("topp", C.c_float), ("routed_scale", C.c_float), ("router_w", _f), ("router_bias", _f)] + \
+        [(n, C.POINTER(C.c_void_p)) for n in ("gq", "gsc", "uq", "usc", "dq", "dsc")] + \
+        [(n, C.c_void_p) for n in ("sh_gq", "sh_uq", "sh_dq", "sh_gsc", "sh_usc", "sh_dsc")]
+
+
+def cref_moe_layer(lib, fmt, x, W, bias, experts, shared, K, mode, norm_topk=0, topp=0.0,
+                   routed_scale=1.0, gs=32):
+    """cref_moe_layer on source-layout experts [(gq, gsc), (uq, usc), (dq, dsc)]
+    (fmt 4: f32 scales; fmt 7 / 17: e8m0 bytes). Returns out, idx, w, keff."""
+    x = np.ascontiguousarray(x, np.float32)
+    S, D = x.shape
+    E = len(experts)
+    I = experts[0][0][0].shape[0]
+    keep = [x, W, bias]
+    def arr(k, j):
+        a = (C.c_void_p * E)(*[e[k][j].ctypes.data for e in experts])
+        keep.append(a)
+        return C.cast(a, C.POINTER(C.c_void_p))
+    m = CrefMoe(fmt, D, I, E, K, gs, mode, norm_topk, 1 if shared is not None else 0, topp, routed_scale,
+                f32p(W), f32p(bias) if bias is not None else None,
+                arr(0, 0), arr(0, 1), arr(1, 0), arr(1, 1), arr(2, 0), arr(2, 1))
+    if shared is not None:
+        m.sh_gq, m.sh_gsc = shared[0][0].ctypes.data, shared[0][1].ctypes.data
+        m.sh_uq, m.sh_usc = shared[1][0].ctypes.data, shared[1][1].ctypes.data
+        m.sh_dq, m.sh_dsc = shared[2][0].ctypes.data, shared[2][1].ctypes.data
+    out = np.empty((S, D), np.float32)
+    idx = np.zeros((S, K), np.int32)
+    w = np.zeros((S, K), np.float32)
+    keff = np.zeros(S, np.int32)
+    rc = lib._moe(C.byref(m), f32p(x), S, f32p(out), i32p(idx), f32p(w), i32p(keff))
+    assert rc == 0
+    return out, idx, w, keff
 
 
 class Ref(_Lib):
