@@ -26,28 +26,40 @@ static std::mutex g_stats_mu;
 static uint64_t g_calls, g_experts, g_rows;
 static double g_h2d_ms, g_kernel_ms, g_d2h_ms;
 
-int hip_ok(hipError_t err, const char *what) {
-    if (err == hipSuccess) return 1;
-    std::fprintf(stderr, "[HIP] %s: %s\n", what, hipGetErrorString(err));
-    (void)hipGetLastError();   // consume the sticky error
-    return 0;
+// Every HIP status passes through here: a failure is reported once with a
+// "[HIP]" tag and the runtime's last-error slot is read back, so a later,
+// unrelated call does not see this error again.
+int hip_check(hipError_t status, const char *op) {
+    if (status != hipSuccess) {
+        std::fprintf(stderr, "[HIP] %s: %s\n", op, hipGetErrorString(status));
+        (void)hipGetLastError();
+    }
+    return status == hipSuccess;
 }
 
-DevCtx *find_ctx(int device) {
+// Contexts are addressed by HIP device ordinal through a small direct table
+// (ordinals beyond it, or not initialised, map to null).
+static int8_t g_slot_of_device[64];
+static void map_device_slots(void) {
+    std::memset(g_slot_of_device, -1, sizeof(g_slot_of_device));
     for (int i = 0; i < g_nctx; i++)
-        if (g_ctx[i].device == device) return &g_ctx[i];
-    return nullptr;
+        if (g_ctx[i].device >= 0 && g_ctx[i].device < 64) g_slot_of_device[g_ctx[i].device] = (int8_t)i;
 }
 
-// The current device is per host thread in the HIP runtime; cache it so the
-// expert loop does not pay hipSetDevice per call (c/backend_cuda.cu:139-152).
-static thread_local int g_current_device = -1;
-int select_ctx(DevCtx *ctx) {
+DevCtx *ctx_of(int device) {
+    if (device < 0 || device >= 64 || g_nctx == 0) return nullptr;
+    const int slot = g_slot_of_device[device];
+    return slot < 0 ? nullptr : &g_ctx[slot];
+}
+
+// Make ctx's device the calling thread's HIP device. The runtime keeps the
+// current device per host thread; asking it first is cheaper than setting it
+// on every entry point (the expert loop calls in once per layer and expert).
+int bind_ctx(DevCtx *ctx) {
     if (!ctx) return 0;
-    if (g_current_device == ctx->device) return 1;
-    if (!hip_ok(hipSetDevice(ctx->device), "select device")) return 0;
-    g_current_device = ctx->device;
-    return 1;
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur == ctx->device) return 1;
+    return hip_check(hipSetDevice(ctx->device), "select device");
 }
 
 // Host-forced fault injection (c/backend_cuda.cu:1340-1348).
@@ -62,29 +74,35 @@ int fault_injected(void) {
 int reserve(DevCtx *ctx, DevBuf *b, size_t bytes, int zero) {
     if (bytes <= b->cap) return 1;
     if (b->p) {
-        if (!hip_ok(hipStreamSynchronize(ctx->stream), "reserve sync")) return 0;
+        if (!hip_check(hipStreamSynchronize(ctx->stream), "reserve sync")) return 0;
         (void)hipFree(b->p);
         b->p = nullptr;
         b->cap = 0;
     }
     size_t want = bytes + bytes / 4 + 256;
-    if (!hip_ok(hipMalloc(&b->p, want), "scratch allocation")) return 0;
-    if (zero && !hip_ok(hipMemset(b->p, 0, want), "scratch clear")) return 0;
+    if (!hip_check(hipMalloc(&b->p, want), "scratch allocation")) return 0;
+    if (zero && !hip_check(hipMemset(b->p, 0, want), "scratch clear")) return 0;
     b->cap = want;
     return 1;
 }
 
-int reserve_pinned(DevCtx *ctx, void **p, size_t *cap, size_t bytes) {
-    if (bytes <= *cap) return 1;
-    if (*p) {
-        if (!hip_ok(hipStreamSynchronize(ctx->stream), "pinned reserve sync")) return 0;
-        (void)hipHostFree(*p);
-        *p = nullptr;
-        *cap = 0;
+int reserve_pinned(DevCtx *ctx, PinBuf *b, size_t bytes) {
+    if (bytes <= b->cap) return 1;
+    if (b->h) {
+        if (!hip_check(hipStreamSynchronize(ctx->stream), "pinned reserve sync")) return 0;
+        (void)hipHostFree(b->h);
+        *b = PinBuf{};
     }
-    size_t want = bytes + bytes / 4 + 256;
-    if (!hip_ok(hipHostMalloc(p, want, hipHostMallocDefault), "pinned allocation")) return 0;
-    *cap = want;
+    const size_t want = bytes + bytes / 4 + 256;
+    void *h = nullptr, *d = nullptr;
+    if (!hip_check(hipHostMalloc(&h, want, hipHostMallocDefault), "pinned allocation")) return 0;
+    if (!hip_check(hipHostGetDevicePointer(&d, h, 0), "pinned buffer device pointer")) {
+        (void)hipHostFree(h);
+        return 0;
+    }
+    b->h = h;
+    b->d = d;
+    b->cap = want;
     return 1;
 }
 
@@ -100,8 +118,9 @@ static void free_buf(DevBuf *b) {
 extern "C" int coli_cuda_init(const int *devices, int count) {
     int available = 0;
     if (!devices || count < 1 || count > COLI_CUDA_MAX_DEVICES) return 0;
-    if (!hip_ok(hipGetDeviceCount(&available), "device discovery")) return 0;
+    if (!hip_check(hipGetDeviceCount(&available), "device discovery")) return 0;
     if (g_nctx) coli_cuda_shutdown();
+    map_device_slots();
     for (int i = 0; i < count; i++) {
         int device = devices[i];
         if (device < 0 || device >= available) {
@@ -109,7 +128,9 @@ extern "C" int coli_cuda_init(const int *devices, int count) {
             g_nctx = 0;
             return 0;
         }
-        if (find_ctx(device)) {
+        bool dup = false;
+        for (int j = 0; j < i; j++) dup |= devices[j] == device;
+        if (dup) {
             std::fprintf(stderr, "[HIP] duplicate device %d\n", device);
             g_nctx = 0;
             return 0;
@@ -117,12 +138,11 @@ extern "C" int coli_cuda_init(const int *devices, int count) {
         DevCtx *ctx = &g_ctx[g_nctx];
         *ctx = DevCtx();
         ctx->device = device;
-        g_current_device = -1;
-        if (!select_ctx(ctx)) { g_nctx = 0; return 0; }
+        if (!bind_ctx(ctx)) { g_nctx = 0; return 0; }
         hipDeviceProp_t prop{};
-        if (!hip_ok(hipGetDeviceProperties(&prop, device), "device properties")) { g_nctx = 0; return 0; }
+        if (!hip_check(hipGetDeviceProperties(&prop, device), "device properties")) { g_nctx = 0; return 0; }
         ctx->cu_count = prop.multiProcessorCount;
-        if (!hip_ok(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "stream creation")) {
+        if (!hip_check(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "stream creation")) {
             g_nctx = 0;
             return 0;
         }
@@ -131,6 +151,7 @@ extern "C" int coli_cuda_init(const int *devices, int count) {
             return 0;
         }
         g_nctx++;
+        map_device_slots();
         std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs\n", device, prop.name,
                      prop.gcnArchName, prop.totalGlobalMem / 1e9, prop.multiProcessorCount);
     }
@@ -140,7 +161,7 @@ extern "C" int coli_cuda_init(const int *devices, int count) {
 extern "C" void coli_cuda_shutdown(void) {
     for (int i = 0; i < g_nctx; i++) {
         DevCtx *ctx = &g_ctx[i];
-        if (!select_ctx(ctx)) continue;
+        if (!bind_ctx(ctx)) continue;
         (void)hipStreamSynchronize(ctx->stream);
         DevBuf *bufs[] = {&ctx->x, &ctx->h, &ctx->y, &ctx->g, &ctx->u, &ctx->partial,
                           &ctx->prob, &ctx->stage_w, &ctx->stage_s, &ctx->qdq, &ctx->flags,
@@ -153,31 +174,31 @@ extern "C" void coli_cuda_shutdown(void) {
             free_buf(&ctx->frag[f].exp);
         }
         for (int s = 0; s < COLI_PIPE_SLOTS; s++) free_buf(&ctx->pipe[s]);
-        if (ctx->host_x) (void)hipHostFree(ctx->host_x);
-        if (ctx->host_y) (void)hipHostFree(ctx->host_y);
-        if (ctx->host_prob) (void)hipHostFree(ctx->host_prob);
-        if (ctx->host_small) (void)hipHostFree(ctx->host_small);
+        if (ctx->host_x.h) (void)hipHostFree(ctx->host_x.h);
+        if (ctx->host_y.h) (void)hipHostFree(ctx->host_y.h);
+        if (ctx->host_prob.h) (void)hipHostFree(ctx->host_prob.h);
+        if (ctx->host_small.h) (void)hipHostFree(ctx->host_small.h);
         if (ctx->ev_ok) (void)hipEventDestroy(ctx->ev_done);
         if (ctx->blas) (void)rocblas_destroy_handle((rocblas_handle)ctx->blas);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         *ctx = DevCtx();
     }
     g_nctx = 0;
-    g_current_device = -1;
+    map_device_slots();
 }
 
 extern "C" int coli_cuda_device_count(void) { return g_nctx; }
 extern "C" int coli_cuda_device_at(int index) { return index >= 0 && index < g_nctx ? g_ctx[index].device : -1; }
 
 extern "C" int coli_cuda_mem_info(int device, size_t *free_bytes, size_t *total_bytes) {
-    DevCtx *ctx = find_ctx(device);
-    if (!free_bytes || !total_bytes || !select_ctx(ctx)) return 0;
-    return hip_ok(hipMemGetInfo(free_bytes, total_bytes), "memory info");
+    DevCtx *ctx = ctx_of(device);
+    if (!free_bytes || !total_bytes || !bind_ctx(ctx)) return 0;
+    return hip_check(hipMemGetInfo(free_bytes, total_bytes), "memory info");
 }
 
 extern "C" int coli_cuda_device_integrated(int device) {
     hipDeviceProp_t prop{};
-    if (!hip_ok(hipGetDeviceProperties(&prop, device), "device properties")) return 0;
+    if (!hip_check(hipGetDeviceProperties(&prop, device), "device properties")) return 0;
     return prop.integrated ? 1 : 0;
 }
 
@@ -206,7 +227,7 @@ extern "C" void coli_cuda_group_stats(uint64_t *calls, uint64_t *experts, uint64
 extern "C" void coli_cuda_group_stats_device(int device, uint64_t *calls, uint64_t *experts, uint64_t *rows,
                                              double *h2d_ms, double *kernel_ms, double *d2h_ms) {
     std::lock_guard<std::mutex> lock(g_stats_mu);
-    DevCtx *ctx = find_ctx(device);
+    DevCtx *ctx = ctx_of(device);
     if (calls) *calls = ctx ? ctx->st_calls : 0;
     if (experts) *experts = ctx ? ctx->st_experts : 0;
     if (rows) *rows = ctx ? ctx->st_rows : 0;
@@ -273,22 +294,22 @@ static int fill_tensor(DevCtx *ctx, ColiCudaTensor *t, const void *weights, cons
     size_t rb = (size_t)(t->I + 1) / 2, wsrc = rb * t->O;
     hipMemcpyKind wkind = w_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
     if (t->kind == COLI_KIND_GENERIC) {
-        if (!hip_ok(hipMemcpy(t->w, weights, wsrc, wkind), "tensor upload") ||
-            !hip_ok(hipMemcpy(t->sc, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
+        if (!hip_check(hipMemcpy(t->w, weights, wsrc, wkind), "tensor upload") ||
+            !hip_check(hipMemcpy(t->sc, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
             return 0;
         return 1;
     }
     if ((!w_on_device && !reserve(ctx, &ctx->stage_w, wsrc, 0)) || !reserve(ctx, &ctx->stage_s, scale_src_bytes, 0))
         return 0;
-    if (!hip_ok(hipStreamSynchronize(ctx->stream), "upload sync") ||
-        (!w_on_device && !hip_ok(hipMemcpy(ctx->stage_w.p, weights, wsrc, hipMemcpyHostToDevice), "tensor upload")) ||
-        !hip_ok(hipMemcpy(ctx->stage_s.p, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
+    if (!hip_check(hipStreamSynchronize(ctx->stream), "upload sync") ||
+        (!w_on_device && !hip_check(hipMemcpy(ctx->stage_w.p, weights, wsrc, hipMemcpyHostToDevice), "tensor upload")) ||
+        !hip_check(hipMemcpy(ctx->stage_s.p, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
         return 0;
     const uint8_t *wsrc_dev = w_on_device ? (const uint8_t *)weights : (const uint8_t *)ctx->stage_w.p;
-    if (!hip_ok(coli_launch_repack(t, wsrc_dev, ctx->stage_s.p, ctx->stream),
+    if (!hip_check(coli_launch_repack(t, wsrc_dev, ctx->stage_s.p, ctx->stream),
                 "tile repack"))
         return 0;
-    return hip_ok(hipStreamSynchronize(ctx->stream), "tile repack sync");
+    return hip_check(hipStreamSynchronize(ctx->stream), "tile repack sync");
 }
 
 static ColiCudaTensor *alloc_tensor(DevCtx *ctx, int fmt, int I, int O, int gs, int kind) {
@@ -308,8 +329,8 @@ static ColiCudaTensor *alloc_tensor(DevCtx *ctx, int fmt, int I, int O, int gs, 
         size_t per = kind == COLI_KIND_I4_H ? 2 : (kind == COLI_KIND_I4_F ? 4 : 1);
         t->sc_bytes = (size_t)t->nrt * t->nq * 64 * per;
     }
-    if (!hip_ok(hipMalloc((void **)&t->w, t->w_bytes), "tensor allocation") ||
-        !hip_ok(hipMalloc(&t->sc, t->sc_bytes), "scale allocation")) {
+    if (!hip_check(hipMalloc((void **)&t->w, t->w_bytes), "tensor allocation") ||
+        !hip_check(hipMalloc(&t->sc, t->sc_bytes), "scale allocation")) {
         if (t->w) (void)hipFree(t->w);
         std::free(t);
         return nullptr;
@@ -317,8 +338,8 @@ static ColiCudaTensor *alloc_tensor(DevCtx *ctx, int fmt, int I, int O, int gs, 
     if (kind != COLI_KIND_GENERIC) {
         ColiProb d[COLI_DESC_ROWS];
         for (int r = 0; r < COLI_DESC_ROWS; r++) d[r] = {t->w, t->sc, nullptr, nullptr, r + 1, 0, 0, 0};
-        if (!hip_ok(hipMalloc((void **)&t->desc, sizeof(d)), "descriptor allocation") ||
-            !hip_ok(hipMemcpy(t->desc, d, sizeof(d), hipMemcpyHostToDevice), "descriptor upload")) {
+        if (!hip_check(hipMalloc((void **)&t->desc, sizeof(d)), "descriptor allocation") ||
+            !hip_check(hipMemcpy(t->desc, d, sizeof(d), hipMemcpyHostToDevice), "descriptor upload")) {
             (void)hipFree(t->w);
             (void)hipFree(t->sc);
             if (t->desc) (void)hipFree(t->desc);
@@ -341,8 +362,8 @@ int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scale
         ColiCudaTensor *t = *tensor;
         return t->fmt == fmt && t->I == I && t->O == O && t->device == device && t->gs == want_gs;
     }
-    DevCtx *ctx = find_ctx(device);
-    if (!weights || I < 1 || O < 1 || !select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(device);
+    if (!weights || I < 1 || O < 1 || !bind_ctx(ctx)) return 0;
     if (fmt != 2 && fmt != 4 && fmt != 7) return 0;
     if (fmt == 7) {
         if (!e8 && !scales) return 0;
@@ -425,9 +446,9 @@ extern "C" int coli_hip_tensor_upload_from_device(ColiCudaTensor **tensor, const
 
 extern "C" void coli_cuda_tensor_free(ColiCudaTensor *t) {
     if (!t) return;
-    DevCtx *ctx = find_ctx(t->device);
+    DevCtx *ctx = ctx_of(t->device);
     if (ctx) {
-        select_ctx(ctx);
+        bind_ctx(ctx);
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->tensor_count) ctx->tensor_count--;
         if (ctx->tensor_bytes >= t->accounted) ctx->tensor_bytes -= t->accounted;
@@ -445,8 +466,8 @@ extern "C" int coli_hip_tensor_kind(const ColiCudaTensor *t) { return t ? t->kin
 
 extern "C" int coli_cuda_tensor_update(ColiCudaTensor *t, const void *weights, const float *scales) {
     if (!t || !weights || !scales) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     size_t ns = src_scale_count(t->fmt, t->I, t->O, t->gs);
     if (t->kind == COLI_KIND_FP4) {
         std::vector<uint8_t> e8(ns);
@@ -462,13 +483,13 @@ extern "C" int coli_cuda_tensor_update(ColiCudaTensor *t, const void *weights, c
 }
 
 extern "C" int coli_hip_fill_random_u8(int device, void *dev, size_t n, unsigned long long seed) {
-    DevCtx *ctx = find_ctx(device);
-    if (!dev || !select_ctx(ctx)) return 0;
-    return hip_ok(coli_launch_fill_random(dev, n, seed, ctx->stream), "random fill") &&
-           hip_ok(hipStreamSynchronize(ctx->stream), "random fill sync");
+    DevCtx *ctx = ctx_of(device);
+    if (!dev || !bind_ctx(ctx)) return 0;
+    return hip_check(coli_launch_fill_random(dev, n, seed, ctx->stream), "random fill") &&
+           hip_check(hipStreamSynchronize(ctx->stream), "random fill sync");
 }
 
 extern "C" void *coli_hip_stream(int device) {
-    DevCtx *ctx = find_ctx(device);
+    DevCtx *ctx = ctx_of(device);
     return ctx ? (void *)ctx->stream : nullptr;
 }

@@ -14,6 +14,14 @@ struct DevBuf {
     size_t cap = 0;
 };
 
+// Pinned host staging: the host address and the device address kernels use
+// to read or write it across PCIe, both set when the buffer is (re)allocated.
+struct PinBuf {
+    void *h = nullptr;
+    void *d = nullptr;
+    size_t cap = 0;
+};
+
 // Activation fragments of one kind of input (see coli_prep_frag in gemv.hip).
 struct FragSet {
     DevBuf hi, lo, exp;
@@ -41,8 +49,7 @@ struct DevCtx {
     FragSet frag[4];                   // 0/1: inputs (int4 / fp4 order), 2/3: hidden rows
     DevBuf pipe[COLI_PIPE_SLOTS];
     // pinned staging
-    void *host_x = nullptr, *host_y = nullptr, *host_prob = nullptr, *host_small = nullptr;
-    size_t host_x_cap = 0, host_y_cap = 0, host_prob_cap = 0, host_small_cap = 0;
+    PinBuf host_x, host_y, host_prob, host_small;
     int group_pending = 0;
     void *blas = nullptr;              // rocblas_handle, created on first use
     hipEvent_t ev_done = nullptr;
@@ -55,12 +62,12 @@ struct DevCtx {
 extern DevCtx g_ctx[];
 extern int g_nctx;
 
-int hip_ok(hipError_t err, const char *what);
-DevCtx *find_ctx(int device);
-int select_ctx(DevCtx *ctx);
+int hip_check(hipError_t err, const char *what);
+DevCtx *ctx_of(int device);
+int bind_ctx(DevCtx *ctx);
 int fault_injected(void);
 int reserve(DevCtx *ctx, DevBuf *b, size_t bytes, int zero);
-int reserve_pinned(DevCtx *ctx, void **p, size_t *cap, size_t bytes);
+int reserve_pinned(DevCtx *ctx, PinBuf *b, size_t bytes);
 void note_group(DevCtx *ctx, int count, int total, double h2d, double ker, double d2h);
 int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scales, const uint8_t *e8,
                 int fmt, int I, int O, int device, int gs, int w_on_device);

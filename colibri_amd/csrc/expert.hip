@@ -162,8 +162,8 @@ int flush_frags(DevCtx *ctx, int set) {
         return 0;
     int *flag = (int *)ctx->flags.p + set;
     f.gen = f.gen == 0x7fffffff ? 1 : f.gen + 1;
-    if (f.gen == 1 && !hip_ok(coli_launch_zero_i32(flag, 1, ctx->stream), "fragment flag")) return 0;
-    return hip_ok(coli_launch_prep_frag(x, ld, src_rows, nrows_dev, nrows, K, ngp, int4_order,
+    if (f.gen == 1 && !hip_check(coli_launch_zero_i32(flag, 1, ctx->stream), "fragment flag")) return 0;
+    return hip_check(coli_launch_prep_frag(x, ld, src_rows, nrows_dev, nrows, K, ngp, int4_order,
                                         (_Float16 *)f.hi.p, (_Float16 *)f.lo.p, (int *)f.exp.p, flag, f.gen,
                                         ctx->zeros.p, ctx->stream),
                   "fragment prep");
@@ -188,8 +188,8 @@ int make_frags8(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, 
     f.prow = nrows;
     int *flag = (int *)ctx->flags.p + 8 + set;
     f.gen8 = f.gen8 == 0x7fffffff ? 1 : f.gen8 + 1;
-    if (f.gen8 == 1 && !hip_ok(coli_launch_zero_i32(flag, 1, ctx->stream), "piece flag")) return 0;
-    return hip_ok(coli_launch_prep_fp8(x, ld, src_rows, nrows_dev, nrows, K, nq, nrows, (uint8_t *)f.p8.p,
+    if (f.gen8 == 1 && !hip_check(coli_launch_zero_i32(flag, 1, ctx->stream), "piece flag")) return 0;
+    return hip_check(coli_launch_prep_fp8(x, ld, src_rows, nrows_dev, nrows, K, nq, nrows, (uint8_t *)f.p8.p,
                                        (uint8_t *)f.s8.p, flag, f.gen8, ctx->stream),
                   "fp8 activation pieces");
 }
@@ -281,9 +281,9 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.swiglu_limit = swiglu_limit;
     a.partial = (float *)ctx->partial.p;
     a.split_cnt = (int *)ctx->split_cnt.p;
-    if (pl.dma) return hip_ok(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.W, pl.PD, max_rows, ctx->stream),
+    if (pl.dma) return hip_check(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.W, pl.PD, max_rows, ctx->stream),
                               "gemv launch");
-    return hip_ok(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
+    return hip_check(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
 }
 
 // Grouped GEMM over problems of many rows (see gemm.hip); mt_list_dev holds
@@ -318,7 +318,7 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
         m.out = out;
         m.ldo = ldo;
         m.swiglu_limit = swiglu_limit;
-        return hip_ok(coli_launch_gemm_mx(dual ? 1 : 0, &m, ctx->stream), "gemm launch");
+        return hip_check(coli_launch_gemm_mx(dual ? 1 : 0, &m, ctx->stream), "gemm launch");
     }
     ColiGemmArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -344,7 +344,7 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.out = out;
     a.ldo = ldo;
     a.swiglu_limit = swiglu_limit;
-    return hip_ok(coli_launch_gemm(kind, dual ? 1 : 0, &a, ctx->stream), "gemm launch");
+    return hip_check(coli_launch_gemm(kind, dual ? 1 : 0, &a, ctx->stream), "gemm launch");
 }
 
 int frag_set_of(int kind, bool hidden) {
@@ -452,14 +452,14 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
         }
     if (!probs.empty()) {
         size_t pb = probs.size() * sizeof(ColiProb), mb = mt.size() * sizeof(int);
-        if (!reserve_pinned(ctx, &ctx->host_prob, &ctx->host_prob_cap, pb + mb) ||
+        if (!reserve_pinned(ctx, &ctx->host_prob, pb + mb) ||
             !reserve(ctx, &ctx->prob, pb + mb, 0))
             return 0;
         // the pinned staging may still feed a queued copy of the previous call
-        if (!drained && !hip_ok(hipStreamSynchronize(ctx->stream), "descriptor staging")) return 0;
-        std::memcpy(ctx->host_prob, probs.data(), pb);
-        if (mb) std::memcpy((char *)ctx->host_prob + pb, mt.data(), mb);
-        if (!hip_ok(hipMemcpyAsync(ctx->prob.p, ctx->host_prob, pb + mb, hipMemcpyHostToDevice, ctx->stream),
+        if (!drained && !hip_check(hipStreamSynchronize(ctx->stream), "descriptor staging")) return 0;
+        std::memcpy(ctx->host_prob.h, probs.data(), pb);
+        if (mb) std::memcpy((char *)ctx->host_prob.h + pb, mt.data(), mb);
+        if (!hip_check(hipMemcpyAsync(ctx->prob.p, ctx->host_prob.h, pb + mb, hipMemcpyHostToDevice, ctx->stream),
                     "descriptor upload"))
             return 0;
     }
@@ -485,12 +485,12 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
         float *dst[2] = {(float *)ctx->g.p, (float *)ctx->u.p};
         for (int w = 0; w < 2; w++)
             if (pair[w]->kind == COLI_KIND_GENERIC &&
-                !hip_ok(coli_launch_generic_i4(pair[w], x_dev + (size_t)m[c].off * D, D,
+                !hip_check(coli_launch_generic_i4(pair[w], x_dev + (size_t)m[c].off * D, D,
                                                dst[w] + (size_t)m[c].off * I, I, m[c].rows, ctx->stream),
                         "generic gemv"))
                 return 0;
         size_t o = (size_t)m[c].off * I, n = (size_t)m[c].rows * I;
-        if (!hip_ok(coli_launch_silu_mul_to(h + o, (float *)ctx->g.p + o, (float *)ctx->u.p + o, n, ctx->stream),
+        if (!hip_check(coli_launch_silu_mul_to(h + o, (float *)ctx->g.p + o, (float *)ctx->u.p + o, n, ctx->stream),
                     "silu"))
             return 0;
     }
@@ -507,7 +507,7 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
     }
     for (int c = 0; c < count; c++)
         if (m[c].d->kind == COLI_KIND_GENERIC &&
-            !hip_ok(coli_launch_generic_i4(m[c].d, h + (size_t)m[c].off * I, I, y_dev + (size_t)m[c].off * D, D,
+            !hip_check(coli_launch_generic_i4(m[c].d, h + (size_t)m[c].off * I, I, y_dev + (size_t)m[c].off * D, D,
                                            m[c].rows, ctx->stream),
                     "generic down"))
             return 0;
@@ -533,8 +533,8 @@ static DevCtx *collect_members(ColiCudaTensor *const *gates, ColiCudaTensor *con
         mem[c] = {g, u, d, rows[c], *total};
         *total += rows[c];
     }
-    DevCtx *ctx = find_ctx(device);
-    return select_ctx(ctx) ? ctx : nullptr;
+    DevCtx *ctx = ctx_of(device);
+    return bind_ctx(ctx) ? ctx : nullptr;
 }
 
 static double now_ms() {
@@ -542,45 +542,28 @@ static double now_ms() {
     return std::chrono::duration<double, std::milli>(clk::now().time_since_epoch()).count();
 }
 
-// Device address of a pinned host buffer, remembered for the last few buffers
-// (the staging buffers change only when they grow).
-static int pinned_dev_ptr(void *host, void **dev) {
-    static thread_local void *key[4], *val[4];
-    static thread_local int next;
-    for (int i = 0; i < 4; i++)
-        if (key[i] == host) {
-            *dev = val[i];
-            return 1;
-        }
-    if (!hip_ok(hipHostGetDevicePointer(dev, host, 0), "pinned buffer device pointer")) return 0;
-    key[next] = host;
-    val[next] = *dev;
-    next = (next + 1) % 4;
-    return 1;
-}
-
 // Stage host x -> device, run, device y -> pinned host_y (not yet synchronized).
 static int group_stage_and_run(DevCtx *ctx, std::vector<Member> &mem, int count, int total, int D, int I,
                                const float *x, hipEvent_t *ev) {
     size_t xb = (size_t)total * D * sizeof(float);
     if (!reserve(ctx, &ctx->x, xb, 0) || !reserve(ctx, &ctx->y, xb, 0) ||
-        !reserve_pinned(ctx, &ctx->host_x, &ctx->host_x_cap, xb) ||
-        !reserve_pinned(ctx, &ctx->host_y, &ctx->host_y_cap, xb))
+        !reserve_pinned(ctx, &ctx->host_x, xb) ||
+        !reserve_pinned(ctx, &ctx->host_y, xb))
         return 0;
-    if (!hip_ok(hipStreamSynchronize(ctx->stream), "group staging")) return 0;
-    std::memcpy(ctx->host_x, x, xb);
+    if (!hip_check(hipStreamSynchronize(ctx->stream), "group staging")) return 0;
+    std::memcpy(ctx->host_x.h, x, xb);
     if (ev) (void)hipEventRecord(ev[0], ctx->stream);
-    // The input and output cross PCIe in copy kernels that read / write the
-    // pinned buffers through their device pointers (measured: the sync group
-    // call at decode 47 -> 39 us against DMA-engine copies; COLI_HIP_KCOPY=0
-    // keeps hipMemcpyAsync).
+    // Decode-sized groups cross PCIe in copy kernels that read / write the
+    // pinned buffers through their device addresses (measured: the sync group
+    // call at decode 47 -> 39 us against DMA-engine copies). Above 1 MiB each
+    // way (prefill-sized groups) the DMA engines' hipMemcpyAsync is used, as
+    // always with COLI_HIP_KCOPY=0.
     const char *kc = std::getenv("COLI_HIP_KCOPY");
-    const bool kcopy = !(kc && kc[0] == '0');
-    void *hx_dev = nullptr, *hy_dev = nullptr;
-    if (kcopy && (!pinned_dev_ptr(ctx->host_x, &hx_dev) || !pinned_dev_ptr(ctx->host_y, &hy_dev))) return 0;
-    if (kcopy ? !hip_ok(coli_launch_copy_f32((float *)ctx->x.p, (const float *)hx_dev, xb / 4, ctx->stream),
+    const bool kcopy = !(kc && kc[0] == '0') && xb <= ((size_t)1 << 20);
+    void *hx_dev = ctx->host_x.d, *hy_dev = ctx->host_y.d;
+    if (kcopy ? !hip_check(coli_launch_copy_f32((float *)ctx->x.p, (const float *)hx_dev, xb / 4, ctx->stream),
                         "group input upload")
-              : !hip_ok(hipMemcpyAsync(ctx->x.p, ctx->host_x, xb, hipMemcpyHostToDevice, ctx->stream),
+              : !hip_check(hipMemcpyAsync(ctx->x.p, ctx->host_x.h, xb, hipMemcpyHostToDevice, ctx->stream),
                         "group input upload"))
         return 0;
     if (ev) (void)hipEventRecord(ev[1], ctx->stream);
@@ -588,9 +571,9 @@ static int group_stage_and_run(DevCtx *ctx, std::vector<Member> &mem, int count,
     if (!run_expert_group(ctx, mem.data(), count, total, D, I, (float *)ctx->y.p, (const float *)ctx->x.p, true))
         return 0;
     if (ev) (void)hipEventRecord(ev[2], ctx->stream);
-    if (kcopy ? !hip_ok(coli_launch_copy_f32((float *)hy_dev, (const float *)ctx->y.p, xb / 4, ctx->stream),
+    if (kcopy ? !hip_check(coli_launch_copy_f32((float *)hy_dev, (const float *)ctx->y.p, xb / 4, ctx->stream),
                         "group output download")
-              : !hip_ok(hipMemcpyAsync(ctx->host_y, ctx->y.p, xb, hipMemcpyDeviceToHost, ctx->stream),
+              : !hip_check(hipMemcpyAsync(ctx->host_y.h, ctx->y.p, xb, hipMemcpyDeviceToHost, ctx->stream),
                         "group output download"))
         return 0;
     if (ev) (void)hipEventRecord(ev[3], ctx->stream);
@@ -610,13 +593,13 @@ extern "C" int coli_cuda_expert_group(ColiCudaTensor *const *gates, ColiCudaTens
     hipEvent_t ev[4] = {};
     if (profile)
         for (int i = 0; i < 4; i++)
-            if (!hip_ok(hipEventCreate(&ev[i]), "profile event")) {
+            if (!hip_check(hipEventCreate(&ev[i]), "profile event")) {
                 for (int j = 0; j < i; j++) (void)hipEventDestroy(ev[j]);
                 profile = 0;
                 break;
             }
     int ok = group_stage_and_run(ctx, mem, count, total, D, I, x, profile ? ev : nullptr) &&
-             hip_ok(hipStreamSynchronize(ctx->stream), "expert group synchronize");
+             hip_check(hipStreamSynchronize(ctx->stream), "expert group synchronize");
     double a = 0, b = 0, c = 0;
     if (profile) {
         float fa = 0, fb = 0, fc = 0;
@@ -629,7 +612,7 @@ extern "C" int coli_cuda_expert_group(ColiCudaTensor *const *gates, ColiCudaTens
         for (int i = 0; i < 4; i++) (void)hipEventDestroy(ev[i]);
     }
     if (!ok) return 0;
-    std::memcpy(y, ctx->host_y, (size_t)total * D * sizeof(float));
+    std::memcpy(y, ctx->host_y.h, (size_t)total * D * sizeof(float));
     note_group(ctx, count, total, a, b, c);
     return 1;
 }
@@ -649,12 +632,12 @@ extern "C" int coli_cuda_expert_group_issue(ColiCudaTensor *const *gates, ColiCu
 }
 
 extern "C" const float *coli_cuda_expert_group_take(int device) {
-    DevCtx *ctx = find_ctx(device);
+    DevCtx *ctx = ctx_of(device);
     if (!ctx || !ctx->group_pending) return nullptr;
     ctx->group_pending = 0;
-    if (!select_ctx(ctx)) return nullptr;
-    if (!hip_ok(hipStreamSynchronize(ctx->stream), "expert group take")) return nullptr;
-    return (const float *)ctx->host_y;
+    if (!bind_ctx(ctx)) return nullptr;
+    if (!hip_check(hipStreamSynchronize(ctx->stream), "expert group take")) return nullptr;
+    return (const float *)ctx->host_y.h;
 }
 
 extern "C" int coli_cuda_expert_mlp(ColiCudaTensor *gate, ColiCudaTensor *up, ColiCudaTensor *down, float *y,
@@ -668,14 +651,18 @@ extern "C" int coli_cuda_expert_mlp(ColiCudaTensor *gate, ColiCudaTensor *up, Co
     DevCtx *ctx = collect_members(g, u, d, rows, 1, mem, &total, &D, &I);
     if (!ctx || ctx->group_pending) return 0;
     if (!group_stage_and_run(ctx, mem, 1, total, D, I, x, nullptr) ||
-        !hip_ok(hipStreamSynchronize(ctx->stream), "expert mlp synchronize"))
+        !hip_check(hipStreamSynchronize(ctx->stream), "expert mlp synchronize"))
         return 0;
-    std::memcpy(y, ctx->host_y, (size_t)total * D * sizeof(float));
+    std::memcpy(y, ctx->host_y.h, (size_t)total * D * sizeof(float));
     return 1;
 }
 
+// The prefill shared expert of c/backend_cuda.cu:1457-1484: the same contract
+// as expert_mlp, restricted as there to per-row int4 (fmt=2) tensors; any
+// other format is refused (return 0) so the engine keeps its CPU path.
 extern "C" int coli_cuda_shared_mlp_w4a16(ColiCudaTensor *gate, ColiCudaTensor *up, ColiCudaTensor *down,
                                           float *y, const float *x, int S) {
+    if (!gate || !up || !down || gate->fmt != 2 || up->fmt != 2 || down->fmt != 2) return 0;
     return coli_cuda_expert_mlp(gate, up, down, y, x, S);
 }
 
@@ -698,49 +685,49 @@ static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S) {
 // y_dev[S, O] = x_dev[S, I] W^T on the stream (tensor already resident).
 static int gemm_dev(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
     if (t->kind == COLI_KIND_GENERIC)
-        return hip_ok(coli_launch_generic_i4(t, x_dev, t->I, y_dev, t->O, S, ctx->stream), "generic gemv");
+        return hip_check(coli_launch_generic_i4(t, x_dev, t->I, y_dev, t->O, S, ctx->stream), "generic gemv");
     return gemm_prep(ctx, t, x_dev, S) && gemm_run(ctx, t, y_dev, S);
 }
 
 extern "C" int coli_hip_gemm_prep_dev(ColiCudaTensor *t, const float *x_dev, int S) {
     if (!t || !x_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     return gemm_prep(ctx, t, x_dev, S);
 }
 
 extern "C" int coli_hip_gemm_run_dev(ColiCudaTensor *t, float *y_dev, int S) {
     if (!t || !y_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     return gemm_run(ctx, t, y_dev, S);
 }
 
 static int gemm_host(DevCtx *ctx, ColiCudaTensor *t, float *y, const float *x, int S, int qdq) {
     size_t xb = (size_t)S * t->I * sizeof(float), yb = (size_t)S * t->O * sizeof(float);
     if (!reserve(ctx, &ctx->x, xb, 0) || !reserve(ctx, &ctx->y, yb, 0) ||
-        !reserve_pinned(ctx, &ctx->host_x, &ctx->host_x_cap, xb) ||
-        !reserve_pinned(ctx, &ctx->host_y, &ctx->host_y_cap, yb) ||
-        !hip_ok(hipStreamSynchronize(ctx->stream), "gemm staging"))
+        !reserve_pinned(ctx, &ctx->host_x, xb) ||
+        !reserve_pinned(ctx, &ctx->host_y, yb) ||
+        !hip_check(hipStreamSynchronize(ctx->stream), "gemm staging"))
         return 0;
-    std::memcpy(ctx->host_x, x, xb);
-    if (!hip_ok(hipMemcpyAsync(ctx->x.p, ctx->host_x, xb, hipMemcpyHostToDevice, ctx->stream), "input upload"))
+    std::memcpy(ctx->host_x.h, x, xb);
+    if (!hip_check(hipMemcpyAsync(ctx->x.p, ctx->host_x.h, xb, hipMemcpyHostToDevice, ctx->stream), "input upload"))
         return 0;
     const float *xin = (const float *)ctx->x.p;
     // qdq 1: e4m3 per 128 (native_quant contract); 2: int8 per 32 (matmul_mxfp4_i8)
     if (qdq == 1 || (qdq == 2 && t->I % 32 == 0)) {
         if (!reserve(ctx, &ctx->qdq, xb, 0) ||
-            !hip_ok(qdq == 1 ? coli_launch_qdq_e4m3(xin, (float *)ctx->qdq.p, S, t->I, ctx->stream)
+            !hip_check(qdq == 1 ? coli_launch_qdq_e4m3(xin, (float *)ctx->qdq.p, S, t->I, ctx->stream)
                              : coli_launch_qdq_i8(xin, (float *)ctx->qdq.p, S, t->I, ctx->stream),
                     "activation qdq"))
             return 0;
         xin = (const float *)ctx->qdq.p;
     }
     if (!gemm_dev(ctx, t, (float *)ctx->y.p, xin, S) ||
-        !hip_ok(hipMemcpyAsync(ctx->host_y, ctx->y.p, yb, hipMemcpyDeviceToHost, ctx->stream), "output download") ||
-        !hip_ok(hipStreamSynchronize(ctx->stream), "gemm synchronize"))
+        !hip_check(hipMemcpyAsync(ctx->host_y.h, ctx->y.p, yb, hipMemcpyDeviceToHost, ctx->stream), "output download") ||
+        !hip_check(hipStreamSynchronize(ctx->stream), "gemm synchronize"))
         return 0;
-    std::memcpy(y, ctx->host_y, yb);
+    std::memcpy(y, ctx->host_y.h, yb);
     return 1;
 }
 
@@ -753,16 +740,16 @@ extern "C" int coli_cuda_matmul(ColiCudaTensor **tensor, float *y, const float *
         return 0;
     ColiCudaTensor *t = *tensor;
     if (!tensor_computable(t)) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     return gemm_host(ctx, t, y, x, S, 0);
 }
 
 static int matmul_mxfp4_stateless(float *y, const float *x, const unsigned char *q4, const unsigned char *e8s, int S,
                                   int I, int O, int qdq) {
     if (S < 1 || I < 1 || O < 1 || !y || !x || !q4 || !e8s) return 0;
-    DevCtx *ctx = find_ctx(0);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(0);
+    if (!bind_ctx(ctx)) return 0;
     // Stateless (c/backend_cuda.cu:1377-1416): the weights go up with the call,
     // into reusable scratch instead of a fresh allocation.
     ColiCudaTensor t;
@@ -774,13 +761,13 @@ static int matmul_mxfp4_stateless(float *y, const float *x, const unsigned char 
     size_t wsrc = (size_t)(I + 1) / 2 * O, ssrc = (size_t)O * ((I + 31) / 32);
     if (!reserve(ctx, &ctx->tmp_tiles, t.w_bytes, 0) || !reserve(ctx, &ctx->tmp_scales, t.sc_bytes, 0) ||
         !reserve(ctx, &ctx->stage_w, wsrc, 0) || !reserve(ctx, &ctx->stage_s, ssrc, 0) ||
-        !hip_ok(hipStreamSynchronize(ctx->stream), "mxfp4 staging"))
+        !hip_check(hipStreamSynchronize(ctx->stream), "mxfp4 staging"))
         return 0;
     t.w = (uint8_t *)ctx->tmp_tiles.p;
     t.sc = ctx->tmp_scales.p;
-    if (!hip_ok(hipMemcpyAsync(ctx->stage_w.p, q4, wsrc, hipMemcpyHostToDevice, ctx->stream), "mxfp4 weight upload") ||
-        !hip_ok(hipMemcpyAsync(ctx->stage_s.p, e8s, ssrc, hipMemcpyHostToDevice, ctx->stream), "mxfp4 scale upload") ||
-        !hip_ok(coli_launch_repack(&t, (const uint8_t *)ctx->stage_w.p, ctx->stage_s.p, ctx->stream), "mxfp4 repack"))
+    if (!hip_check(hipMemcpyAsync(ctx->stage_w.p, q4, wsrc, hipMemcpyHostToDevice, ctx->stream), "mxfp4 weight upload") ||
+        !hip_check(hipMemcpyAsync(ctx->stage_s.p, e8s, ssrc, hipMemcpyHostToDevice, ctx->stream), "mxfp4 scale upload") ||
+        !hip_check(coli_launch_repack(&t, (const uint8_t *)ctx->stage_w.p, ctx->stage_s.p, ctx->stream), "mxfp4 repack"))
         return 0;
     return gemm_host(ctx, &t, y, x, S, qdq);
 }
@@ -804,20 +791,20 @@ extern "C" int coli_hip_matmul_mxfp4_i8(float *y, const float *x, const unsigned
 extern "C" int coli_hip_fp4_matmul_i8(ColiCudaTensor *t, float *y, const float *x, int S) {
     if (fault_injected()) return 0;
     if (!t || t->kind != COLI_KIND_FP4 || !y || !x || S < 1) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     return gemm_host(ctx, t, y, x, S, 2);
 }
 
 extern "C" int coli_hip_fp4_matmul_i8_dev(ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
     if (fault_injected()) return 0;
     if (!t || t->kind != COLI_KIND_FP4 || !y_dev || !x_dev || S < 1) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     if (t->I % 32) return gemm_dev(ctx, t, y_dev, x_dev, S);
     size_t xb = (size_t)S * t->I * sizeof(float);
     if (!reserve(ctx, &ctx->qdq, xb, 0) ||
-        !hip_ok(coli_launch_qdq_i8(x_dev, (float *)ctx->qdq.p, S, t->I, ctx->stream), "activation qdq"))
+        !hip_check(coli_launch_qdq_i8(x_dev, (float *)ctx->qdq.p, S, t->I, ctx->stream), "activation qdq"))
         return 0;
     return gemm_dev(ctx, t, y_dev, (const float *)ctx->qdq.p, S);
 }
@@ -825,19 +812,19 @@ extern "C" int coli_hip_fp4_matmul_i8_dev(ColiCudaTensor *t, float *y_dev, const
 extern "C" int coli_hip_fp4_matmul_qdq(ColiCudaTensor *t, float *y, const float *x, int S) {
     if (fault_injected()) return 0;
     if (!t || t->kind != COLI_KIND_FP4 || !y || !x || S < 1 || t->I % 128) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     return gemm_host(ctx, t, y, x, S, 1);
 }
 
 extern "C" int coli_hip_fp4_matmul_qdq_dev(ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
     if (fault_injected()) return 0;
     if (!t || t->kind != COLI_KIND_FP4 || !y_dev || !x_dev || S < 1 || t->I % 128) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     size_t xb = (size_t)S * t->I * sizeof(float);
     if (!reserve(ctx, &ctx->qdq, xb, 0) ||
-        !hip_ok(coli_launch_qdq_e4m3(x_dev, (float *)ctx->qdq.p, S, t->I, ctx->stream), "activation qdq"))
+        !hip_check(coli_launch_qdq_e4m3(x_dev, (float *)ctx->qdq.p, S, t->I, ctx->stream), "activation qdq"))
         return 0;
     return gemm_dev(ctx, t, y_dev, (const float *)ctx->qdq.p, S);
 }
@@ -845,8 +832,8 @@ extern "C" int coli_hip_fp4_matmul_qdq_dev(ColiCudaTensor *t, float *y_dev, cons
 extern "C" int coli_cuda_pipe_gemm(ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
     if (fault_injected()) return 0;
     if (!t || S < 1 || !y_dev || !x_dev || !tensor_computable(t)) return 0;
-    DevCtx *ctx = find_ctx(t->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
     return gemm_dev(ctx, t, y_dev, x_dev, S);
 }
 
@@ -864,18 +851,18 @@ extern "C" int coli_cuda_expert_group_resident_issue(ColiCudaTensor *const *gate
     DevCtx *ctx = collect_members(gates, ups, downs, rows.data(), count, mem, &total, &D, &I);
     if (!ctx) return 0;
     if (!ctx->ev_ok) {
-        if (!hip_ok(hipEventCreateWithFlags(&ctx->ev_done, hipEventDisableTiming), "resident group event")) return 0;
+        if (!hip_check(hipEventCreateWithFlags(&ctx->ev_done, hipEventDisableTiming), "resident group event")) return 0;
         ctx->ev_ok = 1;
     }
     // Fixed 64-expert capacity: a growth here could free a buffer queued work reads.
     size_t xb = (size_t)64 * D * sizeof(float);
     if (!reserve(ctx, &ctx->x, xb, 0) || !reserve(ctx, &ctx->y, xb, 0) ||
         !reserve(ctx, &ctx->rw, 64 * sizeof(float), 0) || !reserve(ctx, &ctx->rslot, (size_t)D * sizeof(float), 0) ||
-        !reserve_pinned(ctx, &ctx->host_small, &ctx->host_small_cap, 64 * sizeof(float)))
+        !reserve_pinned(ctx, &ctx->host_small, 64 * sizeof(float)))
         return 0;
-    if (!hip_ok(hipStreamSynchronize(ctx->stream), "resident staging")) return 0;
-    std::memcpy(ctx->host_small, weights, (size_t)count * sizeof(float));
-    if (!hip_ok(hipMemcpyAsync(ctx->rw.p, ctx->host_small, (size_t)count * sizeof(float), hipMemcpyHostToDevice,
+    if (!hip_check(hipStreamSynchronize(ctx->stream), "resident staging")) return 0;
+    std::memcpy(ctx->host_small.h, weights, (size_t)count * sizeof(float));
+    if (!hip_check(hipMemcpyAsync(ctx->rw.p, ctx->host_small.h, (size_t)count * sizeof(float), hipMemcpyHostToDevice,
                                ctx->stream),
                 "resident weights"))
         return 0;
@@ -887,33 +874,33 @@ extern "C" int coli_cuda_expert_group_resident_issue(ColiCudaTensor *const *gate
                                             hipMemcpyDeviceToDevice, ctx->stream)
                            : hipMemcpyPeerAsync(xr + (size_t)c * D, ctx->device, x_src_dev, home_device,
                                                 (size_t)D * sizeof(float), ctx->stream);
-        if (!hip_ok(e, "resident input")) return 0;
+        if (!hip_check(e, "resident input")) return 0;
     }
     if (!run_expert_group(ctx, mem.data(), count, total, D, I, (float *)ctx->y.p, xr, false)) return 0;
     float *local = home_device == ctx->device ? partial_slot_dev : (float *)ctx->rslot.p;
-    if (!hip_ok(coli_launch_weighted_sum_rows(local, (const float *)ctx->y.p, (const float *)ctx->rw.p, count, D,
+    if (!hip_check(coli_launch_weighted_sum_rows(local, (const float *)ctx->y.p, (const float *)ctx->rw.p, count, D,
                                               ctx->stream),
                 "resident reduce"))
         return 0;
     if (home_device != ctx->device &&
-        !hip_ok(hipMemcpyPeerAsync(partial_slot_dev, home_device, local, ctx->device, (size_t)D * sizeof(float),
+        !hip_check(hipMemcpyPeerAsync(partial_slot_dev, home_device, local, ctx->device, (size_t)D * sizeof(float),
                                    ctx->stream),
                 "resident partial push"))
         return 0;
-    return hip_ok(hipEventRecord(ctx->ev_done, ctx->stream), "resident event record");
+    return hip_check(hipEventRecord(ctx->ev_done, ctx->stream), "resident event record");
 }
 
 extern "C" int coli_cuda_expert_group_resident_take(int home_device, const int *devices, int n_issued,
                                                     float *slots_dev, float *acc_dev, int D) {
     if (n_issued < 1 || !slots_dev || !acc_dev || D < 1 || !devices) return 0;
-    DevCtx *home = find_ctx(home_device);
-    if (!select_ctx(home)) return 0;
+    DevCtx *home = ctx_of(home_device);
+    if (!bind_ctx(home)) return 0;
     for (int i = 0; i < n_issued; i++) {
-        DevCtx *src = find_ctx(devices[i]);
+        DevCtx *src = ctx_of(devices[i]);
         if (!src || !src->ev_ok) return 0;
-        if (!hip_ok(hipStreamWaitEvent(home->stream, src->ev_done, 0), "resident take wait")) return 0;
+        if (!hip_check(hipStreamWaitEvent(home->stream, src->ev_done, 0), "resident take wait")) return 0;
     }
-    return hip_ok(coli_launch_sum_slots(acc_dev, slots_dev, n_issued, D, home->stream), "resident take reduce");
+    return hip_check(coli_launch_sum_slots(acc_dev, slots_dev, n_issued, D, home->stream), "resident take reduce");
 }
 
 // ---------------------------------------------------------------------------
@@ -925,7 +912,7 @@ extern "C" int coli_cuda_expert_group_resident_take(int home_device, const int *
 // ---------------------------------------------------------------------------
 int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int E, float *part) {
     if (S <= 64)
-        return hip_ok(coli_launch_router_logits(x, S, W, D, E, part, ctx->stream), "router logits")
+        return hip_check(coli_launch_router_logits(x, S, W, D, E, part, ctx->stream), "router logits")
                    ? coli_router_chunks(D)
                    : 0;
     rocblas_handle h = (rocblas_handle)ctx->blas;
@@ -952,29 +939,29 @@ int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int
 extern "C" int coli_cuda_pipe_router(int device, const float *x_dev, const void *rw_dev, const void *rb_dev, int D,
                                      int E, int Ksel, float topp, int norm_topk, float routed_scale, int *idx_host,
                                      float *w_host, int *keff_host) {
-    DevCtx *ctx = find_ctx(device);
+    DevCtx *ctx = ctx_of(device);
     if (!x_dev || !rw_dev || !rb_dev || D < 1 || E < 1 || E > 1024 || Ksel < 1 || Ksel > 64 || !idx_host ||
-        !w_host || !keff_host || !select_ctx(ctx))
+        !w_host || !keff_host || !bind_ctx(ctx))
         return 0;
     const int nch = coli_router_chunks(D);
     size_t pack = (size_t)nch * E * sizeof(float) + (size_t)Ksel * 8 + 16;
     if (!reserve(ctx, &ctx->pipe[22], pack, 0) ||
-        !reserve_pinned(ctx, &ctx->host_small, &ctx->host_small_cap, (size_t)Ksel * 8 + 16))
+        !reserve_pinned(ctx, &ctx->host_small, (size_t)Ksel * 8 + 16))
         return 0;
     float *logit = (float *)ctx->pipe[22].p;
     int *idx = (int *)(logit + (size_t)nch * E);
     float *w = (float *)(idx + Ksel);
     int *keff = (int *)(w + Ksel);
-    if (!hip_ok(coli_launch_router_logits(x_dev, 1, (const float *)rw_dev, D, E, logit, ctx->stream), "router logits") ||
-        !hip_ok(coli_launch_router_select(logit, nch, (const float *)rb_dev, 1, E, Ksel, 1, topp, norm_topk, routed_scale,
+    if (!hip_check(coli_launch_router_logits(x_dev, 1, (const float *)rw_dev, D, E, logit, ctx->stream), "router logits") ||
+        !hip_check(coli_launch_router_select(logit, nch, (const float *)rb_dev, 1, E, Ksel, 1, topp, norm_topk, routed_scale,
                                           idx, w, keff, ctx->stream),
                 "router select") ||
-        !hip_ok(hipMemcpyAsync(ctx->host_small, idx, (size_t)Ksel * 8 + sizeof(int), hipMemcpyDeviceToHost,
+        !hip_check(hipMemcpyAsync(ctx->host_small.h, idx, (size_t)Ksel * 8 + sizeof(int), hipMemcpyDeviceToHost,
                                ctx->stream),
                 "router readback") ||
-        !hip_ok(hipStreamSynchronize(ctx->stream), "router sync"))
+        !hip_check(hipStreamSynchronize(ctx->stream), "router sync"))
         return 0;
-    const char *hb = (const char *)ctx->host_small;
+    const char *hb = (const char *)ctx->host_small.h;
     std::memcpy(idx_host, hb, (size_t)Ksel * sizeof(int));
     std::memcpy(w_host, hb + (size_t)Ksel * sizeof(int), (size_t)Ksel * sizeof(float));
     std::memcpy(keff_host, hb + (size_t)Ksel * 8, sizeof(int));
@@ -985,88 +972,88 @@ extern "C" int coli_cuda_pipe_router(int device, const float *x_dev, const void 
 // resident-pipeline primitives (c/backend_cuda.cu:2036-2135, 2317-2448)
 // ---------------------------------------------------------------------------
 extern "C" float *coli_cuda_pipe_scratch(int device, int slot, size_t bytes) {
-    DevCtx *ctx = find_ctx(device);
-    if (slot < 0 || slot >= COLI_PIPE_SLOTS || !select_ctx(ctx)) return nullptr;
+    DevCtx *ctx = ctx_of(device);
+    if (slot < 0 || slot >= COLI_PIPE_SLOTS || !bind_ctx(ctx)) return nullptr;
     if (!reserve(ctx, &ctx->pipe[slot], bytes, 0)) return nullptr;
     return (float *)ctx->pipe[slot].p;
 }
 
 extern "C" void *coli_cuda_pipe_alloc(int device, size_t bytes) {
-    DevCtx *ctx = find_ctx(device);
-    if (!select_ctx(ctx)) return nullptr;
+    DevCtx *ctx = ctx_of(device);
+    if (!bind_ctx(ctx)) return nullptr;
     void *p = nullptr;
-    if (!hip_ok(hipMalloc(&p, bytes), "pipe alloc")) return nullptr;
+    if (!hip_check(hipMalloc(&p, bytes), "pipe alloc")) return nullptr;
     return p;
 }
 
 extern "C" void coli_cuda_pipe_free(int device, void *p) {
-    DevCtx *ctx = find_ctx(device);
-    if (!p || !select_ctx(ctx)) return;
+    DevCtx *ctx = ctx_of(device);
+    if (!p || !bind_ctx(ctx)) return;
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(p);
 }
 
 extern "C" int coli_cuda_pipe_upload(int device, void *dst, const void *src, size_t bytes) {
-    DevCtx *ctx = find_ctx(device);
-    if (!select_ctx(ctx)) return 0;
-    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "pipe upload") &&
-           hip_ok(hipStreamSynchronize(ctx->stream), "pipe upload sync");
+    DevCtx *ctx = ctx_of(device);
+    if (!bind_ctx(ctx)) return 0;
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "pipe upload") &&
+           hip_check(hipStreamSynchronize(ctx->stream), "pipe upload sync");
 }
 
 extern "C" int coli_cuda_pipe_download(int device, const void *src, void *dst, size_t bytes) {
-    DevCtx *ctx = find_ctx(device);
-    if (!select_ctx(ctx)) return 0;
-    return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "pipe download") &&
-           hip_ok(hipStreamSynchronize(ctx->stream), "pipe download sync");
+    DevCtx *ctx = ctx_of(device);
+    if (!bind_ctx(ctx)) return 0;
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "pipe download") &&
+           hip_check(hipStreamSynchronize(ctx->stream), "pipe download sync");
 }
 
 extern "C" int coli_cuda_pipe_silu_mul(int device, float *gate_dev, const float *up_dev, size_t n) {
     if (fault_injected()) return 0;
-    DevCtx *ctx = find_ctx(device);
-    if (!n || !gate_dev || !up_dev || !select_ctx(ctx)) return 0;
-    return hip_ok(coli_launch_silu_mul(gate_dev, up_dev, n, ctx->stream), "pipe silu mul");
+    DevCtx *ctx = ctx_of(device);
+    if (!n || !gate_dev || !up_dev || !bind_ctx(ctx)) return 0;
+    return hip_check(coli_launch_silu_mul(gate_dev, up_dev, n, ctx->stream), "pipe silu mul");
 }
 
 extern "C" int coli_cuda_pipe_add(int device, float *x_dev, const float *t_dev, size_t n) {
     if (fault_injected()) return 0;
-    DevCtx *ctx = find_ctx(device);
-    if (!n || !x_dev || !t_dev || !select_ctx(ctx)) return 0;
-    return hip_ok(coli_launch_add_n(x_dev, t_dev, n, ctx->stream), "pipe add");
+    DevCtx *ctx = ctx_of(device);
+    if (!n || !x_dev || !t_dev || !bind_ctx(ctx)) return 0;
+    return hip_check(coli_launch_add_n(x_dev, t_dev, n, ctx->stream), "pipe add");
 }
 
 extern "C" int coli_cuda_pipe_rows_add(int device, float *x_dev, const float *partial_dev, const int *rows_dev,
                                        int nrows, int D) {
     if (fault_injected()) return 0;
-    DevCtx *ctx = find_ctx(device);
-    if (nrows < 1 || D < 1 || !x_dev || !partial_dev || !rows_dev || !select_ctx(ctx)) return 0;
-    return hip_ok(coli_launch_rows_add(x_dev, partial_dev, rows_dev, nrows, D, ctx->stream), "pipe rows add");
+    DevCtx *ctx = ctx_of(device);
+    if (nrows < 1 || D < 1 || !x_dev || !partial_dev || !rows_dev || !bind_ctx(ctx)) return 0;
+    return hip_check(coli_launch_rows_add(x_dev, partial_dev, rows_dev, nrows, D, ctx->stream), "pipe rows add");
 }
 
 extern "C" int coli_cuda_pipe_copy2d(int device, float *dst, int dpitch, const float *src, int spitch, int width,
                                      int height) {
-    DevCtx *ctx = find_ctx(device);
-    if (!select_ctx(ctx)) return 0;
-    return hip_ok(hipMemcpy2DAsync(dst, (size_t)dpitch * 4, src, (size_t)spitch * 4, (size_t)width * 4, height,
+    DevCtx *ctx = ctx_of(device);
+    if (!bind_ctx(ctx)) return 0;
+    return hip_check(hipMemcpy2DAsync(dst, (size_t)dpitch * 4, src, (size_t)spitch * 4, (size_t)width * 4, height,
                                    hipMemcpyDeviceToDevice, ctx->stream),
                   "pipe copy2d") &&
-           hip_ok(hipStreamSynchronize(ctx->stream), "pipe copy2d sync");
+           hip_check(hipStreamSynchronize(ctx->stream), "pipe copy2d sync");
 }
 
 extern "C" int coli_cuda_pipe_peer_copy(int dst_dev, float *dst, int src_dev, const float *src, size_t bytes) {
     if (!dst || !src) return 0;
     if (dst_dev == src_dev) {
-        DevCtx *c = find_ctx(dst_dev);
-        if (!select_ctx(c)) return 0;
-        return hip_ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream), "pipe intra copy") &&
-               hip_ok(hipStreamSynchronize(c->stream), "pipe intra copy sync");
+        DevCtx *c = ctx_of(dst_dev);
+        if (!bind_ctx(c)) return 0;
+        return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream), "pipe intra copy") &&
+               hip_check(hipStreamSynchronize(c->stream), "pipe intra copy sync");
     }
-    return hip_ok(hipMemcpyPeer(dst, dst_dev, src, src_dev, bytes), "pipe peer copy");
+    return hip_check(hipMemcpyPeer(dst, dst_dev, src, src_dev, bytes), "pipe peer copy");
 }
 
 extern "C" int coli_cuda_pipe_sync(int device) {
-    DevCtx *ctx = find_ctx(device);
-    if (!select_ctx(ctx)) return 0;
-    return hip_ok(hipStreamSynchronize(ctx->stream), "pipe sync") && hip_ok(hipDeviceSynchronize(), "pipe sync");
+    DevCtx *ctx = ctx_of(device);
+    if (!bind_ctx(ctx)) return 0;
+    return hip_check(hipStreamSynchronize(ctx->stream), "pipe sync") && hip_check(hipDeviceSynchronize(), "pipe sync");
 }
 
 // ---------------------------------------------------------------------------

@@ -318,9 +318,9 @@ __global__ void coli_moe_combine(const float *__restrict__ y, int D, const float
 
 extern "C" void coli_hip_moe_free(ColiHipMoe *m) {
     if (!m) return;
-    DevCtx *ctx = find_ctx(m->device);
+    DevCtx *ctx = ctx_of(m->device);
     if (ctx) {
-        select_ctx(ctx);
+        bind_ctx(ctx);
         (void)hipStreamSynchronize(ctx->stream);
     }
     void *bufs[] = {m->rw, m->rb, m->tab, m->logits, m->wsel, m->h, m->y, m->idx, m->keff, m->state,
@@ -340,8 +340,8 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
         c.route_mode > 3 || !(c.swiglu_limit >= 0.0f))
         return 0;
     if (c.has_shared && (!sg || !su || !sd)) return 0;
-    DevCtx *ctx = find_ctx(device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(device);
+    if (!bind_ctx(ctx)) return 0;
     int kind = gates[0] ? gates[0]->kind : -1;
     if (kind < 0 || kind == COLI_KIND_GENERIC) return 0;
     int n = c.E + (c.has_shared ? 1 : 0);
@@ -361,16 +361,16 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
     m->kind = kind;
     m->S_cap = 0;
     size_t rwb = (size_t)c.E * c.D * sizeof(float);
-    int ok = hip_ok(hipMalloc((void **)&m->rw, rwb), "router weights") &&
-             hip_ok(hipMemcpy(m->rw, router_w, rwb, hipMemcpyHostToDevice), "router weights upload") &&
-             hip_ok(hipMalloc((void **)&m->tab, tab.size() * sizeof(ColiProb)), "expert table") &&
-             hip_ok(hipMemcpy(m->tab, tab.data(), tab.size() * sizeof(ColiProb), hipMemcpyHostToDevice),
+    int ok = hip_check(hipMalloc((void **)&m->rw, rwb), "router weights") &&
+             hip_check(hipMemcpy(m->rw, router_w, rwb, hipMemcpyHostToDevice), "router weights upload") &&
+             hip_check(hipMalloc((void **)&m->tab, tab.size() * sizeof(ColiProb)), "expert table") &&
+             hip_check(hipMemcpy(m->tab, tab.data(), tab.size() * sizeof(ColiProb), hipMemcpyHostToDevice),
                     "expert table upload") &&
-             hip_ok(hipMalloc((void **)&m->route_cnt, sizeof(int)), "routing counter") &&
-             hip_ok(hipMemset(m->route_cnt, 0, sizeof(int)), "routing counter clear");
+             hip_check(hipMalloc((void **)&m->route_cnt, sizeof(int)), "routing counter") &&
+             hip_check(hipMemset(m->route_cnt, 0, sizeof(int)), "routing counter clear");
     if (ok && router_bias)
-        ok = hip_ok(hipMalloc((void **)&m->rb, (size_t)c.E * sizeof(float)), "router bias") &&
-             hip_ok(hipMemcpy(m->rb, router_bias, (size_t)c.E * sizeof(float), hipMemcpyHostToDevice),
+        ok = hip_check(hipMalloc((void **)&m->rb, (size_t)c.E * sizeof(float)), "router bias") &&
+             hip_check(hipMemcpy(m->rb, router_bias, (size_t)c.E * sizeof(float), hipMemcpyHostToDevice),
                     "router bias upload");
     if (!ok) {
         coli_hip_moe_free(m);
@@ -390,7 +390,7 @@ static int moe_tiles(const ColiHipMoeConfig &c, int S) {
 // Per-forward buffers for up to S rows (allocated once per growth of S).
 static int moe_reserve(DevCtx *ctx, ColiHipMoe *m, int S) {
     if (S <= m->S_cap) return 1;
-    if (!hip_ok(hipStreamSynchronize(ctx->stream), "moe reserve sync")) return 0;
+    if (!hip_check(hipStreamSynchronize(ctx->stream), "moe reserve sync")) return 0;
     const ColiHipMoeConfig &c = m->cfg;
     const int P = moe_problems(c, S), rows = moe_rows(c, S);
     void **bufs[] = {(void **)&m->logits, (void **)&m->wsel, (void **)&m->h, (void **)&m->y, (void **)&m->idx,
@@ -406,7 +406,7 @@ static int moe_reserve(DevCtx *ctx, ColiHipMoe *m, int S) {
                             (size_t)c.E * 4, (size_t)rows * 4, (size_t)S * c.K * 4, (size_t)moe_tiles(c, S) * 4,
                             (size_t)P * sizeof(ColiProb), (size_t)P * sizeof(ColiProb)};
     for (int i = 0; i < 13; i++)
-        if (!hip_ok(hipMalloc(bufs[i], sizes[i]), "moe buffers")) return 0;
+        if (!hip_check(hipMalloc(bufs[i], sizes[i]), "moe buffers")) return 0;
     m->S_cap = S;
     return 1;
 }
@@ -446,7 +446,7 @@ static int launch_route(ColiHipMoe *m, const float *x_dev, int S, hipStream_t st
     }
 #undef COLI_ROUTE_JM
 #undef COLI_ROUTE_ARGS
-    return hip_ok(hipGetLastError(), "moe routing");
+    return hip_check(hipGetLastError(), "moe routing");
 }
 
 static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
@@ -467,14 +467,14 @@ static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
     default: COLI_SU(16); break;
     }
 #undef COLI_SU
-    return hip_ok(hipGetLastError(), "moe selection + union");
+    return hip_check(hipGetLastError(), "moe selection + union");
 }
 
 extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float *out_dev, int S) {
     if (fault_injected()) return 0;
     if (!m || !x_dev || !out_dev || S < 1 || S > COLI_MOE_MAX_ROWS || S * m->cfg.K > COLI_MOE_MAX_SEL) return 0;
-    DevCtx *ctx = find_ctx(m->device);
-    if (!select_ctx(ctx) || !moe_reserve(ctx, m, S)) return 0;
+    DevCtx *ctx = ctx_of(m->device);
+    if (!bind_ctx(ctx) || !moe_reserve(ctx, m, S)) return 0;
     const ColiHipMoeConfig &c = m->cfg;
     const int P = moe_problems(c, S), rows = moe_rows(c, S);
     const int nq_d = (c.D + 127) / 128, nq_i = (c.I + 127) / 128;
@@ -497,7 +497,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
         if (!nch || !launch_select_union(m, nch, S, st)) return 0;
     } else {
         const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
-        if (!nch || !hip_ok(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
+        if (!nch || !hip_check(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
                                                       c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, st),
                             "moe router select"))
             return 0;
@@ -505,7 +505,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
         const size_t ush = (size_t)(7 * c.E + 5) * sizeof(int);
         hipLaunchKernelGGL(coli_moe_union, dim3(1), dim3(1024), ush, st, m->idx, m->keff, S, c.K, c.E, c.has_shared,
                            m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state);
-        if (!hip_ok(hipGetLastError(), "moe union")) return 0;
+        if (!hip_check(hipGetLastError(), "moe union")) return 0;
     }
     // 5. gate/up + SwiGLU over the union, 6. hidden fragments, 7. down
     const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
@@ -530,40 +530,40 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
     // 8. combine
     hipLaunchKernelGGL(coli_moe_combine, dim3((c.D + 255) / 256, S), dim3(256), 0, st, m->y, c.D, m->wsel, m->keff,
                        m->slotrow, c.K, m->state, c.has_shared, S, out_dev);
-    return hip_ok(hipGetLastError(), "moe combine");
+    return hip_check(hipGetLastError(), "moe combine");
 }
 
 extern "C" int coli_hip_moe_forward(ColiHipMoe *m, const float *x, float *out, int S, int *idx, float *w,
                                     int *keff) {
     if (!m || !x || !out || S < 1 || S > COLI_MOE_MAX_ROWS) return 0;
-    DevCtx *ctx = find_ctx(m->device);
-    if (!select_ctx(ctx)) return 0;
+    DevCtx *ctx = ctx_of(m->device);
+    if (!bind_ctx(ctx)) return 0;
     const ColiHipMoeConfig &c = m->cfg;
     size_t xb = (size_t)S * c.D * sizeof(float);
     if (!reserve(ctx, &ctx->x, xb, 0) || !reserve(ctx, &ctx->y, xb, 0) ||
-        !hip_ok(hipStreamSynchronize(ctx->stream), "moe staging") ||
-        !hip_ok(hipMemcpyAsync(ctx->x.p, x, xb, hipMemcpyHostToDevice, ctx->stream), "moe input upload") ||
+        !hip_check(hipStreamSynchronize(ctx->stream), "moe staging") ||
+        !hip_check(hipMemcpyAsync(ctx->x.p, x, xb, hipMemcpyHostToDevice, ctx->stream), "moe input upload") ||
         !coli_hip_moe_forward_dev(m, (const float *)ctx->x.p, (float *)ctx->y.p, S) ||
-        !hip_ok(hipMemcpyAsync(out, ctx->y.p, xb, hipMemcpyDeviceToHost, ctx->stream), "moe output download"))
+        !hip_check(hipMemcpyAsync(out, ctx->y.p, xb, hipMemcpyDeviceToHost, ctx->stream), "moe output download"))
         return 0;
-    if (idx && !hip_ok(hipMemcpyAsync(idx, m->idx, (size_t)S * c.K * 4, hipMemcpyDeviceToHost, ctx->stream), "idx"))
+    if (idx && !hip_check(hipMemcpyAsync(idx, m->idx, (size_t)S * c.K * 4, hipMemcpyDeviceToHost, ctx->stream), "idx"))
         return 0;
-    if (w && !hip_ok(hipMemcpyAsync(w, m->wsel, (size_t)S * c.K * 4, hipMemcpyDeviceToHost, ctx->stream), "w"))
+    if (w && !hip_check(hipMemcpyAsync(w, m->wsel, (size_t)S * c.K * 4, hipMemcpyDeviceToHost, ctx->stream), "w"))
         return 0;
-    if (keff && !hip_ok(hipMemcpyAsync(keff, m->keff, (size_t)S * 4, hipMemcpyDeviceToHost, ctx->stream), "keff"))
+    if (keff && !hip_check(hipMemcpyAsync(keff, m->keff, (size_t)S * 4, hipMemcpyDeviceToHost, ctx->stream), "keff"))
         return 0;
-    return hip_ok(hipStreamSynchronize(ctx->stream), "moe synchronize");
+    return hip_check(hipStreamSynchronize(ctx->stream), "moe synchronize");
 }
 
 extern "C" int coli_hip_moe_last_union(ColiHipMoe *m, int *nu, int *uniq) {
     if (!m || !nu || !m->state) return 0;
-    DevCtx *ctx = find_ctx(m->device);
-    if (!select_ctx(ctx) || !hip_ok(hipStreamSynchronize(ctx->stream), "union sync")) return 0;
+    DevCtx *ctx = ctx_of(m->device);
+    if (!bind_ctx(ctx) || !hip_check(hipStreamSynchronize(ctx->stream), "union sync")) return 0;
     int st[3];
-    if (!hip_ok(hipMemcpy(st, m->state, sizeof(st), hipMemcpyDeviceToHost), "union state")) return 0;
+    if (!hip_check(hipMemcpy(st, m->state, sizeof(st), hipMemcpyDeviceToHost), "union state")) return 0;
     *nu = st[2];
     if (uniq && st[2] > 0 &&
-        !hip_ok(hipMemcpy(uniq, m->uniq, (size_t)st[2] * sizeof(int), hipMemcpyDeviceToHost), "union ids"))
+        !hip_check(hipMemcpy(uniq, m->uniq, (size_t)st[2] * sizeof(int), hipMemcpyDeviceToHost), "union ids"))
         return 0;
     return 1;
 }

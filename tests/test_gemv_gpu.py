@@ -38,7 +38,7 @@ def test_int4_g32_fp16_scales(session, O, I, S):
 # The dense benchmark shapes: the up projection runs one group per
 # row block, the down projection splits K across workgroups.
 @pytest.mark.parametrize("O,I", [(14336, 4096), (4096, 14336)])
-@pytest.mark.parametrize("S", [1, 16])
+@pytest.mark.parametrize("S", [1, 4, 8, 16])
 def test_int4_dense_bench_shapes(session, O, I, S):
     rng = np.random.default_rng(O + I + S)
     q4, sc = rand_i4(rng, O, I, 32)
