@@ -624,7 +624,8 @@ extern "C" int coli_cuda_expert_group_issue(ColiCudaTensor *const *gates, ColiCu
     std::vector<Member> mem;
     int total, D, I;
     DevCtx *ctx = collect_members(gates, ups, downs, rows, count, mem, &total, &D, &I);
-    if (!ctx || ctx->group_pending) return 0;
+    // decode-scale only, as c/backend_cuda.cu:1716: larger packs take the sync call
+    if (!ctx || ctx->group_pending || total > 8) return 0;
     if (!group_stage_and_run(ctx, mem, count, total, D, I, x, nullptr)) return 0;
     ctx->group_pending = 1;
     note_group(ctx, count, total, 0, 0, 0);
