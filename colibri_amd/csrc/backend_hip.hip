@@ -21,6 +21,13 @@
 #include <vector>
 
 DevCtx g_ctx[COLI_CUDA_MAX_DEVICES];
+
+// Fixed device scratch of the allocation-free entry point
+// (coli_hip_pipe_gemm_noalloc): each device holds its own copy from module
+// load to process end. Host code never passes this name to a kernel or a
+// copy: it is a host-side stand-in; the device address comes from
+// hipGetSymbolAddress at init (DevCtx::scratch).
+static __device__ __align__(256) uint8_t scratch[COLI_NA_BYTES];
 int g_nctx;
 static std::mutex g_stats_mu;
 static uint64_t g_calls, g_experts, g_rows;
@@ -150,6 +157,14 @@ extern "C" int coli_cuda_init(const int *devices, int count) {
             g_nctx = 0;
             return 0;
         }
+        // this device's copy of the static scratch, cleared (zero block, lo
+        // flag, split-K counters must start at zero): with a fill kernel on
+        // the stream, then waited for
+        void *sp = nullptr;
+        if (hip_check(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)), "scratch symbol address") &&
+            hip_check(coli_launch_zero_i32((int *)sp, (int)(COLI_NA_BYTES / sizeof(int)), ctx->stream), "scratch clear") &&
+            hip_check(hipStreamSynchronize(ctx->stream), "scratch clear sync"))
+            ctx->scratch = (uint8_t *)sp;
         g_nctx++;
         map_device_slots();
         std::fprintf(stderr, "[HIP] device %d: %s (%s), %.1f GB HBM, %d CUs\n", device, prop.name,

@@ -9,6 +9,23 @@
 // Batches larger than this run the grouped GEMM instead of the GEMV.
 #define COLI_GEMM_MIN_ROWS 32
 
+// The static scratch array behind coli_hip_pipe_gemm_noalloc (one copy per
+// device, held until the process ends): regions and the limits they imply.
+#define COLI_NA_MAX_ROWS 16
+#define COLI_NA_MAX_K 16384
+#define COLI_NA_FRAG_BYTES ((size_t)COLI_NA_MAX_ROWS * (COLI_NA_MAX_K / 128) * 4 * 32 * 2)   // 512 KiB
+#define COLI_NA_EXP_BYTES ((size_t)4096)
+#define COLI_NA_CNT_BYTES ((size_t)64 << 10)
+#define COLI_NA_OFF_ZERO ((size_t)0)                                           // COLI_ZERO_BYTES of zeros
+#define COLI_NA_OFF_HI (COLI_NA_OFF_ZERO + COLI_ZERO_BYTES)
+#define COLI_NA_OFF_LO (COLI_NA_OFF_HI + COLI_NA_FRAG_BYTES)
+#define COLI_NA_OFF_EXP (COLI_NA_OFF_LO + COLI_NA_FRAG_BYTES)
+#define COLI_NA_OFF_FLAG (COLI_NA_OFF_EXP + COLI_NA_EXP_BYTES)                 // the lo flag (256 B slot)
+#define COLI_NA_OFF_CNT (COLI_NA_OFF_FLAG + 256)
+#define COLI_NA_OFF_PART (COLI_NA_OFF_CNT + COLI_NA_CNT_BYTES)
+#define COLI_NA_BYTES ((size_t)8 << 20)
+#define COLI_NA_PART_BYTES (COLI_NA_BYTES - COLI_NA_OFF_PART)
+
 struct DevBuf {
     void *p = nullptr;
     size_t cap = 0;
@@ -50,6 +67,10 @@ struct DevCtx {
     DevBuf pipe[COLI_PIPE_SLOTS];
     // pinned staging
     PinBuf host_x, host_y, host_prob, host_small;
+    // this device's copy of the library's static scratch array (see
+    // coli_hip_pipe_gemm_noalloc), looked up at init; null if unavailable
+    uint8_t *scratch = nullptr;
+    FragSet na_frag;                   // views into scratch (no allocations)
     int group_pending = 0;
     void *blas = nullptr;              // rocblas_handle, created on first use
     hipEvent_t ev_done = nullptr;
@@ -133,11 +154,25 @@ int frag_set_of(int kind, bool hidden);
 bool mx_gemm_enabled();
 int make_frags8(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, const int *src_rows = nullptr,
                 const int *nrows_dev = nullptr);
+// Fixed buffers a GEMV launch may use in place of the context's grow-only
+// scratch (the allocation-free entry point): the fragment set (hi / lo / exp
+// with their capacities), its lo flag, the zero block, and the split-K
+// partials and arrival counters.
+struct GemvScratch {
+    FragSet *frag;
+    int *flag;
+    const void *zero;
+    float *partial;
+    size_t partial_bytes;
+    int *split_cnt;
+    size_t split_cnt_n;
+};
 // One tiled GEMV over `nprob` problems (descriptors on the device, or one
-// inline problem) reading fragment set `set`.
+// inline problem) reading fragment set `set` (or ws's buffers, allocating
+// nothing, when ws is given).
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
-             const ColiProb *inline_prob = nullptr, float swiglu_limit = 0.0f);
+             const ColiProb *inline_prob = nullptr, float swiglu_limit = 0.0f, const GemvScratch *ws = nullptr);
 // One grouped GEMM over a device work list of (problem << 16 | 64-row tile).
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,

@@ -133,9 +133,8 @@ static bool plan_dma(const DevCtx *ctx, GemvLaunchPlan &p, int kind, int nprob, 
 static int ngp_of(int K) { return (K + 127) / 128 * 4; }
 
 // Fragments of rows x[0..nrows) (or src_rows[r]) of width K into set `set`.
-int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
-               const int *src_rows, const int *nrows_dev) {
-    FragSet &f = ctx->frag[set];
+static int record_frags(FragSet &f, const float *x, int ld, int nrows, int K, int int4_order, const int *src_rows,
+                        const int *nrows_dev) {
     if (!x || nrows < 0 || K < 1 || ld < K) return 0;
     f.pending = true;
     f.px = x;
@@ -148,8 +147,14 @@ int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, i
     return 1;
 }
 
-int flush_frags(DevCtx *ctx, int set) {
-    FragSet &f = ctx->frag[set];
+int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
+               const int *src_rows, const int *nrows_dev) {
+    return record_frags(ctx->frag[set], x, ld, nrows, K, int4_order, src_rows, nrows_dev);
+}
+
+// Build the pending fragments of f. ws == null: grow-only context buffers;
+// else the caller's fixed buffers (capacity checked, nothing allocated).
+static int flush_frags_into(DevCtx *ctx, FragSet &f, int *flag, const void *zero, const GemvScratch *ws) {
     if (!f.pending) return 1;
     f.pending = false;
     const float *x = f.px;
@@ -157,16 +162,22 @@ int flush_frags(DevCtx *ctx, int set) {
     const int *src_rows = f.psrc, *nrows_dev = f.pnrows_dev;
     int ngp = ngp_of(K);
     size_t halves = (size_t)nrows * ngp * 32;
-    if (!reserve(ctx, &f.hi, halves * 2, 0) || !reserve(ctx, &f.lo, halves * 2, 0) ||
-        !reserve(ctx, &f.exp, (size_t)nrows * sizeof(int), 0))
+    if (ws) {
+        if (halves * 2 > f.hi.cap || halves * 2 > f.lo.cap || (size_t)nrows * sizeof(int) > f.exp.cap) return 0;
+    } else if (!reserve(ctx, &f.hi, halves * 2, 0) || !reserve(ctx, &f.lo, halves * 2, 0) ||
+               !reserve(ctx, &f.exp, (size_t)nrows * sizeof(int), 0)) {
         return 0;
-    int *flag = (int *)ctx->flags.p + set;
+    }
     f.gen = f.gen == 0x7fffffff ? 1 : f.gen + 1;
     if (f.gen == 1 && !hip_check(coli_launch_zero_i32(flag, 1, ctx->stream), "fragment flag")) return 0;
     return hip_check(coli_launch_prep_frag(x, ld, src_rows, nrows_dev, nrows, K, ngp, int4_order,
                                         (_Float16 *)f.hi.p, (_Float16 *)f.lo.p, (int *)f.exp.p, flag, f.gen,
-                                        ctx->zeros.p, ctx->stream),
+                                        zero, ctx->stream),
                   "fragment prep");
+}
+
+int flush_frags(DevCtx *ctx, int set) {
+    return flush_frags_into(ctx, ctx->frag[set], (int *)ctx->flags.p + set, ctx->zeros.p, nullptr);
 }
 
 // Many-row MXFP4 problems run the exact fp16-MFMA grouped GEMM by default.
@@ -210,16 +221,28 @@ static bool xstage_enabled() {
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
-             const ColiProb *inline_prob, float swiglu_limit) {
+             const ColiProb *inline_prob, float swiglu_limit, const GemvScratch *ws) {
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
     GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
     plan_dma(ctx, pl, kind, nprob, n_bt, nrt, nq, dual, max_rows);
     size_t inst = (size_t)nprob * n_bt * pl.rbpp;
-    if (pl.splits > 1 && (!reserve(ctx, &ctx->partial, inst * pl.splits * pl.R * 4 * 64 * sizeof(float), 0) ||
-                          !reserve(ctx, &ctx->split_cnt, inst * sizeof(int), 1)))
-        return 0;
-    FragSet &f = ctx->frag[set];
+    const size_t part_bytes = inst * pl.splits * pl.R * 4 * 64 * sizeof(float);
+    if (pl.splits > 1) {
+        if (ws) {
+            if (part_bytes > ws->partial_bytes || inst > ws->split_cnt_n) {
+                std::fprintf(stderr, "[HIP] gemv: split-K scratch of %zu B / %zu counters exceeds the fixed buffer\n",
+                             part_bytes, inst);
+                return 0;
+            }
+        } else if (!reserve(ctx, &ctx->partial, part_bytes, 0) ||
+                   !reserve(ctx, &ctx->split_cnt, inst * sizeof(int), 1)) {
+            return 0;
+        }
+    }
+    FragSet &f = ws ? *ws->frag : ctx->frag[set];
+    int *flag = ws ? ws->flag : (int *)ctx->flags.p + set;
+    const void *zero = ws ? ws->zero : ctx->zeros.p;
     ColiGemvArgs a;
     std::memset(&a, 0, sizeof(a));
     // Up to 32768 activations (rows x K) on the LDS-ring kernel are read as
@@ -241,7 +264,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
         if (max_rows <= 1 && inline_prob && xstage_enabled() &&
             (long)pl.W * pl.PD * dma_slot_bytes(kind, pl.R, max_rows) + (long)nq * 516 <= 160 * 1024)
             a.xstage = 1;
-    } else if (!flush_frags(ctx, set)) {
+    } else if (!flush_frags_into(ctx, f, flag, zero, ws)) {
         return 0;
     }
     // ring depth override (tuning; deeper rings measured slower: fewer
@@ -273,14 +296,14 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.xlo = (const _Float16 *)f.lo.p;
     a.xstride = nq * 4 * 32;
     a.xexp = (const int *)f.exp.p;
-    a.haslo = (const int *)ctx->flags.p + set;
+    a.haslo = flag;
     a.lo_gen = f.gen;
-    a.zero = (const _Float16 *)ctx->zeros.p;
+    a.zero = (const _Float16 *)zero;
     a.out = out;
     a.ldo = ldo;
     a.swiglu_limit = swiglu_limit;
-    a.partial = (float *)ctx->partial.p;
-    a.split_cnt = (int *)ctx->split_cnt.p;
+    a.partial = ws ? ws->partial : (float *)ctx->partial.p;
+    a.split_cnt = ws ? ws->split_cnt : (int *)ctx->split_cnt.p;
     if (pl.dma) return hip_check(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.W, pl.PD, max_rows, ctx->stream),
                               "gemv launch");
     return hip_check(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
@@ -836,6 +859,44 @@ extern "C" int coli_cuda_pipe_gemm(ColiCudaTensor *t, float *y_dev, const float 
     DevCtx *ctx = ctx_of(t->device);
     if (!bind_ctx(ctx)) return 0;
     return gemm_dev(ctx, t, y_dev, x_dev, S);
+}
+
+// coli_cuda_pipe_gemm without any allocation: every buffer the launch needs
+// beyond x and y (activation fragments, their lo flag, the zero block,
+// split-K partials and arrival counters) lives in the library's static
+// scratch array, whose per-device address the init call looked up. The
+// decomposition is pipe_gemm's, so the results are bitwise equal.
+extern "C" int coli_hip_pipe_gemm_noalloc(ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
+    if (fault_injected()) return 0;
+    if (!t || S < 1 || !y_dev || !x_dev || !tensor_computable(t)) return 0;
+    if (S > COLI_NA_MAX_ROWS || t->I > COLI_NA_MAX_K) {
+        std::fprintf(stderr, "[HIP] pipe_gemm_noalloc: %d rows x I = %d exceed the fixed scratch (rows <= %d, I <= %d)\n",
+                     S, t->I, COLI_NA_MAX_ROWS, COLI_NA_MAX_K);
+        return 0;
+    }
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx) || !ctx->scratch) return 0;
+    if (t->kind == COLI_KIND_GENERIC)
+        return hip_check(coli_launch_generic_i4(t, x_dev, t->I, y_dev, t->O, S, ctx->stream), "generic gemv");
+    uint8_t *sc = ctx->scratch;
+    FragSet &f = ctx->na_frag;
+    f.hi.p = sc + COLI_NA_OFF_HI;
+    f.hi.cap = COLI_NA_FRAG_BYTES;
+    f.lo.p = sc + COLI_NA_OFF_LO;
+    f.lo.cap = COLI_NA_FRAG_BYTES;
+    f.exp.p = sc + COLI_NA_OFF_EXP;
+    f.exp.cap = COLI_NA_EXP_BYTES;
+    if (!record_frags(f, x_dev, t->I, S, t->I, t->kind != COLI_KIND_FP4, nullptr, nullptr)) return 0;
+    const GemvScratch ws = {&f,
+                            (int *)(sc + COLI_NA_OFF_FLAG),
+                            sc + COLI_NA_OFF_ZERO,
+                            (float *)(sc + COLI_NA_OFF_PART),
+                            COLI_NA_PART_BYTES,
+                            (int *)(sc + COLI_NA_OFF_CNT),
+                            COLI_NA_CNT_BYTES / sizeof(int)};
+    const ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
+    return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, frag_set_of(t->kind, false),
+                    nullptr, y_dev, t->O, &p, 0.0f, &ws);
 }
 
 // ---------------------------------------------------------------------------

@@ -102,6 +102,17 @@ int coli_hip_moe_forward(ColiHipMoe *moe, const float *x, float *out, int S, int
  * (c/colibri.c:4146-4152). Synchronizes. */
 int coli_hip_moe_last_union(ColiHipMoe *moe, int *nu, int *uniq);
 
+/* coli_cuda_pipe_gemm (device pointers, asynchronous on the backend stream)
+ * that allocates nothing. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Every buffer beyond x and
+ * y lives in one static 8 MiB device array per GPU, held until the process
+ * ends. Limits: S <= 16 rows and I <= 16384 (larger calls return 0 with a
+ * diagnostic); results are bitwise those of coli_cuda_pipe_gemm. All calls on
+ * one GPU share that array: calls that overlap on one GPU (other host
+ * threads, other streams) race. Returns 1 / 0. */
+int coli_hip_pipe_gemm_noalloc(ColiCudaTensor *tensor, float *y_dev, const float *x_dev, int S);
+
 /* ---- plumbing for benchmarks and tests ----------------------------------- */
 /* coli_cuda_pipe_gemm in two halves, so a timer can bracket the GEMV kernel
  * alone: prep names the activations x_dev[S, I] for the tensor's storage
