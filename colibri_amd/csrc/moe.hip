@@ -204,6 +204,82 @@ __device__ __forceinline__ void moe_union_body(const int *idx, const int *keff, 
     }
 }
 
+// The union of at most 64 selections (S * K <= 64, decode) by one wave, no
+// LDS and no barrier: lane i holds selection i = (t, kk). Same results as
+// moe_union_body: first-seen order of the experts, each expert's rows packed
+// in selection order, the shared expert's rows last, the GEMM tile list.
+__device__ __forceinline__ void moe_union_wave(const int *idx, const int *keff, int S, int K, int E, int has_shared,
+                                               const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
+                                               ColiProb *__restrict__ pdown, int *__restrict__ uniq,
+                                               int *__restrict__ xrows, int *__restrict__ slotrow,
+                                               int *__restrict__ mt, int *__restrict__ state, int lane) {
+    const int n = S * K;
+    const int t = lane / K, kk = lane - t * K;
+    int e = -1;
+    if (lane < n) {
+        const int ei = idx[lane];
+        if (kk < keff[t] && ei >= 0 && ei < E) e = ei;
+    }
+    // per lane: same-expert selections before it, in total, and the first one
+    int before = 0, total = 0, firstl = lane;
+    for (int j = 0; j < n; j++) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        const bool same = ej == e && e >= 0;
+        before += same && j < lane ? 1 : 0;
+        total += same ? 1 : 0;
+        if (same && j < firstl) firstl = j;
+    }
+    const bool first = e >= 0 && before == 0;
+    const unsigned long long fm = __builtin_amdgcn_ballot_w64(first);
+    const int rank = __popcll(fm & ((1ull << lane) - 1ull));   // valid on first lanes
+    const int nu = __popcll(fm);
+    // packed offset of each expert's list: exclusive prefix of the counts in
+    // first-seen (lane) order
+    int c = first ? total : 0, inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(inc, o);
+        if (lane >= o) inc += y;
+    }
+    const int off = inc - c;                                    // valid on first lanes
+    const int rows_routed = __shfl(inc, 63);
+    const int my_off = __shfl(off, firstl);
+    if (e >= 0) {
+        const int row = my_off + before;
+        xrows[row] = t;
+        slotrow[lane] = row;
+    }
+    if (first) {
+        uniq[rank] = e;
+        ColiProb d = tab[2 * e], dn = tab[2 * e + 1];
+        d.nrows = dn.nrows = total;
+        d.xrow_off = dn.xrow_off = off;
+        d.out_row0 = dn.out_row0 = off;
+        pdual[rank] = d;
+        pdown[rank] = dn;
+        mt[rank] = rank << 16;   // one 64-row tile per expert (total <= S <= 64)
+    }
+    const int np = nu + (has_shared ? 1 : 0);
+    if (has_shared) {
+        if (lane < S) xrows[rows_routed + lane] = lane;
+        if (lane == 0) {
+            ColiProb d = tab[2 * E], dn = tab[2 * E + 1];
+            d.nrows = dn.nrows = S;
+            d.xrow_off = dn.xrow_off = rows_routed;
+            d.out_row0 = dn.out_row0 = rows_routed;
+            pdual[nu] = d;
+            pdown[nu] = dn;
+            mt[nu] = nu << 16;
+        }
+    }
+    if (lane == 0) {
+        state[0] = np;
+        state[1] = rows_routed + (has_shared ? S : 0);
+        state[2] = nu;
+        state[3] = np;
+    }
+}
+
 __global__ __launch_bounds__(1024) void coli_moe_union(const int *__restrict__ idx, const int *__restrict__ keff,
                                                        int S, int K, int E, int has_shared,
                                                        const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
@@ -239,22 +315,32 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
     int *sidx = sm, *skeff = sm + S * K, *work = skeff + S;
     select_row<JM, true, false>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
                                 (float *)work + (size_t)wave * E, blockIdx.x * 4 + wave, lane, sidx, skeff);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = old == (int)gridDim.x - 1;
-        if (s_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (gridDim.x > 1) {
+        // publish, count; only the last workgroup goes on
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = old == (int)gridDim.x - 1;
+            if (s_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        // the other workgroups' rows (this one's are in LDS already)
+        const int own0 = blockIdx.x * 4, own1 = min(S, own0 + 4);
+        for (int i = threadIdx.x; i < S * K; i += blockDim.x)
+            if (i / K < own0 || i / K >= own1)
+                sidx[i] = __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int t = threadIdx.x; t < S; t += blockDim.x)
+            if (t < own0 || t >= own1)
+                skeff[t] = __hip_atomic_load(keff + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!s_last) return;
-    // the other workgroups' rows (this one's are in LDS already)
-    const int own0 = blockIdx.x * 4, own1 = min(S, own0 + 4);
-    for (int i = threadIdx.x; i < S * K; i += blockDim.x)
-        if (i / K < own0 || i / K >= own1) sidx[i] = __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int t = threadIdx.x; t < S; t += blockDim.x)
-        if (t < own0 || t >= own1) skeff[t] = __hip_atomic_load(keff + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
+    if (S * K <= 64) {   // decode: the one-wave union
+        if (wave == 0) moe_union_wave(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt,
+                                      state, lane);
+        return;
+    }
     moe_union_body(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, work);
 }
 
@@ -300,6 +386,11 @@ __global__ __launch_bounds__(256) void coli_moe_route(const float *__restrict__ 
         select_row<JM, true>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
                              (float *)work + (size_t)wave * E, s, lane, sidx, skeff);
     __syncthreads();
+    if (S * K <= 64) {
+        if (wave == 0) moe_union_wave(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt,
+                                      state, lane);
+        return;
+    }
     moe_union_body(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, work);
 }
 
@@ -309,10 +400,27 @@ __global__ void coli_moe_combine(const float *__restrict__ y, int D, const float
                                  const int *__restrict__ state, int has_shared, int S, float *__restrict__ out) {
     int t = blockIdx.y, d = blockIdx.x * blockDim.x + threadIdx.x;
     if (d >= D) return;
+    // keff, the weights, the slot rows and the shared row's position are
+    // loaded together, then the expert outputs: two memory round trips
+    const int ke = keff[t];
+    const int shared_row = has_shared ? state[1] - S + t : 0;
     float acc = 0.0f;
-    int ke = keff[t];
-    for (int kk = 0; kk < ke; kk++) acc = fmaf(w[t * K + kk], y[(size_t)slotrow[t * K + kk] * D + d], acc);
-    if (has_shared) acc += y[((size_t)state[1] - S + t) * D + d];
+    for (int kk0 = 0; kk0 < K; kk0 += 8) {
+        float wv[8], yv[8];
+        int sr[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int kk = kk0 + u;
+            wv[u] = kk < K ? w[t * K + kk] : 0.0f;
+            sr[u] = kk < K ? slotrow[t * K + kk] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) yv[u] = kk0 + u < ke ? y[(size_t)sr[u] * D + d] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (kk0 + u < ke) acc = fmaf(wv[u], yv[u], acc);
+    }
+    if (has_shared) acc += y[(size_t)shared_row * D + d];
     out[(size_t)t * D + d] = acc;
 }
 
