@@ -341,29 +341,91 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
     }
     nvalid = wave_sum_i(nvalid);
     const int want = nvalid < K ? nvalid : K;
-    // K rounds of a wave-wide argmax (largest key, then lowest expert index):
-    // round kk yields the expert of rank kk (and its weight source), which its
-    // owner lane then retires; lane kk keeps slot kk.
+    // The selection is the order of (key desc, expert index asc): round kk
+    // of the reference's argmax picks the entry of rank kk. my_e / my_w end
+    // in lane kk for slot kk.
     int my_e = 0;
     float my_w = 0.0f;
-    for (int kk = 0; kk < want; kk++) {
-        unsigned bk = 0;
-        int be = 0x7fffffff;
-        float bw = 0.0f;
+    if (JM * K <= 64) {
+        // Ranks by comparison instead of K serial rounds. Entries are ordered
+        // by c = key << 32 | ~index (a larger c ranks first; keys are unique
+        // per index, so c is a strict total order). Stage 1 ranks each lane's
+        // entry of register group j among the 64 of that group (the group
+        // broadcast through LDS); the top K of every group are candidates
+        // (the overall top K lies among them); stage 2 ranks the JM * K
+        // candidates, one per lane.
+        __shared__ __attribute__((aligned(16))) unsigned long long rk_c[4][64], rk_sel[4][64];
+        const int wv = (threadIdx.x >> 6) & 3;
+        unsigned long long *cb = rk_c[wv], *sel = rk_sel[wv];
+        int ncand = 0;
 #pragma unroll
-        for (int j = 0; j < JM; j++)
-            if (key[j] > bk) {   // strict: the lower index (smaller j) wins a tie
-                bk = key[j];
-                be = lane + 64 * j;
-                bw = pv[j];
+        for (int j = 0; j < JM; j++) {
+            if (j < jmax) {   // wave-uniform
+            const int e = lane + 64 * j;
+            const unsigned long long c =
+                key[j] ? ((unsigned long long)key[j] << 32) | (0xFFFFFFFFu - (unsigned)e) : 0ull;
+            cb[lane] = c;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            // all 64 entries read before the first comparison (32 reads of
+            // two entries in flight together)
+            unsigned long long v[64];
+#pragma unroll
+            for (int i = 0; i < 64; i += 2) {
+                const ulonglong2 t2 = *(const ulonglong2 *)(cb + i);
+                v[i] = t2.x;
+                v[i + 1] = t2.y;
             }
-        wave_argmax(bk, be, bw);
+            int r = 0;
 #pragma unroll
-        for (int j = 0; j < JM; j++)
-            if (lane + 64 * j == be) key[j] = 0;
-        if (lane == kk) {
-            my_e = be;
-            my_w = bw;
+            for (int i = 0; i < 64; i++) r += v[i] > c;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const int nj = min(K, wave_sum_i(c != 0ull ? 1 : 0));   // valid entries of the group, capped
+            if (c != 0ull && r < K) sel[ncand + r] = c;
+            ncand += nj;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        unsigned long long c = lane < ncand ? sel[lane] : 0ull;
+        if (JM > 1) {
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            int r = 0;
+#pragma unroll
+            for (int i = 0; i < 64; i += 2) {
+                const ulonglong2 t2 = *(const ulonglong2 *)(sel + i);
+                r += (i < ncand && t2.x > c) + (i + 1 < ncand && t2.y > c);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            if (lane < ncand && r < K) cb[r] = c;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            c = lane < want ? cb[lane] : 0ull;
+        }
+        if (lane < want) {
+            my_e = (int)(0xFFFFFFFFu - (unsigned)(c & 0xFFFFFFFFull));
+            my_w = p[my_e];
+        }
+    } else {
+        // K rounds of a wave-wide argmax (largest key, then lowest expert
+        // index): round kk yields the expert of rank kk (and its weight
+        // source), which its owner lane then retires; lane kk keeps slot kk.
+        for (int kk = 0; kk < want; kk++) {
+            unsigned bk = 0;
+            int be = 0x7fffffff;
+            float bw = 0.0f;
+#pragma unroll
+            for (int j = 0; j < JM; j++)
+                if (key[j] > bk) {   // strict: the lower index (smaller j) wins a tie
+                    bk = key[j];
+                    be = lane + 64 * j;
+                    bw = pv[j];
+                }
+            wave_argmax(bk, be, bw);
+#pragma unroll
+            for (int j = 0; j < JM; j++)
+                if (lane + 64 * j == be) key[j] = 0;
+            if (lane == kk) {
+                my_e = be;
+                my_w = bw;
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // p[] written by all lanes

@@ -204,6 +204,10 @@ __device__ __forceinline__ void moe_union_body(const int *idx, const int *keff, 
     }
 }
 
+// ints of the selection / union work area (LDS) of E experts; the decode
+// kernels keep the descriptor templates [2 (E + 1)] after it
+__host__ __device__ inline int moe_work_ints(int E) { return 4 * E > 7 * E + 5 ? 4 * E : 7 * E + 5; }
+
 // The union of at most 64 selections (S * K <= 64, decode) by one wave, no
 // LDS and no barrier: lane i holds selection i = (t, kk). Same results as
 // moe_union_body: first-seen order of the experts, each expert's rows packed
@@ -220,6 +224,11 @@ __device__ __forceinline__ void moe_union_wave(const int *idx, const int *keff, 
         const int ei = idx[lane];
         if (kk < keff[t] && ei >= 0 && ei < E) e = ei;
     }
+    // the descriptor templates are requested first: their latency overlaps
+    // the scans below
+    const int et = e >= 0 ? e : 0;
+    ColiProb d = tab[2 * et], dn = tab[2 * et + 1];
+    ColiProb sd = tab[2 * E], sdn = tab[2 * E + 1];   // the shared expert's row (E + 1 templates exist)
     // per lane: same-expert selections before it, in total, and the first one
     int before = 0, total = 0, firstl = lane;
     for (int j = 0; j < n; j++) {
@@ -251,7 +260,6 @@ __device__ __forceinline__ void moe_union_wave(const int *idx, const int *keff, 
     }
     if (first) {
         uniq[rank] = e;
-        ColiProb d = tab[2 * e], dn = tab[2 * e + 1];
         d.nrows = dn.nrows = total;
         d.xrow_off = dn.xrow_off = off;
         d.out_row0 = dn.out_row0 = off;
@@ -263,12 +271,11 @@ __device__ __forceinline__ void moe_union_wave(const int *idx, const int *keff, 
     if (has_shared) {
         if (lane < S) xrows[rows_routed + lane] = lane;
         if (lane == 0) {
-            ColiProb d = tab[2 * E], dn = tab[2 * E + 1];
-            d.nrows = dn.nrows = S;
-            d.xrow_off = dn.xrow_off = rows_routed;
-            d.out_row0 = dn.out_row0 = rows_routed;
-            pdual[nu] = d;
-            pdown[nu] = dn;
+            sd.nrows = sdn.nrows = S;
+            sd.xrow_off = sdn.xrow_off = rows_routed;
+            sd.out_row0 = sdn.out_row0 = rows_routed;
+            pdual[nu] = sd;
+            pdown[nu] = sdn;
             mt[nu] = nu << 16;
         }
     }
@@ -313,6 +320,11 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // LDS: slots [S K] | keff [S] | selection weights [4 E] floats, then the union's (7 E + 5) ints
     int *sidx = sm, *skeff = sm + S * K, *work = skeff + S;
+    // decode: the descriptor templates go to LDS while the selection runs
+    const bool small = S * K <= 64 && gridDim.x == 1;
+    ColiProb *stab = (ColiProb *)(((uintptr_t)(work + moe_work_ints(E)) + 15) & ~(uintptr_t)15);
+    if (small)
+        for (int i = threadIdx.x; i < 2 * (E + 1); i += blockDim.x) stab[i] = tab[i];
     select_row<JM, true, false>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
                                 (float *)work + (size_t)wave * E, blockIdx.x * 4 + wave, lane, sidx, skeff);
     if (gridDim.x > 1) {
@@ -337,8 +349,8 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
     }
     __syncthreads();
     if (S * K <= 64) {   // decode: the one-wave union
-        if (wave == 0) moe_union_wave(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt,
-                                      state, lane);
+        if (wave == 0) moe_union_wave(sidx, skeff, S, K, E, has_shared, small ? stab : tab, pdual, pdown, uniq, xrows,
+                                      slotrow, mt, state, lane);
         return;
     }
     moe_union_body(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, work);
@@ -382,12 +394,16 @@ __global__ __launch_bounds__(256) void coli_moe_route(const float *__restrict__ 
     if (!s_last) return;
     // LDS: slots [S K] | keff [S] | selection weights [4 E] floats, then the union's (7 E + 5) ints
     int *sidx = sm, *skeff = sm + S * K, *work = skeff + S;
+    // decode: the descriptor templates go to LDS while the selection runs
+    ColiProb *stab = (ColiProb *)(((uintptr_t)(work + moe_work_ints(E)) + 15) & ~(uintptr_t)15);
+    if (S * K <= 64)
+        for (int i = threadIdx.x; i < 2 * (E + 1); i += blockDim.x) stab[i] = tab[i];
     for (int s = wave; s < S; s += 4)
         select_row<JM, true>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
                              (float *)work + (size_t)wave * E, s, lane, sidx, skeff);
     __syncthreads();
     if (S * K <= 64) {
-        if (wave == 0) moe_union_wave(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt,
+        if (wave == 0) moe_union_wave(sidx, skeff, S, K, E, has_shared, stab, pdual, pdown, uniq, xrows, slotrow, mt,
                                       state, lane);
         return;
     }
@@ -529,7 +545,7 @@ static bool fused_route_disabled() {
 static int launch_route(ColiHipMoe *m, const float *x_dev, int S, hipStream_t st) {
     const ColiHipMoeConfig &c = m->cfg;
     const int nch = coli_router_chunks(c.D), neb = (c.E + 3) / 4;
-    const size_t work = std::max((size_t)4 * c.E * sizeof(float), (size_t)(7 * c.E + 5) * sizeof(int));
+    const size_t work = (size_t)moe_work_ints(c.E) * sizeof(int) + 16 + (size_t)2 * (c.E + 1) * sizeof(ColiProb);
     const size_t shm = (size_t)(S * c.K + S) * sizeof(int) + work;
     const int jm = c.E <= 64 ? 1 : c.E <= 128 ? 2 : c.E <= 256 ? 4 : c.E <= 512 ? 8 : 16;
     const dim3 grid((unsigned)(neb * nch)), block(256);
@@ -559,7 +575,7 @@ static int launch_route(ColiHipMoe *m, const float *x_dev, int S, hipStream_t st
 
 static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
     const ColiHipMoeConfig &c = m->cfg;
-    const size_t work = std::max((size_t)4 * c.E * sizeof(float), (size_t)(7 * c.E + 5) * sizeof(int));
+    const size_t work = (size_t)moe_work_ints(c.E) * sizeof(int) + 16 + (size_t)2 * (c.E + 1) * sizeof(ColiProb);
     const size_t shm = (size_t)(S * c.K + S) * sizeof(int) + work;
     const int jm = c.E <= 64 ? 1 : c.E <= 128 ? 2 : c.E <= 256 ? 4 : c.E <= 512 ? 8 : 16;
     const dim3 grid((unsigned)((S + 3) / 4)), block(256);
