@@ -10,8 +10,6 @@
 #include "coli_hip_ext.h"
 #include "coli_hip_host.h"
 
-#include <rocblas/rocblas.h>
-
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -194,7 +192,6 @@ extern "C" void coli_cuda_shutdown(void) {
         if (ctx->host_prob.h) (void)hipHostFree(ctx->host_prob.h);
         if (ctx->host_small.h) (void)hipHostFree(ctx->host_small.h);
         if (ctx->ev_ok) (void)hipEventDestroy(ctx->ev_done);
-        if (ctx->blas) (void)rocblas_destroy_handle((rocblas_handle)ctx->blas);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         *ctx = DevCtx();
     }

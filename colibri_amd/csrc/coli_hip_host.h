@@ -72,7 +72,6 @@ struct DevCtx {
     uint8_t *scratch = nullptr;
     FragSet na_frag;                   // views into scratch (no allocations)
     int group_pending = 0;
-    void *blas = nullptr;              // rocblas_handle, created on first use
     hipEvent_t ev_done = nullptr;
     int ev_ok = 0;
     // statistics
@@ -116,6 +115,7 @@ hipError_t coli_launch_qdq_i8(const float *x, float *y, int S, int K, hipStream_
 int coli_router_chunks(int D);   // column chunks of the router partials
 hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E, float *part,
                                      hipStream_t st);
+hipError_t coli_launch_router_gemm(const float *x, int S, const float *W, int D, int E, float *part, hipStream_t st);
 hipError_t coli_launch_router_select(const float *part, int nch, const float *bias, int S, int E, int K, int mode,
                                      float topp, int norm_topk, float routed_scale, int *idx, float *w,
                                      int *keff, hipStream_t st);
@@ -179,6 +179,5 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
              const int *xrows_dev, float *out, int ldo, float swiglu_limit = 0.0f);
 
 // Router logits of S rows into `part`; returns the number of column-chunk
-// partials the selection must add (1 when the batch went through one GEMM),
-// or 0 on failure.
+// partials the selection must add, or 0 on failure.
 int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int E, float *part);

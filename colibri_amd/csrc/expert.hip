@@ -8,7 +8,6 @@
 // 1677-1812 for issue/take).
 #include "coli_hip_host.h"
 
-#include <rocblas/rocblas.h>
 
 #include "coli_backend_abi.h"
 #include "coli_hip_ext.h"
@@ -973,26 +972,11 @@ extern "C" int coli_cuda_expert_group_resident_take(int home_device, const int *
 // x^T... i.e. op(A) = A^T with A = W as a D x E col-major matrix).
 // ---------------------------------------------------------------------------
 int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int E, float *part) {
-    if (S <= 64)
-        return hip_check(coli_launch_router_logits(x, S, W, D, E, part, ctx->stream), "router logits")
-                   ? coli_router_chunks(D)
-                   : 0;
-    rocblas_handle h = (rocblas_handle)ctx->blas;
-    if (!h) {
-        if (rocblas_create_handle(&h) != rocblas_status_success) {
-            std::fprintf(stderr, "[HIP] rocblas handle creation failed\n");
-            return 0;
-        }
-        ctx->blas = h;
-    }
-    const float one = 1.0f, zero = 0.0f;
-    if (rocblas_set_stream(h, ctx->stream) != rocblas_status_success ||
-        rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, E, S, D, &one, W, D, x, D, &zero, part,
-                      E) != rocblas_status_success) {
-        std::fprintf(stderr, "[HIP] router sgemm failed\n");
-        return 0;
-    }
-    return 1;
+    // up to 64 rows: the GEMV-shaped partial kernel (passes of 16 rows);
+    // beyond: the MFMA f32 GEMM (pipe.hip). Both leave the same chunk partials.
+    const hipError_t err = S <= 64 ? coli_launch_router_logits(x, S, W, D, E, part, ctx->stream)
+                                   : coli_launch_router_gemm(x, S, W, D, E, part, ctx->stream);
+    return hip_check(err, "router logits") ? coli_router_chunks(D) : 0;
 }
 
 // ---------------------------------------------------------------------------

@@ -82,6 +82,94 @@ __global__ __launch_bounds__(256) void coli_router_partial(const float *__restri
 
 extern "C" int coli_router_chunks(int D) { return (D + COLI_ROUTER_CHUNK - 1) / COLI_ROUTER_CHUNK; }
 
+// Router logits of many rows (prefill): part[ch][s][e] = sum over the chunk's
+// columns of x[s, d] * W[e, d], an f32 GEMM on v_mfma_f32_16x16x4_f32. A
+// 256-thread workgroup computes a 64-row x 64-expert tile over one 512-column
+// chunk (the same chunk partials the selection adds in chunk order); each wave
+// owns a 32 x 32 quarter (2 x 2 MFMA blocks). Steps of 32 columns are staged
+// in LDS with a row pitch of 33 floats, so the sixteen rows one MFMA operand
+// read touches sit in sixteen different banks.
+#define COLI_RG_BM 64
+#define COLI_RG_BK 32
+__global__ __launch_bounds__(256) void coli_router_gemm(const float *__restrict__ x, int S,
+                                                        const float *__restrict__ W, int D, int E,
+                                                        float *__restrict__ part) {
+    __shared__ float xs[COLI_RG_BM][COLI_RG_BK + 1], ws[COLI_RG_BM][COLI_RG_BK + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int s0 = blockIdx.x * COLI_RG_BM, e0 = blockIdx.y * COLI_RG_BM, ch = blockIdx.z;
+    const int d_begin = ch * COLI_ROUTER_CHUNK, d_end = min(D, d_begin + COLI_ROUTER_CHUNK);
+    const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;   // the wave's quarter
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) acc[a][b] = (floatx4){0.f, 0.f, 0.f, 0.f};
+    const bool vec = (D & 3) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)W & 15) == 0;
+    for (int d0 = d_begin; d0 < d_end; d0 += COLI_RG_BK) {
+        // stage 64 rows x 32 columns of x and of W: thread t loads float4 t and t + 256
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int f = threadIdx.x + 256 * h, r = f >> 3, c = (f & 7) * 4;
+            const int d = d0 + c;
+            float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = xv;
+            if (vec && d + 4 <= d_end) {
+                if (s0 + r < S) xv = *(const float4 *)(x + (size_t)(s0 + r) * D + d);
+                if (e0 + r < E) wv = *(const float4 *)(W + (size_t)(e0 + r) * D + d);
+            } else {
+                float xa[4] = {0.f, 0.f, 0.f, 0.f}, wa[4] = {0.f, 0.f, 0.f, 0.f};
+                for (int u = 0; u < 4; u++) {
+                    if (d + u < d_end) {
+                        if (s0 + r < S) xa[u] = x[(size_t)(s0 + r) * D + d + u];
+                        if (e0 + r < E) wa[u] = W[(size_t)(e0 + r) * D + d + u];
+                    }
+                }
+                xv = make_float4(xa[0], xa[1], xa[2], xa[3]);
+                wv = make_float4(wa[0], wa[1], wa[2], wa[3]);
+            }
+            xs[r][c] = xv.x; xs[r][c + 1] = xv.y; xs[r][c + 2] = xv.z; xs[r][c + 3] = xv.w;
+            ws[r][c] = wv.x; ws[r][c + 1] = wv.y; ws[r][c + 2] = wv.z; ws[r][c + 3] = wv.w;
+        }
+        __syncthreads();
+        // A lane (m = lane % 16, k = lane / 16) of each 16 x 16 x 4 step; B likewise
+#pragma unroll
+        for (int k0 = 0; k0 < COLI_RG_BK; k0 += 4) {
+            const int k = k0 + (lane >> 4);
+            float av[2], bv[2];
+#pragma unroll
+            for (int a = 0; a < 2; a++) av[a] = xs[wr + 16 * a + (lane & 15)][k];
+#pragma unroll
+            for (int b = 0; b < 2; b++) bv[b] = ws[wc + 16 * b + (lane & 15)][k];
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // lane holds C[4 (lane / 16) + i][lane % 16] of each 16 x 16 block
+    float *dst = part + (size_t)ch * S * E;
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int s = s0 + wr + 16 * a + 4 * (lane >> 4) + i, e = e0 + wc + 16 * b + (lane & 15);
+                if (s < S && e < E) dst[(size_t)s * E + e] = acc[a][b][i];
+            }
+}
+
+extern "C" hipError_t coli_launch_router_gemm(const float *x, int S, const float *W, int D, int E, float *part,
+                                              hipStream_t st) {
+    const dim3 grid((S + COLI_RG_BM - 1) / COLI_RG_BM, (E + COLI_RG_BM - 1) / COLI_RG_BM,
+                    (D + COLI_ROUTER_CHUNK - 1) / COLI_ROUTER_CHUNK);
+    hipLaunchKernelGGL(coli_router_gemm, grid, dim3(256), 0, st, x, S, W, D, E, part);
+    return hipGetLastError();
+}
+
+
+
 // part: [coli_router_chunks(D)][S][E] f32 partial logits.
 extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E,
                                                 float *part, hipStream_t st) {
