@@ -213,17 +213,32 @@ class Bench:
         for t in ups + downs:
             b.cuda_tensor_free(t)
 
-    # -- CPU baseline: the reference's own kernel ------------------------------
+    # -- CPU baseline: the reference's own kernels ------------------------------
     def cpu_baseline(self):
+        """The reference's CPU path on this host (OpenMP over
+        the physical cores, OMP_PROC_BIND=close, set in main() before any OpenMP
+        library loads): the dense int4 step of configs[1] (`value`), plus an
+        MXFP4 expert GEMV leg (configs[2] shapes) and an OLMoE-shaped MoE layer
+        leg (configs[0], the oracle's restatement of the composition)."""
         sys.path.insert(0, os.path.join(ROOT, "tests"))
         from oracle_lib import REF_PATH, Ref, Cref
         kind = "reference" if os.path.exists(REF_PATH) else "port"
         lib = Ref() if kind == "reference" else Cref()
-        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        cref = Cref()
+        secs = self.args.cpu_seconds
         (qu, su), (qd, sd) = self.cpu_inputs["up"], self.cpu_inputs["down"]
         h = np.empty((16, UP[0]), np.float32)
 
-        def one_pass():
+        def timed(fn):
+            fn()                          # warm the page cache / thread pool
+            t0 = time.perf_counter()
+            work, reps = 0, 0
+            while time.perf_counter() - t0 < secs:
+                work += fn()
+                reps += 1
+            return work, reps, time.perf_counter() - t0
+
+        def dense_pass():
             nbytes = 0
             for B in BATCHES:
                 xb = np.ascontiguousarray(self.cpu_x[:B])
@@ -232,17 +247,62 @@ class Bench:
                 nbytes += bytes_i4(*UP, B) + bytes_i4(*DOWN, B)
             return nbytes
 
-        one_pass()                       # warm the page cache / thread pool
-        t0 = time.perf_counter()
-        nbytes, reps = 0, 0
-        while time.perf_counter() - t0 < self.args.cpu_seconds:
-            nbytes += one_pass()
-            reps += 1
-        dt = time.perf_counter() - t0
-        return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
-                "sample": f"{reps} passes of the bench step (up+down GEMV at batch 1/4/8/16) over one "
-                          f"weight copy, {dt:.1f} s, c/quant.h matmul_i4_grouped (AVX2+FMA, OpenMP)",
-                "ms_per_step": round(dt / reps * 1e3, 2)}
+        nbytes, reps, dt = timed(dense_pass)
+        out = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": CPU_INFO["threads"], "kind": kind,
+               "sample": f"{reps} passes of the bench step (up+down GEMV at batch 1/4/8/16) over one "
+                         f"weight copy, {dt:.1f} s, c/quant.h matmul_i4_grouped (OpenMP)",
+               "ms_per_step": round(dt / reps * 1e3, 2), "cpu": CPU_INFO}
+        # MXFP4 expert GEMV, DeepSeek-V3 expert shapes (gate/up 2048x7168, down 7168x2048), batch 1
+        rng = np.random.default_rng(77)
+        mats = [(rng.integers(0, 256, (O, I // 2), dtype=np.uint8), rng.integers(119, 124, (O, I // 32), dtype=np.uint8),
+                 O, I) for O, I in ((2048, 7168), (7168, 2048))]
+        x1 = {I: bf16_exact(rng.standard_normal((1, I)).astype(np.float32)) for I in (7168, 2048)}
+
+        def mx_pass():
+            nb = 0
+            for q4, e8, O, I in mats:
+                lib.matmul_mxfp4(x1[I], q4, e8, O, I)
+                nb += bytes_fp4(O, I, 1)
+            return nb
+
+        nb, reps, dt = timed(mx_pass)
+        out["mxfp4_gemv"] = {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "kind": kind,
+                             "sample": f"{reps} x (2048x7168 + 7168x2048) matmul_mxfp4 at batch 1, {dt:.1f} s"}
+        # OLMoE-shaped MoE layer: 64 int4 experts, top-8 softmax, batch 1
+        D, I, E, K = 2048, 1024, 64, 8
+        experts = []
+        for _ in range(E):
+            trip = []
+            for O, II in ((I, D), (I, D), (D, I)):
+                trip.append((rng.integers(0, 256, (O, II // 2), dtype=np.uint8), fp16_scales(rng, O, II // 32)))
+            experts.append(tuple(trip))
+        W = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+        xs = bf16_exact(rng.standard_normal((64, D)).astype(np.float32))
+        state = {"i": 0}
+
+        def moe_pass():
+            # the reference's kernels for the router GEMV and the experts
+            # (c/olmoe.c:645-697 order): softmax top-8, silu(gate) * up, down,
+            # weighted sum in slot order
+            r = state["i"] % 64
+            state["i"] += 1
+            x = xs[r:r + 1]
+            logits = lib.matmul_f32(x, W)
+            idx, w, keff = cref.route(logits, K, 0)
+            acc = np.zeros(D, np.float32)
+            for kk in range(keff[0]):
+                (gq, gs), (uq, us), (dq, dsc) = experts[idx[0, kk]]
+                g = lib.matmul_i4_grouped(x, gq, gs, I, D, 32)
+                u = lib.matmul_i4_grouped(x, uq, us, I, D, 32)
+                hid = cref.swiglu(g, u)
+                acc += w[0, kk] * lib.matmul_i4_grouped(hid, dq, dsc, D, I, 32)[0]
+            return 1
+
+        toks, reps, dt = timed(moe_pass)
+        out["moe_layer_olmoe_int4"] = {"value": round(toks / dt, 1), "unit": "tokens/s", "kind": kind,
+                                       "sample": f"{reps} single-token layers (router GEMV + top-8 + 8 experts on "
+                                                 f"the reference's c/quant.h kernels), {dt:.1f} s"}
+        return out
 
     # -- fused MoE layer ------------------------------
     def moe(self, name, fmt, D, I, E, K, mode, shared, batches, layers_for_anticache, bias, zipf=None,
@@ -507,7 +567,38 @@ def moe_layers(bench):
     return res
 
 
+def cpu_topology():
+    """CPU model, physical cores and logical CPUs this process may run on."""
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    model, cores, cur = "unknown", set(), {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f.read().split("\n\n"):
+                kv = dict(l.split(":", 1) for l in line.splitlines() if ":" in l)
+                kv = {k.strip(): v.strip() for k, v in kv.items()}
+                if "processor" not in kv:
+                    continue
+                model = kv.get("model name", model)
+                if int(kv["processor"]) in cpus:
+                    cores.add((kv.get("physical id", "0"), kv.get("core id", kv["processor"])))
+    except (OSError, ValueError, KeyError):
+        pass
+    return model, max(1, len(cores)), len(cpus)
+
+
+CPU_INFO = {}
+
+
 def main():
+    # The CPU baseline's OpenMP runs on the physical cores, bound close
+    # (BASELINE.md section 3): set before any OpenMP library is loaded. An
+    # OMP_NUM_THREADS already in the environment (the host's CPU share) caps it.
+    model, phys, logical = cpu_topology()
+    threads = min(phys, int(os.environ.get("OMP_NUM_THREADS", phys)))
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    os.environ["OMP_PROC_BIND"] = "close"
+    CPU_INFO.update({"model": model, "physical_cores": phys, "logical_cpus": logical, "threads": threads,
+                     "OMP_NUM_THREADS": threads, "OMP_PROC_BIND": "close"})
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
