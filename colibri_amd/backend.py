@@ -97,6 +97,8 @@ _SIGS = {
     "coli_hip_matmul_mxfp4_i8": ([_f, _f, _u8, _u8, _i, _i, _i], _i),
     "coli_hip_fp4_matmul_i8": ([_tp, _f, _f, _i], _i),
     "coli_hip_fp4_matmul_i8_dev": ([_tp, _vp, _vp, _i], _i),
+    "coli_hip_matmul_i4_idot": ([_tp, _f, _f, _i], _i),
+    "coli_hip_matmul_i4_idot_dev": ([_tp, _vp, _vp, _i], _i),
     "coli_hip_moe_create": ([C.POINTER(_vp), _i, C.POINTER(ColiHipMoeConfig), _f, _f, _tpp, _tpp, _tpp,
                              _tp, _tp, _tp], _i),
     "coli_hip_moe_free": ([_vp], None),

@@ -179,7 +179,7 @@ extern "C" void coli_cuda_shutdown(void) {
         DevBuf *bufs[] = {&ctx->x, &ctx->h, &ctx->y, &ctx->g, &ctx->u, &ctx->partial,
                           &ctx->prob, &ctx->stage_w, &ctx->stage_s, &ctx->qdq, &ctx->flags,
                           &ctx->rslot, &ctx->rw, &ctx->tmp_tiles, &ctx->tmp_scales, &ctx->zeros,
-                          &ctx->split_cnt};
+                          &ctx->split_cnt, &ctx->idot_y, &ctx->idot_sx};
         for (DevBuf *b : bufs) free_buf(b);
         for (int f = 0; f < 4; f++) {
             free_buf(&ctx->frag[f].hi);
@@ -468,6 +468,7 @@ extern "C" void coli_cuda_tensor_free(ColiCudaTensor *t) {
     if (t->w) (void)hipFree(t->w);
     if (t->sc) (void)hipFree(t->sc);
     if (t->desc) (void)hipFree(t->desc);
+    if (t->sc_unit) (void)hipFree(t->sc_unit);
     std::free(t);
 }
 

@@ -62,7 +62,7 @@ struct DevCtx {
     size_t tensor_count = 0, tensor_bytes = 0;
     // grow-only scratch
     DevBuf x, h, y, g, u, partial, prob, zeros, stage_w, stage_s, qdq, flags;
-    DevBuf rslot, rw, tmp_tiles, tmp_scales, split_cnt;
+    DevBuf rslot, rw, tmp_tiles, tmp_scales, split_cnt, idot_y, idot_sx;
     FragSet frag[4];                   // 0/1: inputs (int4 / fp4 order), 2/3: hidden rows
     DevBuf pipe[COLI_PIPE_SLOTS];
     // pinned staging
@@ -112,6 +112,11 @@ hipError_t coli_launch_generic_i4(const ColiCudaTensor *t, const float *x, int l
                                   int S, hipStream_t st);
 hipError_t coli_launch_qdq_e4m3(const float *x, float *y, int S, int K, hipStream_t st);
 hipError_t coli_launch_qdq_i8(const float *x, float *y, int S, int K, hipStream_t st);
+hipError_t coli_launch_qrow_i8_frag(const float *x, int ldx, int nrows, int K, int ngp, int int4_order,
+                                    _Float16 *hi, int *exp2out, float *sx, hipStream_t st);
+hipError_t coli_launch_unit_scales(void *sc, size_t n, int half_scales, hipStream_t st);
+hipError_t coli_launch_idot_scale(float *y, const float *yi, const float *sx, const void *sc, int half_scales,
+                                  int nq, int O, int S, hipStream_t st);
 int coli_router_chunks(int D);   // column chunks of the router partials
 hipError_t coli_launch_router_logits(const float *x, int S, const float *W, int D, int E, float *part,
                                      hipStream_t st);

@@ -45,6 +45,7 @@ struct ColiCudaTensor {
     int ng_src;                  // scale groups per source row (GENERIC)
     size_t accounted;            // bytes charged to the device statistics
     struct ColiProb *desc;       // device: 64 descriptors, entry s-1 = this matrix on s rows
+    void *sc_unit;               // fmt=2 int8-activation path: unit group scales (made on first use)
 };
 
 // One GEMV problem: a matrix (or a gate/up pair) applied to a set of batch rows.

@@ -726,6 +726,51 @@ extern "C" int coli_hip_gemm_run_dev(ColiCudaTensor *t, float *y_dev, int S) {
     return gemm_run(ctx, t, y_dev, S);
 }
 
+// fmt=2 with int8 activations (c/colibri.c:937-945, matmul_i4_idot): the
+// rows quantized by qrow_i8 into exact fp16 fragments, the integer dot on the
+// tiled GEMV over unit group scales (every partial sum an exact integer), then
+// y = (dot * scale[o]) * sx[s]. Results are bitwise the reference's.
+#define COLI_IDOT_MAX_I 16512   // 8 * 127 * I < 2^24: every f32 partial sum is exact
+static int idot_dev(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
+    if (t->fmt != 2 || (t->kind != COLI_KIND_I4_H && t->kind != COLI_KIND_I4_F) || t->I > COLI_IDOT_MAX_I)
+        return 0;
+    const int half = t->kind == COLI_KIND_I4_H;
+    if (!t->sc_unit) {
+        void *p = nullptr;
+        if (!hip_check(hipMalloc(&p, t->sc_bytes), "unit scales") ||
+            !hip_check(coli_launch_unit_scales(p, t->sc_bytes / (half ? 2 : 4), half, ctx->stream), "unit scales")) {
+            if (p) (void)hipFree(p);
+            return 0;
+        }
+        t->sc_unit = p;
+    }
+    const int set = frag_set_of(t->kind, false), ngp = ngp_of(t->I);
+    FragSet &f = ctx->frag[set];
+    const size_t halves = (size_t)S * ngp * 32;
+    if (!reserve(ctx, &f.hi, halves * 2, 0) || !reserve(ctx, &f.lo, halves * 2, 0) ||
+        !reserve(ctx, &f.exp, (size_t)S * sizeof(int), 0) || !reserve(ctx, &ctx->idot_y, (size_t)S * t->O * 4, 0) ||
+        !reserve(ctx, &ctx->idot_sx, (size_t)S * 4, 0))
+        return 0;
+    // a fresh generation with no lo part: the set's flag holds an older one
+    f.pending = false;
+    f.px = nullptr;
+    f.psrc = nullptr;
+    f.gen = f.gen == 0x7fffffff ? 1 : f.gen + 1;
+    if (f.gen == 1 && !hip_check(coli_launch_zero_i32((int *)ctx->flags.p + set, 1, ctx->stream), "fragment flag"))
+        return 0;
+    if (!hip_check(coli_launch_qrow_i8_frag(x_dev, t->I, S, t->I, ngp, 1, (_Float16 *)f.hi.p, (int *)f.exp.p,
+                                            (float *)ctx->idot_sx.p, ctx->stream),
+                   "int8 activation rows"))
+        return 0;
+    const ColiProb p = {t->w, t->sc_unit, nullptr, nullptr, S, 0, 0, 0};
+    if (!run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr,
+                  (float *)ctx->idot_y.p, t->O, &p))
+        return 0;
+    return hip_check(coli_launch_idot_scale(y_dev, (const float *)ctx->idot_y.p, (const float *)ctx->idot_sx.p, t->sc,
+                                            half, t->nq, t->O, S, ctx->stream),
+                     "int8 activation scales");
+}
+
 static int gemm_host(DevCtx *ctx, ColiCudaTensor *t, float *y, const float *x, int S, int qdq) {
     size_t xb = (size_t)S * t->I * sizeof(float), yb = (size_t)S * t->O * sizeof(float);
     if (!reserve(ctx, &ctx->x, xb, 0) || !reserve(ctx, &ctx->y, yb, 0) ||
@@ -746,12 +791,28 @@ static int gemm_host(DevCtx *ctx, ColiCudaTensor *t, float *y, const float *x, i
             return 0;
         xin = (const float *)ctx->qdq.p;
     }
-    if (!gemm_dev(ctx, t, (float *)ctx->y.p, xin, S) ||
+    if (!(qdq == 3 ? idot_dev(ctx, t, (float *)ctx->y.p, xin, S) : gemm_dev(ctx, t, (float *)ctx->y.p, xin, S)) ||
         !hip_check(hipMemcpyAsync(ctx->host_y.h, ctx->y.p, yb, hipMemcpyDeviceToHost, ctx->stream), "output download") ||
         !hip_check(hipStreamSynchronize(ctx->stream), "gemm synchronize"))
         return 0;
     std::memcpy(y, ctx->host_y.h, yb);
     return 1;
+}
+
+extern "C" int coli_hip_matmul_i4_idot(ColiCudaTensor *t, float *y, const float *x, int S) {
+    if (fault_injected()) return 0;
+    if (!t || !y || !x || S < 1 || t->fmt != 2) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
+    return gemm_host(ctx, t, y, x, S, 3);
+}
+
+extern "C" int coli_hip_matmul_i4_idot_dev(ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
+    if (fault_injected()) return 0;
+    if (!t || !y_dev || !x_dev || S < 1 || t->fmt != 2) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
+    return idot_dev(ctx, t, y_dev, x_dev, S);
 }
 
 extern "C" int coli_cuda_matmul(ColiCudaTensor **tensor, float *y, const float *x, const void *weights,

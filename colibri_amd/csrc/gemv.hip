@@ -765,3 +765,96 @@ extern "C" hipError_t coli_launch_qdq_i8(const float *x, float *y, int S, int K,
     hipLaunchKernelGGL(coli_qdq_i8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, S, K);
     return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// fmt=2 with int8 activations (the IDOT path, c/colibri.c:937-945): qrow_i8
+// per row (c/quant.h:581-586), then y = (float)(integer dot) * scale[o] *
+// sx[s] (matmul_i4_idot, c/quant.h:924-933). On the device the integer dot
+// runs on the regular GEMV: the int8 values enter as exact fp16 activation
+// fragments (exponent 0, no lo part), the tensor's group scales are replaced
+// by ones, and every MFMA result and partial sum is an integer below 2^24
+// (|sum| <= 8 * 127 * I, I <= 16512), so the f32 accumulation is exact in any
+// order; the two scale products follow in the reference's order.
+// ---------------------------------------------------------------------------
+// One 256-thread block per row: the row's maximum, s = max / 127 (at least
+// 1e-12), inv = 1 / s, q = rint(x * inv) as fp16 fragments in the GEMV's
+// A-operand order (columns past K are zero), exponent 0; sx[row] = s.
+__global__ __launch_bounds__(256) void coli_qrow_i8_frag(const float *__restrict__ x, int ldx, int K, int ngp,
+                                                         int int4_order, _Float16 *__restrict__ hi,
+                                                         int *__restrict__ exp2out, float *__restrict__ sx) {
+    const int r = blockIdx.x;
+    const float *xr = x + (size_t)r * ldx;
+    float m = 0.0f;
+    for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(xr[k]));
+#pragma unroll
+    for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __shared__ float wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float s = m / 127.f;
+    if (s < 1e-12f) s = 1e-12f;
+    const float inv = 1.f / s;
+    if (threadIdx.x == 0) {
+        exp2out[r] = 0;
+        sx[r] = s;
+    }
+    const int nslot = ngp * 4;
+    for (int slot = threadIdx.x; slot < nslot; slot += 256) {
+        half8v h;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int off = int4_order ? ((t < 4) ? 2 * t : 2 * (t - 4) + 1) : t;
+            const int k = slot * 8 + off;
+            float q = k < K ? rintf(xr[k] * inv) : 0.0f;
+            if (int4_order && (off & 1)) q *= 0.0625f;   // exact: |q| <= 128
+            h[t] = (_Float16)q;
+        }
+        *(half8v *)(hi + (size_t)r * ngp * 32 + (size_t)slot * 8) = h;
+    }
+}
+
+__global__ void coli_fill_u16(uint16_t *p, size_t n, uint16_t v) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+__global__ void coli_fill_f32(float *p, size_t n, float v) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// y[s, o] = (yi[s, o] * scale[o]) * sx[s], scale[o] read from the tensor's
+// tile-ordered group scales (group 0 of row o: fmt=2 scales are per row).
+__global__ void coli_idot_scale(float *__restrict__ y, const float *__restrict__ yi, const float *__restrict__ sx,
+                                const void *__restrict__ sc, int half_scales, int nq, int O) {
+    const int o = blockIdx.x * blockDim.x + threadIdx.x, s = blockIdx.y;
+    if (o >= O) return;
+    const size_t e = ((size_t)(o >> 4) * nq * 16 + (o & 15)) * 4;   // tile (o / 16, quad 0), row o % 16, group 0
+    const float so = half_scales ? (float)((const _Float16 *)sc)[e] : ((const float *)sc)[e];
+    y[(size_t)s * O + o] = (yi[(size_t)s * O + o] * so) * sx[s];
+}
+
+extern "C" hipError_t coli_launch_qrow_i8_frag(const float *x, int ldx, int nrows, int K, int ngp, int int4_order,
+                                               _Float16 *hi, int *exp2out, float *sx, hipStream_t st) {
+    if (nrows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(coli_qrow_i8_frag, dim3(nrows), dim3(256), 0, st, x, ldx, K, ngp, int4_order, hi, exp2out,
+                       sx);
+    return hipGetLastError();
+}
+
+// Ones in the tensor's scale format (fp16 or f32), n scale entries.
+extern "C" hipError_t coli_launch_unit_scales(void *sc, size_t n, int half_scales, hipStream_t st) {
+    if (half_scales)
+        hipLaunchKernelGGL(coli_fill_u16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (uint16_t *)sc, n,
+                           (uint16_t)0x3C00u);
+    else
+        hipLaunchKernelGGL(coli_fill_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (float *)sc, n, 1.0f);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t coli_launch_idot_scale(float *y, const float *yi, const float *sx, const void *sc,
+                                             int half_scales, int nq, int O, int S, hipStream_t st) {
+    hipLaunchKernelGGL(coli_idot_scale, dim3((O + 255) / 256, S), dim3(256), 0, st, y, yi, sx, sc, half_scales, nq,
+                       O);
+    return hipGetLastError();
+}

@@ -59,6 +59,18 @@ int coli_hip_matmul_mxfp4_i8(float *y, const float *x, const unsigned char *q4,
 int coli_hip_fp4_matmul_i8(ColiCudaTensor *tensor, float *y, const float *x, int S);
 int coli_hip_fp4_matmul_i8_dev(ColiCudaTensor *tensor, float *y_dev, const float *x_dev, int S);
 
+/* fmt=2 (int4, one f32 scale per row) with int8 activations: replaces the
+ * reference's IDOT path for fmt=2 experts (c/colibri.c:937-945: qrow_i8
+ * c/quant.h:581-586 per row, then matmul_i4_idot c/quant.h:924-933 with
+ * dot_i4i8 674-801). Each row is quantized to int8 (s = max|x| / 127, at least
+ * 1e-12; q = rint(x * (1 / s))), the integer dot is exact, and y[s, o] =
+ * (float)dot * scale[o] * s: bitwise the reference's result. I <= 16512.
+ * Resident fmt=2 tensor; host pointers (synchronous) / device pointers
+ * (asynchronous on the backend stream). Returns 1 / 0 (y untouched on
+ * failure). */
+int coli_hip_matmul_i4_idot(ColiCudaTensor *tensor, float *y, const float *x, int S);
+int coli_hip_matmul_i4_idot_dev(ColiCudaTensor *tensor, float *y_dev, const float *x_dev, int S);
+
 /* ---- fused MoE layer (router -> union -> experts -> SwiGLU -> scatter) ---- */
 typedef struct ColiHipMoe ColiHipMoe;
 

@@ -209,6 +209,47 @@ void cref_matmul_i4_grouped(float *y, const float *x, const uint8_t *q4,
 
 /* fmt=2 per-row int4, c/quant.h:125-165 (the 16-column AVX2 body: one
  * 8-lane accumulator over the whole row, hsum8, pair tail, then x scale). */
+/* Row quantization of the int8-activation (IDOT) path, qrow_i8
+ * (c/quant.h:581-586): s = max|x| / 127 (at least 1e-12), q = rint(x * (1 / s))
+ * in f32, no clamp. Returns s. */
+float cref_qrow_i8(const float *x, int8_t *q, int I) {
+    float amax = 0.0f;
+    for (int i = 0; i < I; i++) {
+        float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    float s = amax / 127.f;
+    if (s < 1e-12f) s = 1e-12f;
+    float inv = 1.f / s;
+    for (int i = 0; i < I; i++) q[i] = (int8_t)lrintf(x[i] * inv);
+    return s;
+}
+
+/* fmt=2 with int8 activations (the IDOT path, c/colibri.c:937-945 and
+ * matmul_i4_idot c/quant.h:924-933 with dot_i4i8 674-801): each row is
+ * quantized by qrow_i8; y[s, o] = (float)(sum_i (nib - 8) * q[s, i]) *
+ * scale[o] * sx[s], the integer sum exact. */
+void cref_matmul_i4_idot(float *y, const float *x, const uint8_t *q4,
+                         const float *scale, int S, int I, int O) {
+    int rb = (I + 1) / 2;
+    int8_t *xq = (int8_t *)malloc((size_t)S * (I > 0 ? I : 1));
+    float *sx = (float *)malloc((size_t)(S > 0 ? S : 1) * sizeof(float));
+    if (!xq || !sx) { free(xq); free(sx); return; }
+    for (int s = 0; s < S; s++) sx[s] = cref_qrow_i8(x + (int64_t)s * I, xq + (int64_t)s * I, I);
+    #pragma omp parallel for schedule(static)
+    for (int o = 0; o < O; o++) {
+        const uint8_t *w = q4 + (int64_t)o * rb;
+        for (int s = 0; s < S; s++) {
+            const int8_t *xs = xq + (int64_t)s * I;
+            int32_t d = 0;
+            for (int i = 0; i < I; i++) d += (nib_at(w, i) - 8) * (int32_t)xs[i];
+            y[(int64_t)s * O + o] = (float)d * scale[o] * sx[s];
+        }
+    }
+    free(xq);
+    free(sx);
+}
+
 void cref_matmul_i4(float *y, const float *x, const uint8_t *q4,
                     const float *scale, int S, int I, int O) {
     int rb = (I + 1) / 2;

@@ -20,6 +20,9 @@
  *       magnitude-relative 1e-6 metric of c/tests/test_i4_grouped.c:28-54
  *       on ragged shapes; closed form (unit scales, x = e_i gives nibble-8).
  *   cref_matmul_i4: fmt=2 == fmt=4 with gs = I (c/tests/test_grouped_g4_cuda.cu:29-46)
+ *   cref_qrow_i8 / cref_matmul_i4_idot (fmt=2 int8 activations): bitwise vs
+ *       oracle/_ref qrow_i8 + matmul_i4_idot and tests/golden/golden_idot.npz;
+ *       the exact-integer closed form (int64 dot, then the two f32 products).
  *       + brute force.
  *   cref_matmul_mxfp4: bitwise vs oracle/_ref matmul_mxfp4; all-16-codes
  *       exactness (c/tests/test_mxfp4_cuda.cu:106-132); e8 edges 0/127/255.
@@ -71,6 +74,9 @@ int cref_fp8_activation_qdq(float *out, uint8_t *scales, const float *in,
 void cref_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O);
 void cref_matmul_i4_grouped(float *y, const float *x, const uint8_t *q4,
                             const float *scale, int S, int I, int O, int gs);
+float cref_qrow_i8(const float *x, int8_t *q, int I);
+void cref_matmul_i4_idot(float *y, const float *x, const uint8_t *q4,
+                         const float *scale, int S, int I, int O);
 void cref_matmul_i4(float *y, const float *x, const uint8_t *q4,
                     const float *scale, int S, int I, int O);
 void cref_matmul_mxfp4(float *y, const float *x, const uint8_t *q4,

@@ -33,3 +33,16 @@ void ref_matmul_mxfp4_i8(float *y, const float *x, const uint8_t *q4,
                          const uint8_t *e8, int S, int I, int O) {
     matmul_mxfp4_i8(y, x, q4, e8, S, I, O);
 }
+float ref_qrow_i8(const float *x, int8_t *q, int I) { return qrow_i8(x, q, I); }
+/* the fmt=2 IDOT path as c/colibri.c:937-945 runs it: qrow_i8 per row, then
+ * matmul_i4_idot */
+void ref_matmul_i4_idot(float *y, const float *x, const uint8_t *q4,
+                        const float *scale, int S, int I, int O) {
+    int8_t *xq = (int8_t *)malloc((size_t)S * (I > 0 ? I : 1));
+    float *sx = (float *)malloc((size_t)(S > 0 ? S : 1) * sizeof(float));
+    if (!xq || !sx) { free(xq); free(sx); return; }
+    for (int s = 0; s < S; s++) sx[s] = qrow_i8(x + (int64_t)s * I, xq + (int64_t)s * I, I);
+    matmul_i4_idot(y, xq, sx, q4, scale, S, I, O);
+    free(xq);
+    free(sx);
+}

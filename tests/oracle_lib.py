@@ -68,6 +68,8 @@ class Cref(_Lib):
         self._f32 = self.fn("matmul_f32", [_f, _f, _f, _i, _i, _i])
         self._i4g = self.fn("matmul_i4_grouped", [_f, _f, _u8, _f, _i, _i, _i, _i])
         self._i4 = self.fn("matmul_i4", [_f, _f, _u8, _f, _i, _i, _i])
+        self._i4d = self.fn("matmul_i4_idot", [_f, _f, _u8, _f, _i, _i, _i])
+        self._qrow = self.fn("qrow_i8", [_f, C.POINTER(C.c_int8), _i], C.c_float)
         self._mx = self.fn("matmul_mxfp4", [_f, _f, _u8, _u8, _i, _i, _i])
         self._mx8 = self.fn("matmul_mxfp4_i8", [_f, _f, _u8, _u8, _i, _i, _i])
         self._fp4b = self.fn("fp4_matmul_batch", [_f, _u8, _u8, _i, _i, _f, _i], _i)
@@ -106,6 +108,19 @@ class Cref(_Lib):
         y = np.empty((S, O), np.float32)
         self._i4(f32p(y), f32p(x), u8p(q4), f32p(sc), S, I, O)
         return y
+
+    def matmul_i4_idot(self, x, q4, sc, O, I):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty((x.shape[0], O), np.float32)
+        self._i4d(f32p(y), f32p(x), u8p(np.ascontiguousarray(q4)), f32p(np.ascontiguousarray(sc, np.float32)),
+                  x.shape[0], I, O)
+        return y
+
+    def qrow_i8(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.empty(x.size, np.int8)
+        s = self._qrow(f32p(x), q.ctypes.data_as(C.POINTER(C.c_int8)), x.size)
+        return q, np.float32(s)
 
     def matmul_mxfp4(self, x, q4, e8, O, I):
         S = x.shape[0]
@@ -218,6 +233,8 @@ class Ref(_Lib):
         super().__init__(path, "")
         self._i4g = self.fn("ref_matmul_i4_grouped", [_f, _f, _u8, _f, _i, _i, _i, _i])
         self._i4 = self.fn("ref_matmul_i4", [_f, _f, _u8, _f, _i, _i, _i])
+        self._i4d = self.fn("ref_matmul_i4_idot", [_f, _f, _u8, _f, _i, _i, _i])
+        self._qrow = self.fn("ref_qrow_i8", [_f, C.POINTER(C.c_int8), _i], C.c_float)
         self._mx = self.fn("ref_matmul_mxfp4", [_f, _f, _u8, _u8, _i, _i, _i])
         self._mx8 = self.fn("ref_matmul_mxfp4_i8", [_f, _f, _u8, _u8, _i, _i, _i])
         self._f32 = self.fn("ref_matmul_f32", [_f, _f, _f, _i, _i, _i])
@@ -255,6 +272,9 @@ class Ref(_Lib):
         y = np.empty((S, O), np.float32)
         self._i4g(f32p(y), f32p(x), u8p(q4), f32p(sc), S, I, O, gs)
         return y
+
+    matmul_i4_idot = Cref.matmul_i4_idot
+    qrow_i8 = Cref.qrow_i8
 
     def matmul_i4(self, x, q4, sc, O, I):
         S = x.shape[0]

@@ -319,3 +319,62 @@ def test_gemv_kernel_paths(session, monkeypatch, mode, fmt, S, O, I, xkind):
         session.free(h)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
     check(y, ref, mag)
+
+
+# fmt=2 with int8 activations (the reference's IDOT path for fmt=2 experts,
+# c/colibri.c:937-945): bitwise equal to the oracle, which is pinned bitwise
+# to the reference's qrow_i8 + matmul_i4_idot.
+@pytest.mark.parametrize("O,I,S,fp16", [(64, 256, 1, True), (1024, 2048, 4, True), (100, 97, 3, False),
+                                        (4096, 14336, 2, True), (48, 640, 16, False), (300, 512, 40, True)])
+def test_int4_fmt2_int8_activations(session, O, I, S, fp16):
+    import ctypes as C
+    from colibri_amd.backend import f32p
+    rng = np.random.default_rng(O * 3 + I + S)
+    q4, sc = rand_i4(rng, O, I, 0, fp16_scales=fp16)
+    x = (rng.standard_normal((S, I)) * 3).astype(np.float32)
+    x[0, :3] = [0.5, -2.5, 0.0]
+    h = session.upload(q4, sc, 2, I, O)
+    y = np.zeros((S, O), np.float32)
+    b = session.b
+    try:
+        assert b.hip_tensor_kind(h) == (0 if fp16 else 1)
+        assert b.hip_matmul_i4_idot(h, f32p(y), f32p(x), S)
+        # device-pointer form, twice (the unit scales are made on first use)
+        px, py = b.cuda_pipe_alloc(0, x.nbytes), b.cuda_pipe_alloc(0, y.nbytes)
+        try:
+            assert b.cuda_pipe_upload(0, px, x.ctypes.data_as(C.c_void_p), x.nbytes)
+            assert b.hip_matmul_i4_idot_dev(h, py, px, S)
+            y2 = np.zeros_like(y)
+            assert b.cuda_pipe_sync(0)
+            assert b.cuda_pipe_download(0, py, y2.ctypes.data_as(C.c_void_p), y2.nbytes)
+        finally:
+            b.cuda_pipe_free(0, px)
+            b.cuda_pipe_free(0, py)
+    finally:
+        session.free(h)
+    ref = cref.matmul_i4_idot(x, q4, sc, O, I)
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), np.abs(y - ref).max()
+    assert np.array_equal(y2.view(np.uint32), ref.view(np.uint32))
+
+
+def test_int4_fmt2_int8_activations_refusals(session):
+    from colibri_amd.backend import f32p
+    rng = np.random.default_rng(5)
+    q4, sc = rand_i4(rng, 32, 256, 32)
+    h = session.upload(q4, sc, 4, 256, 32, 32)          # fmt=4: not this path
+    x = rand_x(rng, 1, 256)
+    y = np.full((1, 32), 3.0, np.float32)
+    try:
+        assert not session.b.hip_matmul_i4_idot(h, f32p(y), f32p(x), 1)
+    finally:
+        session.free(h)
+    assert np.all(y == 3.0)
+    q4, sc = rand_i4(rng, 16, 16640, 0)                  # I > 16512: an f32 partial sum could round
+    h = session.upload(q4, sc, 2, 16640, 16)
+    x = rand_x(rng, 1, 16640)
+    y = np.full((1, 16), 3.0, np.float32)
+    try:
+        assert not session.b.hip_matmul_i4_idot(h, f32p(y), f32p(x), 1)
+    finally:
+        session.free(h)
+    assert np.all(y == 3.0)

@@ -535,3 +535,60 @@ def test_moe_layer_vs_f64_composition(fmt, mode, shared):
     assert np.allclose(w, rw, rtol=2e-6, atol=0)
     err = np.abs(out.astype(np.float64) - ref) / np.maximum(mag, 1e-30)
     assert err.max() <= 2e-5, err.max()
+
+
+# ---- fmt=2 with int8 activations (IDOT, c/quant.h:581-586, 674-801, 924-933) ----
+def _idot_closed_form(x, q4, sc, O, I):
+    """qrow_i8 in float32 numpy (IEEE round-to-nearest-even, as lrintf), the
+    integer dot in int64, then (float)d * scale * sx in float32."""
+    from quant_util import nibbles
+    S = x.shape[0]
+    y = np.empty((S, O), np.float32)
+    w = (nibbles(q4, I) - 8).astype(np.int64)
+    for s in range(S):
+        amax = np.float32(np.max(np.abs(x[s]))) if I else np.float32(0)
+        sx = np.float32(amax / np.float32(127.0))
+        if sx < np.float32(1e-12):
+            sx = np.float32(1e-12)
+        inv = np.float32(np.float32(1.0) / sx)
+        q = np.rint((x[s] * inv).astype(np.float32)).astype(np.int64)
+        d = w @ q
+        y[s] = (d.astype(np.float32) * sc.astype(np.float32)) * sx
+    return y
+
+
+def test_golden_idot():
+    g = np.load(os.path.join(os.path.dirname(GOLDEN), "golden_idot.npz"))
+    n = 0
+    while f"c{n}_x" in g:
+        S, I, O = (int(v) for v in g[f"c{n}_shape"])
+        got = cref.matmul_i4_idot(g[f"c{n}_x"], g[f"c{n}_q4"], g[f"c{n}_sc"], O, I)
+        assert np.array_equal(bits(got), bits(g[f"c{n}_y"])), n
+        n += 1
+    assert n >= 5
+
+
+def test_idot_closed_form():
+    rng = np.random.default_rng(4242)
+    for S, I, O in [(1, 64, 9), (3, 255, 17), (2, 1024, 5)]:
+        q4, sc = rand_i4(rng, O, I, 0, fp16_scales=False)
+        x = (rng.standard_normal((S, I)) * 5).astype(np.float32)
+        x[0, :4] = [0.5, -2.5, 127.0, 0.0]
+        got = cref.matmul_i4_idot(x, q4, sc, O, I)
+        assert np.array_equal(bits(got), bits(_idot_closed_form(x, q4, sc, O, I)))
+
+
+@pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built (needs the reference tree)")
+def test_idot_vs_compiled_reference():
+    ref = Ref()
+    rng = np.random.default_rng(4343)
+    for _ in range(25):
+        S, I, O = int(rng.integers(1, 6)), int(rng.integers(1, 700)), int(rng.integers(1, 40))
+        q4, sc = rand_i4(rng, O, I, 0, fp16_scales=False)
+        x = (rng.standard_normal((S, I)) * 10 ** rng.uniform(-3, 3)).astype(np.float32)
+        a = cref.matmul_i4_idot(x, q4, sc, O, I)
+        b = ref.matmul_i4_idot(x, q4, sc, O, I)
+        assert np.array_equal(bits(a), bits(b)), (S, I, O)
+        qa, sa = cref.qrow_i8(x[0])
+        qb, sb = ref.qrow_i8(x[0])
+        assert np.array_equal(qa, qb) and sa == sb
