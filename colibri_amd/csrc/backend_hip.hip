@@ -435,16 +435,24 @@ extern "C" int coli_hip_tensor_upload_mxfp4(ColiCudaTensor **tensor, const unsig
 extern "C" int coli_hip_tensor_upload_fp4_rows16(ColiCudaTensor **tensor, const unsigned char *pd,
                                                  const unsigned char *ps, int I, int O, int device) {
     if (!tensor || *tensor || !pd || !ps || O < 16 || O % 16 || I < 128 || I % 128) return 0;
-    // Undo the 16-row interleave (c/deepseek_v4.c:10975-10993) on the host,
-    // then take the row-major path.
-    size_t ds = (size_t)I / 2, ss = (size_t)I / 32;
-    std::vector<uint8_t> q4((size_t)O * ds), e8((size_t)O * ss);
-    for (size_t r = 0; r < (size_t)O; r++) {
-        size_t tile = r / 16, lane = r % 16;
-        for (size_t c = 0; c < ds; c++) q4[r * ds + c] = pd[(tile * ds + c) * 16 + lane];
-        for (size_t c = 0; c < ss; c++) e8[r * ss + c] = ps[(tile * ss + c) * 16 + lane];
-    }
-    return upload_impl(tensor, q4.data(), nullptr, e8.data(), 7, I, O, device, 32, 0);
+    DevCtx *ctx = ctx_of(device);
+    if (!bind_ctx(ctx)) return 0;
+    // The 16-row interleave (c/deepseek_v4.c:10975-10993) is undone on the
+    // device, into row-major bytes the tiled repack then reads from device
+    // memory; the e8m0 scales (1/16 of the bytes) are de-interleaved here.
+    const size_t ds = (size_t)I / 2, ss = (size_t)I / 32, wb = (size_t)O * ds;
+    std::vector<uint8_t> e8((size_t)O * ss);
+    for (size_t r = 0; r < (size_t)O; r++)
+        for (size_t c = 0; c < ss; c++) e8[r * ss + c] = ps[((r / 16) * ss + c) * 16 + r % 16];
+    if (!reserve(ctx, &ctx->stage_w, 2 * wb, 0) || !hip_check(hipStreamSynchronize(ctx->stream), "rows16 staging") ||
+        !hip_check(hipMemcpy(ctx->stage_w.p, pd, wb, hipMemcpyHostToDevice), "rows16 upload"))
+        return 0;
+    uint8_t *rows = (uint8_t *)ctx->stage_w.p + wb;
+    if (!hip_check(coli_launch_rows16_to_rows((const uint8_t *)ctx->stage_w.p, rows, O, (int)ds, ctx->stream),
+                   "rows16 de-interleave") ||
+        !hip_check(hipStreamSynchronize(ctx->stream), "rows16 de-interleave sync"))
+        return 0;
+    return upload_impl(tensor, rows, nullptr, e8.data(), 7, I, O, device, 32, 1);
 }
 
 extern "C" int coli_hip_tensor_upload_from_device(ColiCudaTensor **tensor, const void *weights_dev,

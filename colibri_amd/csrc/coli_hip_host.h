@@ -114,6 +114,7 @@ hipError_t coli_launch_qdq_e4m3(const float *x, float *y, int S, int K, hipStrea
 hipError_t coli_launch_qdq_i8(const float *x, float *y, int S, int K, hipStream_t st);
 hipError_t coli_launch_qrow_i8_frag(const float *x, int ldx, int nrows, int K, int ngp, int int4_order,
                                     _Float16 *hi, int *exp2out, float *sx, hipStream_t st);
+hipError_t coli_launch_rows16_to_rows(const uint8_t *packed, uint8_t *rows, int O, int nb, hipStream_t st);
 hipError_t coli_launch_unit_scales(void *sc, size_t n, int half_scales, hipStream_t st);
 hipError_t coli_launch_idot_scale(float *y, const float *yi, const float *sx, const void *sc, int half_scales,
                                   int nq, int O, int S, hipStream_t st);

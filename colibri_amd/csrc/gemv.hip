@@ -858,3 +858,21 @@ extern "C" hipError_t coli_launch_idot_scale(float *y, const float *yi, const fl
                        O);
     return hipGetLastError();
 }
+
+// 16-row interleave of coli_fp4_pack_rows16_v10 (c/deepseek_v4.c:10975-10993)
+// back to row-major bytes: row r, byte c <- packed[((r / 16) * nb + c) * 16 + r % 16]
+// (nb bytes per row), one thread per destination byte.
+__global__ void coli_rows16_to_rows(const uint8_t *__restrict__ packed, uint8_t *__restrict__ rows, int O, int nb) {
+    const size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= (size_t)O * nb) return;
+    const size_t r = d / nb, c = d - r * nb;
+    rows[d] = packed[((r >> 4) * nb + c) * 16 + (r & 15)];
+}
+
+extern "C" hipError_t coli_launch_rows16_to_rows(const uint8_t *packed, uint8_t *rows, int O, int nb,
+                                                 hipStream_t st) {
+    const size_t n = (size_t)O * nb;
+    hipLaunchKernelGGL(coli_rows16_to_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, packed, rows, O,
+                       nb);
+    return hipGetLastError();
+}

@@ -277,16 +277,16 @@ def outlier_x(rng, S, I):
 
 # Both GEMV kernels and both activation paths of the LDS-ring kernel (f32
 # rows converted in the kernel, per-quad exponents; or prepared fragments,
-# per-row exponents) on the same inputs. The extreme per-quad ranges of
-# wild_x (2^44 across a row) are for the per-quad path only.
+# per-row exponents) on the same inputs, including wild_x's 2^44 range across
+# a row on every path and batch size: values far below the row maximum lose
+# bits on the per-row-exponent paths, but their terms are as small against
+# the magnitude sum, and every output stays within the bar.
 @pytest.mark.parametrize("mode", [("dma", "1"), ("dma", "1", "stage0"), ("dma", "0"), ("tiles", "1")])
 @pytest.mark.parametrize("fmt", ["i4h", "i4f", "mx"])
 @pytest.mark.parametrize("S", [1, 2, 3, 4, 8, 16])
 @pytest.mark.parametrize("O,I,xkind", [(256, 1024, "bf16"), (96, 768, "wild"), (128, 640, "outlier"),
                                        (40, 384, "f32"), (48, 200, "f32")])
 def test_gemv_kernel_paths(session, monkeypatch, mode, fmt, S, O, I, xkind):
-    if xkind == "wild" and (mode[:2] != ("dma", "1") or S > 4):
-        pytest.skip("per-row exponent: a 2^44 range inside one row is beyond the fragment path")
     monkeypatch.setenv("COLI_HIP_GEMV", mode[0])
     monkeypatch.setenv("COLI_HIP_XF32", mode[1])
     # one-row f32 GEMVs: the row staged once per workgroup (default) or per stage
