@@ -111,3 +111,38 @@ def test_kimi_prefill_512_full_size(session, fmt):
     x, W, b = make_router_inputs(rng, 512, D, E, K, 2, zipf=1.1)
     sample = rng.choice(512, 12, replace=False)
     run_layer(session, layer, x, W, b, K, 2, sample=sample)
+
+
+# configs[4] on the opt-in block-scaled MFMA (COLI_HIP_MX=1): the MXFP4 prefill
+# GEMM on v_mfma_scale_f32_16x16x128_f8f6f4 with e4m3 activation pieces. The
+# hardware sums each 128-column block of products with an error of about
+# 2^-15 of the block's magnitude sum, so the bound is 2e-4 of the magnitude sum
+# of the layer output (not the 1e-3 north-star metric, which it can miss on
+# outputs that cancel); the routing stays bit-exact. Prints the distribution
+# of the north-star metric.
+def test_kimi_prefill_512_block_scaled_mfma(session, monkeypatch):
+    monkeypatch.setenv("COLI_HIP_MX", "1")
+    rng = np.random.default_rng(5007)
+    D, I, E, K = 7168, 2048, 384, 8
+    layer = Layer(rng, 7, D, I, E, distinct=6)
+    x, W, b = make_router_inputs(rng, 512, D, E, K, 2, zipf=1.1)
+    rows = rng.choice(512, 16, replace=False)
+    m, hs = create(session, layer, W, b, K, 2)
+    try:
+        out, idx, w, keff = forward(session, m, x, K)
+    finally:
+        session.b.hip_moe_free(m)
+        free_handles(session, hs)
+    ri, rw, rk = cref.route(cref.matmul_f32(x, W), K, 2, bias=b)
+    assert np.array_equal(idx, ri) and np.array_equal(keff, rk)
+    _, _, _, ref, mag = moe_reference(layer, x[rows], W, b, K, 2)
+    got = out[rows].astype(np.float64)
+    assert np.isfinite(got).all()
+    err_mag = np.abs(got - ref) / mag
+    ns = rel_err(out[rows], ref, mag)
+    absref = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+    print(f"\nblock-scaled MFMA, Kimi 512-token layer, {rows.size} rows x {D} outputs: "
+          f"|err|/sum|t| max {err_mag.max():.3g}; north-star metric median {np.median(ns):.3g} "
+          f"p99 {np.quantile(ns, 0.99):.3g} max {ns.max():.3g} (> 1e-3: {np.mean(ns > 1e-3) * 100:.3f} %); "
+          f"|err|/|ref| median {np.median(absref):.3g} p99 {np.quantile(absref, 0.99):.3g}")
+    assert err_mag.max() <= 2e-4
