@@ -99,7 +99,11 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
             src[k] = (const _Float16 *)a.zero;
             sstep[k] = 0;
         }
-        dst[k] = hl * 16384 + (((m * 4 + j) * 4 + ks) * 16 + b) * 16;
+        // the 16 chunks of one row sit on 16 consecutive lanes: their slots are
+        // XOR-swizzled by the chunk (f = 4 j + ks) so those lanes write 16
+        // different bank groups, and the MFMA read below (16 rows of one
+        // chunk) stays conflict-free
+        dst[k] = hl * 16384 + (((m * 4 + j) * 4 + ks) * 16 + (b ^ f)) * 16;
     }
     // Activation staging ring: quad q's fragments are read into registers two
     // iterations ahead (slot q % 3) and written to LDS one iteration ahead, so
@@ -135,7 +139,8 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
 #pragma unroll
             for (int m = 0; m < 4; m++) {
                 if (m >= nm) break;
-                const unsigned fo = buf * BUF + ((((m * 4 + j) * 4 + (lane >> 4)) * 16 + (lane & 15)) * 16);
+                const unsigned fo =
+                    buf * BUF + ((((m * 4 + j) * 4 + (lane >> 4)) * 16 + ((lane & 15) ^ (4 * j + (lane >> 4)))) * 16);
                 const half8v xh = *(const half8v *)(lds + fo);
                 half8v xl = xh;
                 if (use_lo) xl = *(const half8v *)(lds + 16384 + fo);
