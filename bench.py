@@ -419,6 +419,7 @@ class Bench:
             if B >= 64:
                 flops = 2.0 * 3 * D * I * (B * K + (B if shared else 0))
                 rec["max_rows_per_expert"] = int(max(int(l.max()) for l in loads))
+                rec["row_tiles_64"] = round(float(np.mean([int(np.sum((l + 63) // 64)) for l in loads])), 1)
                 rec["mfma_TFLOPs"] = round(flops * n_steps / gpu_ms / 1e9, 1)
                 rec["mfma_frac_of_fp16_peak"] = round(flops * n_steps / gpu_ms / 1e9 / 2500.0, 4)
             result[f"B{B}" + ("_per_token" if per_token else "")] = rec

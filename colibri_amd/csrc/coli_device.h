@@ -19,6 +19,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // in-order counter the software pipeline relies on.
 #define GPTR(T, p) ((const __attribute__((address_space(1))) T *)(const void *)(p))
 
+typedef __attribute__((address_space(3))) void lds_void;
+// LDS written by the DMA is invisible to the compiler's memory model: read it
+// through volatile pointers so no read is folded or reordered across a wait.
+#define LDS_RD(T, p) (*(const volatile __attribute__((address_space(3))) T *)(lds_void *)(p))
+#define LDS_WR(T, p, v) (*(volatile __attribute__((address_space(3))) T *)(lds_void *)(p) = (v))
+
 // A pointer every lane of the wave holds, moved to scalar registers (values
 // read from memory by a vector load otherwise stay in VGPRs, and so would all
 // address arithmetic derived from them).
@@ -175,3 +181,35 @@ __device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiP
         }
     }
 }
+
+// ---- LDS DMA rings (gemv_dma.hip, gemm.hip) ----
+// Scale bytes of one tile quad: 16 rows x 4 groups of fp16 / f32 / e8m0.
+template <int KIND> struct ScaleGeom {
+    static constexpr int kBytes = ScaleRegs<KIND>::kTileBytes;   // 128 / 256 / 64
+    static constexpr int kLanes = kBytes / 4;                      // dword lanes per tile
+    static constexpr int kPerInst = 64 / kLanes;                   // tiles per dword DMA
+};
+
+template <int KIND>
+__device__ __forceinline__ void scale_from_lds(ScaleRegs<KIND> &s, const uint8_t *p, int r16) {
+    if constexpr (KIND == COLI_KIND_I4_H) s.v = LDS_RD(u32x2, p + r16 * 8);
+    else if constexpr (KIND == COLI_KIND_I4_F) s.v = LDS_RD(floatx4, p + r16 * 16);
+    else s.v = LDS_RD(uint32_t, p + r16 * 4);
+}
+
+// Wait until at most `pend` (0 .. PD-2) stages of L loads are still in flight.
+template <int L, int PD>
+__device__ __forceinline__ void dma_wait_tail(int pend) {
+#define COLI_WT(k)                                                         \
+    if (pend == k) {                                                       \
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(k * L) : "memory");       \
+        return;                                                            \
+    }
+    if constexpr (PD > 5) { COLI_WT(4) }
+    if constexpr (PD > 4) { COLI_WT(3) }
+    if constexpr (PD > 3) { COLI_WT(2) }
+    if constexpr (PD > 2) { COLI_WT(1) }
+#undef COLI_WT
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+

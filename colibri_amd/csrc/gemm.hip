@@ -6,29 +6,53 @@
 //
 // Work item = (problem, 64-row tile, output block). A workgroup of
 // COLI_GM_WAVES waves owns 2 row tiles per wave (DUAL: the gate tile and the up
-// tile of the same 16 rows, SwiGLU in the epilogue) over the full K:
-//  * each wave streams its own weight tiles through a 3-stage register ring;
-//  * the 64 rows' activation fragments (fp16 hi + lo of x * 2^-E, built by
-//    coli_prep_frag) are staged per 128-column quad into LDS, double-buffered,
-//    and read back in the MFMA A-operand order (conflict-free 16-byte lanes);
-//  * each 32-column group is one v_mfma_f32_16x16x32_f16 per (row tile,
-//    16-row subtile), its result scaled by the group scale and accumulated.
-// The unpacked B operand of a group is reused by the 4 row subtiles.
+// tile of the same 16 rows, SwiGLU in the epilogue) over the full K, one
+// 128-column quad per step:
+//  * every load of the main loop is an LDS DMA into a ring of PD stages: each
+//    wave's two weight tiles and their scales (private to the wave), and the
+//    quad's activation fragments of the 64 rows (fp16 hi + lo of x * 2^-E,
+//    built by coli_prep_frag; shared by the workgroup, each wave fetching two
+//    (hi) or four (hi + lo) of the 16 chunks). No load of the loop writes a
+//    register, so the compiler inserts no wait of its own: the loop waits with
+//    exact s_waitcnt vmcnt(N) for its oldest stage and synchronizes with a
+//    bare s_barrier (the fence of __syncthreads() would drain the ring). The
+//    activations ride in the same ring as the weights, as deep: loads retire
+//    in order, so a shallower activation ring would retire the weights with it;
+//  * the chunks are laid out in the MFMA A-operand order (lane l of a DMA
+//    fetches the 16 B lane l of the MFMA reads), so the reads are free of bank
+//    conflicts; chunks of dead 16-row subtiles re-read the tile's last row (one
+//    cache line), which keeps the count of loads per stage fixed;
+//  * each 32-column group is one v_mfma_f32_16x16x32_f16 per (weight tile,
+//    live 16-row subtile) -- two with the lo fragments -- its result scaled by
+//    the group scale and accumulated in f32. The unpacked B operand of a group
+//    is reused by the 4 row subtiles.
+// The ring is 4 stages deep when no lo part is set (the common case of
+// activations exact in fp16 after the row exponent), 3 with lo parts.
+#include <type_traits>
+
 #include "coli_device.h"
 
+// per-wave weight slot: 2 tiles + their scales (one or two dword DMAs)
 template <int KIND>
-struct GmStage {
-    u32x4 w[2];
-    ScaleRegs<KIND> sc[2];
+struct GmGeom {
+    static constexpr int kScaleInst = (2 + ScaleGeom<KIND>::kPerInst - 1) / ScaleGeom<KIND>::kPerInst;
+    static constexpr int kWSlot = 2 * COLI_TILE_BYTES + kScaleInst * 256;
+    static constexpr int kActHi = 16384;   // 64 rows x 128 columns x fp16
+    static constexpr int kPdHi = 4, kPdLo = 3;
+    static constexpr int bytes(bool lo) {
+        return (lo ? kPdLo : kPdHi) * ((lo ? 2 : 1) * kActHi + COLI_GM_WAVES * kWSlot);
+    }
+    static constexpr int kLds = bytes(true) > bytes(false) ? bytes(true) : bytes(false);
 };
+static_assert(GmGeom<COLI_KIND_I4_F>::kLds <= 160 * 1024, "ring exceeds the LDS of a CU");
 
 template <int KIND, bool DUAL>
 __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmArgs a) {
+    using G = GmGeom<KIND>;
+    using SG = ScaleGeom<KIND>;
     constexpr int W = COLI_GM_WAVES;
     constexpr int R = 2;                 // weight tiles per wave
     constexpr int RT = DUAL ? 1 : 2;     // distinct output row tiles per wave
-    constexpr int PD = 3;
-    constexpr int BUF = 32768;           // one staging buffer: hi 16 KiB + lo 16 KiB
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     // readfirstlane: the wave index is wave-uniform, so everything derived from it
     // (tile indices, validity, base pointers) stays in scalar registers.
@@ -47,132 +71,137 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
 
     int rt[R];
     bool live[R];
-    const uint8_t *wb[R];
-    const void *sb[R];
-    size_t tbase[R];
-    int tstep[R];
+    const uint8_t *wr[R], *sr[R];   // tile (rt, 0) of the wave's weights and scales
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const int rr = DUAL ? 0 : r;
         rt[r] = (rb * W + wave) * RT + rr;
         live[r] = rt[r] < a.nrt;
         const bool second = DUAL && r == 1;
-        wb[r] = live[r] ? (second ? pr.w1 : pr.w0) : a.zero;
-        sb[r] = live[r] ? (second ? pr.s1 : pr.s0) : (const void *)a.zero;
-        tbase[r] = live[r] ? (size_t)rt[r] * a.nq : 0;
-        tstep[r] = live[r] ? 1 : 0;
+        const uint8_t *w = (const uint8_t *)(second ? pr.w1 : pr.w0);
+        const uint8_t *sc = (const uint8_t *)(second ? pr.s1 : pr.s0);
+        // a dead tile re-reads tile (0, q) of the problem: the count of loads
+        // stays fixed and no address is hammered by every quad
+        const size_t t0 = live[r] ? (size_t)rt[r] * a.nq : 0;
+        wr[r] = w + t0 * COLI_TILE_BYTES;
+        sr[r] = sc + t0 * SG::kBytes;
     }
-    auto load_w = [&](GmStage<KIND> &sg, int q) {
-        const bool valid = q < a.nq;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const size_t tq = valid ? tbase[r] + (size_t)q * tstep[r] : 0;
-            const uint8_t *w = valid ? wb[r] : a.zero;
-            const void *sp = valid ? sb[r] : (const void *)a.zero;
-            sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + tq * COLI_TILE_BYTES) + lane);
-            sg.sc[r].load(sp, tq, lane & 15);
-        }
-    };
-    GmStage<KIND> st[PD];
-    load_w(st[0], 0);
-    load_w(st[1], 1);
-
     const bool use_lo = *a.haslo >= a.lo_gen;   // >=: stays correct under graph replay
-    // Staging assignment: 2048 chunks of 16 B per quad (64 rows x 16 hi + 16
-    // lo fragments); thread t takes chunks t + 512 k, all of one half (hi or
-    // lo, t & 16), so the lo threads idle when no lo part is non-zero.
-    const _Float16 *src[4];
-    int sstep[4];
-    unsigned dst[4];
-    const int hl = (threadIdx.x >> 4) & 1;
-    const bool stager = !hl || use_lo;
+    const int nm = (nrows + 15) >> 4;           // live 16-row subtiles
+
+    // Activation chunks of this wave: c = wave + W k (m = c / 4, j = c % 4);
+    // lane l fetches row 16 m + (l & 15) (clamped to the tile's last row),
+    // columns 32 j + 8 (l >> 4) .. + 7.
+    static_assert(W == 8, "the chunk assignment is written for 8 waves");
+    int xoff[2];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int c = threadIdx.x + 64 * W * k;
-        const int r = c >> 5, f = c & 15, j = f >> 2, ks = f & 3, m = r >> 4, b = r & 15;
-        if (r < nrows) {
-            const int br = pr.xrow_off + m0 + r;
-            const int fr = a.xrows ? a.xrows[br] : br;
-            src[k] = (hl ? a.xlo : a.xhi) + (size_t)fr * a.xstride + f * 8;
-            sstep[k] = 128;
-        } else {
-            src[k] = (const _Float16 *)a.zero;
-            sstep[k] = 0;
-        }
-        // the 16 chunks of one row sit on 16 consecutive lanes: their slots are
-        // XOR-swizzled by the chunk (f = 4 j + ks) so those lanes write 16
-        // different bank groups, and the MFMA read below (16 rows of one
-        // chunk) stays conflict-free
-        dst[k] = hl * 16384 + (((m * 4 + j) * 4 + ks) * 16 + (b ^ f)) * 16;
+    for (int k = 0; k < 2; k++) {
+        const int r = min(16 * ((wave >> 2) + 2 * k) + (lane & 15), nrows - 1);
+        const int br = pr.xrow_off + m0 + r;
+        const int fr = a.xrows ? a.xrows[br] : br;
+        xoff[k] = fr * a.xstride + 32 * (wave & 3) + 8 * (lane >> 4);
     }
-    // Activation staging ring: quad q's fragments are read into registers two
-    // iterations ahead (slot q % 3) and written to LDS one iteration ahead, so
-    // their L2 latency is covered by a full iteration of math.
-    u32x4 creg[PD][4];
-    auto gload = [&](u32x4 (&cr)[4], int q) {
-        if (!stager) return;
-#pragma unroll
-        for (int k = 0; k < 4; k++) cr[k] = *GPTR(u32x4, src[k] + (size_t)q * sstep[k]);
-    };
-    auto swrite = [&](const u32x4 (&cr)[4], int buf) {
-        if (!stager) return;
-#pragma unroll
-        for (int k = 0; k < 4; k++) *(u32x4 *)(lds + buf * BUF + dst[k]) = cr[k];
-    };
+    // the ring is written behind the compiler's back: let it escape, so the
+    // "memory" clobbers of the waits below force fresh reads (plain loads: no
+    // read moves across a wait or barrier, and the compiler may batch the
+    // reads of one step)
+    asm volatile("" ::"v"(lds) : "memory");
 
     floatx4 acc[R][4];
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int m = 0; m < 4; m++) acc[r][m] = (floatx4){0.f, 0.f, 0.f, 0.f};
-    const int nm = (nrows + 15) >> 4;   // live 16-row subtiles
-    auto compute = [&](const GmStage<KIND> &sg, int buf) {
+
+    auto run = [&](auto lo_tag) {
+        constexpr bool LO = decltype(lo_tag)::value;
+        constexpr int PD = LO ? G::kPdLo : G::kPdHi;
+        constexpr int ACT = (LO ? 2 : 1) * G::kActHi;   // activation bytes of one stage
+        constexpr int L = R + G::kScaleInst + (LO ? 4 : 2);   // DMA instructions per wave and stage
+        uint8_t *const wring = lds + PD * ACT + wave * PD * G::kWSlot;
+        auto issue = [&](int q, int slot) {
+            uint8_t *ws = wring + slot * G::kWSlot;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            half8v bw[R];
-            float scl[R];
+            for (int r = 0; r < R; r++)
+                __builtin_amdgcn_global_load_lds((const void *)(wr[r] + (size_t)q * COLI_TILE_BYTES + lane * 16),
+                                                 (lds_void *)(ws + r * COLI_TILE_BYTES), 16, 0, 0);
+#pragma unroll
+            for (int k = 0; k < G::kScaleInst; k++) {
+                const int r = min(R - 1, k * SG::kPerInst + lane / SG::kLanes);
+                const uint8_t *base = r == 0 ? sr[0] : sr[1];
+                __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)q * SG::kBytes + (lane % SG::kLanes) * 4),
+                                                 (lds_void *)(ws + 2 * COLI_TILE_BYTES + k * 256), 4, 0, 0);
+            }
+            uint8_t *xs = lds + slot * ACT;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const size_t o = (size_t)xoff[k] + (size_t)q * 128;
+                uint8_t *dst = xs + (wave + W * k) * 1024;
+                __builtin_amdgcn_global_load_lds((const void *)(a.xhi + o), (lds_void *)dst, 16, 0, 0);
+                if constexpr (LO)
+                    __builtin_amdgcn_global_load_lds((const void *)(a.xlo + o), (lds_void *)(dst + G::kActHi), 16,
+                                                     0, 0);
+            }
+        };
+        auto compute = [&](int slot) {
+            const uint8_t *ws = wring + slot * G::kWSlot;
+            const uint8_t *xs = lds + slot * ACT;
+            u32x4 w[R];
+            ScaleRegs<KIND> sc[R];
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                bw[r] = unpack_b<KIND>(sg.w[r][j]);
-                scl[r] = sg.sc[r].get(j);
+                w[r] = *(const u32x4 *)(ws + r * COLI_TILE_BYTES + lane * 16);
+                sc[r].v = *(const decltype(sc[r].v) *)(ws + 2 * COLI_TILE_BYTES + r * SG::kBytes +
+                                                       (lane & 15) * sizeof(sc[r].v));
             }
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                if (m >= nm) break;
-                const unsigned fo =
-                    buf * BUF + ((((m * 4 + j) * 4 + (lane >> 4)) * 16 + ((lane & 15) ^ (4 * j + (lane >> 4)))) * 16);
-                const half8v xh = *(const half8v *)(lds + fo);
-                half8v xl = xh;
-                if (use_lo) xl = *(const half8v *)(lds + 16384 + fo);
+            for (int j = 0; j < 4; j++) {
+                half8v bw[R];
+                float scl[R];
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[r], (floatx4){0.f, 0.f, 0.f, 0.f},
-                                                                      0, 0, 0);
-                    if (use_lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[r], d, 0, 0, 0);
+                    bw[r] = unpack_b<KIND>(w[r][j]);
+                    scl[r] = sc[r].get(j);
+                }
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[r][m][i] = fmaf(d[i], scl[r], acc[r][m][i]);
+                for (int m = 0; m < 4; m++) {
+                    if (m >= nm) break;
+                    const uint8_t *fo = xs + (m * 4 + j) * 1024 + lane * 16;
+                    const half8v xh = *(const half8v *)fo;
+                    half8v xl = xh;
+                    if constexpr (LO) xl = *(const half8v *)(fo + G::kActHi);
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[r], (floatx4){0.f, 0.f, 0.f, 0.f},
+                                                                          0, 0, 0);
+                        if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[r], d, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[r][m][i] = fmaf(d[i], scl[r], acc[r][m][i]);
+                    }
                 }
             }
+        };
+        // Step q: wait for this wave's stage q (at most min(PD - 2, nq - 1 - q)
+        // younger stages may stay in flight), barrier (every wave's chunks of
+        // stage q have landed, and every wave is done with quad q - 1, whose
+        // slot the next issue reuses), issue stage q + PD - 1, compute quad q.
+        const int nq = a.nq;
+#pragma unroll
+        for (int i = 0; i < PD - 1; i++)
+            if (i < nq) issue(i, i);
+        int slot = 0;
+        for (int q = 0; q < nq; q++) {
+            dma_wait_tail<L, PD>(min(PD - 2, nq - 1 - q));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (q + PD - 1 < nq) issue(q + PD - 1, slot == 0 ? PD - 1 : slot - 1);
+            compute(slot);
+            slot = slot == PD - 1 ? 0 : slot + 1;
         }
     };
-
-    static_assert(PD == 3, "the staging ring below is written for three slots");
-    gload(creg[0], 0);
-    if (a.nq > 1) gload(creg[1], 1);
-    swrite(creg[0], 0);
-    __syncthreads();
-    for (int q0 = 0; q0 < a.nq; q0 += PD) {
-#pragma unroll
-        for (int u = 0; u < PD; u++) {
-            const int q = q0 + u;
-            if (q >= a.nq) break;
-            if (q + 2 < a.nq) gload(creg[(u + 2) % PD], q + 2);
-            load_w(st[(u + PD - 1) % PD], q + PD - 1);
-            compute(st[u], q & 1);
-            if (q + 1 < a.nq) swrite(creg[(u + 1) % PD], (q + 1) & 1);
-            __syncthreads();
-        }
-    }
+    if (use_lo) run(std::true_type{});
+    else run(std::false_type{});
 
     // epilogue: batch row m0 + 16 m + 4 (lane / 16) + i, output row rt * 16 + lane % 16
 #pragma unroll
@@ -201,7 +230,7 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
 template <int KIND>
 static hipError_t launch_gemm_kind(const ColiGemmArgs &a, bool dual, hipStream_t st) {
     const dim3 grid((unsigned)a.n_mt * a.rb_per_prob), block(64 * COLI_GM_WAVES);
-    const size_t shm = 2 * 32768;
+    const size_t shm = GmGeom<KIND>::kLds;
     if (dual) hipLaunchKernelGGL((coli_gemm_tiles<KIND, true>), grid, block, shm, st, a);
     else hipLaunchKernelGGL((coli_gemm_tiles<KIND, false>), grid, block, shm, st, a);
     return hipGetLastError();
