@@ -317,6 +317,13 @@ static int fill_tensor(DevCtx *ctx, ColiCudaTensor *t, const void *weights, cons
         (!w_on_device && !hip_check(hipMemcpy(ctx->stage_w.p, weights, wsrc, hipMemcpyHostToDevice), "tensor upload")) ||
         !hip_check(hipMemcpy(ctx->stage_s.p, scales_src, scale_src_bytes, hipMemcpyHostToDevice), "scale upload"))
         return 0;
+    if (t->kind == COLI_KIND_FP4) {
+        // 0.5 * 2^(e-127) >= 2^-14 and 6 * 2^(e-127) <= 65504
+        const uint8_t *e8 = (const uint8_t *)scales_src;
+        int fold = 1;
+        for (size_t i = 0; i < scale_src_bytes && fold; i++) fold = e8[i] >= 114 && e8[i] <= 140;
+        t->e8_fold = fold;
+    }
     const uint8_t *wsrc_dev = w_on_device ? (const uint8_t *)weights : (const uint8_t *)ctx->stage_w.p;
     if (!hip_check(coli_launch_repack(t, wsrc_dev, ctx->stage_s.p, ctx->stream),
                 "tile repack"))

@@ -99,6 +99,16 @@ __device__ __forceinline__ half8v unpack_b(uint32_t w) {
     }
 }
 
+// e2m1 nibbles times a power-of-two scale, converted exactly to fp16 when the
+// products are normal fp16 values (scales 2^-13 .. 2^13).
+__device__ __forceinline__ half8v unpack_fp4_scaled(uint32_t w, float s) {
+    half2v a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0);
+    half2v b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1);
+    half2v c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2);
+    half2v d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3);
+    return (half8v){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // Scale of group j (0..3) of the lane's row, from the per-tile-quad scale word(s).
 template <int KIND> struct ScaleRegs;
 template <> struct ScaleRegs<COLI_KIND_I4_H> {

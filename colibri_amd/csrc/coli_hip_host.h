@@ -182,7 +182,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
 // One grouped GEMM over a device work list of (problem << 16 | 64-row tile).
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
-             const int *xrows_dev, float *out, int ldo, float swiglu_limit = 0.0f);
+             const int *xrows_dev, float *out, int ldo, float swiglu_limit = 0.0f, bool fold = false);
 
 // Router logits of S rows into `part`; returns the number of column-chunk
 // partials the selection must add, or 0 on failure.

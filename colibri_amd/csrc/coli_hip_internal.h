@@ -46,6 +46,8 @@ struct ColiCudaTensor {
     size_t accounted;            // bytes charged to the device statistics
     struct ColiProb *desc;       // device: 64 descriptors, entry s-1 = this matrix on s rows
     void *sc_unit;               // fmt=2 int8-activation path: unit group scales (made on first use)
+    int e8_fold;                 // MXFP4: every e8m0 byte in [114, 140], so each e2m1 value times its
+                                 // scale is a normal fp16 (the GEMM folds the scale into the operand)
 };
 
 // One GEMV problem: a matrix (or a gate/up pair) applied to a set of batch rows.
@@ -109,6 +111,7 @@ struct ColiGemmArgs {
     float *out;
     int ldo;
     float swiglu_limit;       // > 0: DeepSeek-V4 clamped SwiGLU in the DUAL epilogue
+    int fold;                 // MXFP4, every matrix e8_fold: scales folded into the unpacked operand
 };
 
 // Grouped MXFP4 GEMM on the block-scaled MFMA (gemm_mx.hip): activations as

@@ -313,7 +313,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
 // probs_dev.
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,
-             const int *xrows_dev, float *out, int ldo, float swiglu_limit) {
+             const int *xrows_dev, float *out, int ldo, float swiglu_limit, bool fold) {
     if (n_mt <= 0) return 1;
     FragSet &f = ctx->frag[set];
     if (!(kind == COLI_KIND_FP4 && mx_gemm_enabled()) && !flush_frags(ctx, set)) return 0;
@@ -366,6 +366,7 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.out = out;
     a.ldo = ldo;
     a.swiglu_limit = swiglu_limit;
+    a.fold = fold && kind == COLI_KIND_FP4;
     return hip_check(coli_launch_gemm(kind, dual ? 1 : 0, &a, ctx->stream), "gemm launch");
 }
 
@@ -399,9 +400,12 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
     std::vector<int> dual_kind(count, -1);
     bool need_x[2] = {false, false}, need_h[2] = {false, false}, need_gu = false;
     int max_rows = 0;
+    bool fold = true;   // every MXFP4 matrix of the call allows the folded scales
     for (int c = 0; c < count; c++) {
         const Member &mm = m[c];
         max_rows = std::max(max_rows, mm.rows);
+        for (const ColiCudaTensor *t : {mm.g, mm.u, mm.d})
+            if (t->kind == COLI_KIND_FP4 && !t->e8_fold) fold = false;
         bool tiled_g = mm.g->kind != COLI_KIND_GENERIC, tiled_u = mm.u->kind != COLI_KIND_GENERIC;
         if (tiled_g && tiled_u && mm.g->kind == mm.u->kind) dual_kind[c] = mm.g->kind;
         else need_gu = true;
@@ -491,7 +495,7 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
         const Launch &L = launches[l];
         if (use_gemm)
             return run_gemm(ctx, L.kind, dual, pdev + L.first, L.n, nullptr, mtdev + mt_first[l], nullptr,
-                            mt_count[l], L.nrt, L.nq, L.O, L.set, nullptr, L.out, L.ldo);
+                            mt_count[l], L.nrt, L.nq, L.O, L.set, nullptr, L.out, L.ldo, 0.0f, fold);
         return run_gemv(ctx, L.kind, dual, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set,
                         nullptr, L.out, L.ldo);
     };

@@ -25,7 +25,10 @@
 //  * each 32-column group is one v_mfma_f32_16x16x32_f16 per (weight tile,
 //    live 16-row subtile) -- two with the lo fragments -- its result scaled by
 //    the group scale and accumulated in f32. The unpacked B operand of a group
-//    is reused by the 4 row subtiles.
+//    is reused by the 4 row subtiles. MXFP4 matrices whose e8m0 scales keep
+//    every e2m1 value times its scale a normal fp16 (fold) take the scale into
+//    the unpack instead (exact) and accumulate inside the MFMA: no per-group
+//    VALU work beyond the conversion.
 // The ring is 4 stages deep when no lo part is set (the common case of
 // activations exact in fp16 after the row exponent), 3 with lo parts.
 #include <type_traits>
@@ -113,8 +116,9 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
 #pragma unroll
         for (int m = 0; m < 4; m++) acc[r][m] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
-    auto run = [&](auto lo_tag) {
+    auto run = [&](auto lo_tag, auto fold_tag) {
         constexpr bool LO = decltype(lo_tag)::value;
+        constexpr bool FOLD = decltype(fold_tag)::value;
         constexpr int PD = LO ? G::kPdLo : G::kPdHi;
         constexpr int ACT = (LO ? 2 : 1) * G::kActHi;   // activation bytes of one stage
         constexpr int L = R + G::kScaleInst + (LO ? 4 : 2);   // DMA instructions per wave and stage
@@ -160,8 +164,9 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
                 float scl[R];
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    bw[r] = unpack_b<KIND>(w[r][j]);
                     scl[r] = sc[r].get(j);
+                    if constexpr (FOLD) bw[r] = unpack_fp4_scaled(w[r][j], scl[r]);
+                    else bw[r] = unpack_b<KIND>(w[r][j]);
                 }
 #pragma unroll
                 for (int m = 0; m < 4; m++) {
@@ -172,11 +177,18 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
                     if constexpr (LO) xl = *(const half8v *)(fo + G::kActHi);
 #pragma unroll
                     for (int r = 0; r < R; r++) {
-                        floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[r], (floatx4){0.f, 0.f, 0.f, 0.f},
-                                                                          0, 0, 0);
-                        if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[r], d, 0, 0, 0);
+                        if constexpr (FOLD) {
+                            // the operand carries the group scale: accumulate in the MFMA
+                            acc[r][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[r], acc[r][m], 0, 0, 0);
+                            if constexpr (LO)
+                                acc[r][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[r], acc[r][m], 0, 0, 0);
+                        } else {
+                            floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[r],
+                                                                              (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[r], d, 0, 0, 0);
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[r][m][i] = fmaf(d[i], scl[r], acc[r][m][i]);
+                            for (int i = 0; i < 4; i++) acc[r][m][i] = fmaf(d[i], scl[r], acc[r][m][i]);
+                        }
                     }
                 }
             }
@@ -200,8 +212,20 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
             slot = slot == PD - 1 ? 0 : slot + 1;
         }
     };
-    if (use_lo) run(std::true_type{});
-    else run(std::false_type{});
+    if constexpr (KIND == COLI_KIND_FP4) {
+        if (a.fold) {
+            if (use_lo) run(std::true_type{}, std::true_type{});
+            else run(std::false_type{}, std::true_type{});
+        } else if (use_lo) {
+            run(std::true_type{}, std::false_type{});
+        } else {
+            run(std::false_type{}, std::false_type{});
+        }
+    } else if (use_lo) {
+        run(std::true_type{}, std::false_type{});
+    } else {
+        run(std::false_type{}, std::false_type{});
+    }
 
     // epilogue: batch row m0 + 16 m + 4 (lane / 16) + i, output row rt * 16 + lane % 16
 #pragma unroll

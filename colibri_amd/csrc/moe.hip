@@ -39,6 +39,7 @@ struct ColiHipMoe {
     int device;
     ColiHipMoeConfig cfg;
     int kind;                 // storage kind shared by every expert matrix
+    std::vector<const ColiCudaTensor *> mats;   // every expert matrix (e8_fold is read per forward)
     int S_cap;
     float *rw = nullptr, *rb = nullptr;
     ColiProb *tab = nullptr;  // [E (+1 shared)][2]: dual template, down template
@@ -469,6 +470,7 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
     int kind = gates[0] ? gates[0]->kind : -1;
     if (kind < 0 || kind == COLI_KIND_GENERIC) return 0;
     int n = c.E + (c.has_shared ? 1 : 0);
+    std::vector<const ColiCudaTensor *> mats;
     std::vector<ColiProb> tab(2 * (c.E + 1));
     for (int e = 0; e < n; e++) {
         ColiCudaTensor *g = e < c.E ? gates[e] : sg, *u = e < c.E ? ups[e] : su, *d = e < c.E ? downs[e] : sd;
@@ -476,6 +478,9 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
             g->kind != kind || u->kind != kind || d->kind != kind || g->I != c.D || u->I != c.D || g->O != c.I ||
             u->O != c.I || d->I != c.I || d->O != c.D)
             return 0;
+        mats.push_back(g);
+        mats.push_back(u);
+        mats.push_back(d);
         tab[2 * e] = {g->w, g->sc, u->w, u->sc, 0, 0, 0, 0};
         tab[2 * e + 1] = {d->w, d->sc, nullptr, nullptr, 0, 0, 0, 0};
     }
@@ -483,6 +488,7 @@ extern "C" int coli_hip_moe_create(ColiHipMoe **out, int device, const ColiHipMo
     m->device = device;
     m->cfg = c;
     m->kind = kind;
+    m->mats = std::move(mats);
     m->S_cap = 0;
     size_t rwb = (size_t)c.E * c.D * sizeof(float);
     int ok = hip_check(hipMalloc((void **)&m->rw, rwb), "router weights") &&
@@ -632,10 +638,14 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
         if (!hip_check(hipGetLastError(), "moe union")) return 0;
     }
     // 5. gate/up + SwiGLU over the union, 6. hidden fragments, 7. down
+    // (MXFP4 scales folded into the operand when every matrix allows it;
+    // re-checked per call, since tensor_update may change the scales)
+    bool fold = gemm && m->kind == COLI_KIND_FP4;
+    for (size_t i = 0; fold && i < m->mats.size(); i++) fold = m->mats[i]->e8_fold != 0;
     const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
     if (gemm) {
         if (!run_gemm(ctx, m->kind, true, m->pdual, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_i, nq_d,
-                      c.I, fx, m->xrows, m->h, c.I, c.swiglu_limit))
+                      c.I, fx, m->xrows, m->h, c.I, c.swiglu_limit, fold))
             return 0;
     } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I,
                          nullptr, c.swiglu_limit)) {
@@ -646,7 +656,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
         return 0;
     if (gemm) {
         if (!run_gemm(ctx, m->kind, false, m->pdown, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_d, nq_i,
-                      c.D, fh, nullptr, m->y, c.D))
+                      c.D, fh, nullptr, m->y, c.D, 0.0f, fold))
             return 0;
     } else if (!run_gemv(ctx, m->kind, false, m->pdown, P, m->state, nrt_d, nq_i, c.D, S, fh, nullptr, m->y, c.D)) {
         return 0;

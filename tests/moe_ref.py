@@ -53,8 +53,9 @@ class Layer:
     distinct: number of distinct weight sets, expert e using set e % distinct
     (full-size layers without full-size host and device memory)."""
 
-    def __init__(self, rng, fmt, D, I, E, shared=False, swiglu_limit=0.0, distinct=None):
+    def __init__(self, rng, fmt, D, I, E, shared=False, swiglu_limit=0.0, distinct=None, e8_range=(119, 123)):
         self.fmt, self.D, self.I, self.E = fmt, D, I, E
+        self.e8_range = e8_range   # MXFP4 scale exponents drawn from [lo, hi]
         self.swiglu_limit = swiglu_limit   # > 0: DeepSeek-V4 clamped SwiGLU
         n = E if distinct is None else min(E, distinct)
         sets = [self._expert(rng) for _ in range(n)]
@@ -69,9 +70,9 @@ class Layer:
             u = rand_i4(rng, I, D, 32)
             d = rand_i4(rng, D, I, 32)
         else:
-            g = rand_mxfp4(rng, I, D)
-            u = rand_mxfp4(rng, I, D)
-            d = rand_mxfp4(rng, D, I)
+            g = rand_mxfp4(rng, I, D, *self.e8_range)
+            u = rand_mxfp4(rng, I, D, *self.e8_range)
+            d = rand_mxfp4(rng, D, I, *self.e8_range)
         return g, u, d
 
     def gemv(self, mat, x, O, I):

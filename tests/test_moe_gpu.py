@@ -253,14 +253,19 @@ def test_pipe_router_ties_and_invalid(session, case):
         assert list(idx[3:]) == list(range(3, K))
 
 
-@pytest.mark.parametrize("fmt,lo", [(4, False), (7, False), (4, True), (7, True)])
-def test_expert_group_grouped_gemm(session, fmt, lo):
+@pytest.mark.parametrize("fmt,lo,e8", [(4, False, None), (7, False, None), (4, True, None), (7, True, None),
+                                        (7, False, (114, 140)), (7, True, (114, 140)), (7, False, (100, 150)),
+                                        (7, True, (100, 150))])
+def test_expert_group_grouped_gemm(session, fmt, lo, e8):
     """Members with more than 32 rows run the grouped GEMM (64-row tiles, LDS
     staged activations): ragged tiles (70 = 64 + 6, 129 = 2 x 64 + 1), a small
-    member in the same launch, bf16-exact and full f32 activations."""
-    rng = np.random.default_rng(300 + fmt + 10 * lo)
+    member in the same launch, bf16-exact and full f32 activations. MXFP4
+    scale exponents inside [114, 140] are folded into the unpacked operand
+    (both ends of that range are drawn); a wider range (100 .. 150) keeps the
+    per-group scaling."""
+    rng = np.random.default_rng(300 + fmt + 10 * lo + (e8[0] if e8 else 0))
     D, I = 384, 256
-    layer = Layer(rng, fmt, D, I, 3)
+    layer = Layer(rng, fmt, D, I, 3, e8_range=e8 or (119, 123))
     hs = layer.upload(session)
     rows = [70, 3, 129]
     x = rng.standard_normal((sum(rows), D)).astype(np.float32) if lo else rand_x(rng, sum(rows), D)
