@@ -87,10 +87,15 @@ struct ColiGemvArgs {
 };
 
 
-// Grouped GEMM (prefill): problems of many rows, tiled 64 rows x (COLI_GM_WAVES
-// waves x 2 row tiles) with the activation fragments staged in LDS.
+// Grouped GEMM (prefill): problems of many rows, tiled 64 rows x
+// COLI_GM_BLOCK_TILES row tiles (half as many gate/up pairs when dual) with
+// the activation fragments staged in LDS. COLI_GM_WAVES: the block-scaled
+// variant (gemm_mx.hip), 8 waves x 2 row tiles.
 #define COLI_GM_WAVES 8
+#define COLI_GM_BLOCK_TILES 16
+#ifndef COLI_GM_ROWS
 #define COLI_GM_ROWS 64
+#endif
 
 struct ColiGemmArgs {
     const ColiProb *prob;

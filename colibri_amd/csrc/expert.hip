@@ -353,7 +353,7 @@ int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.nrt = nrt;
     a.nq = nq;
     a.O = O;
-    const int tiles_per_block = COLI_GM_WAVES * (dual ? 1 : 2);
+    const int tiles_per_block = COLI_GM_BLOCK_TILES / (dual ? 2 : 1);
     a.rb_per_prob = (nrt + tiles_per_block - 1) / tiles_per_block;
     a.xrows = xrows_dev;
     a.xhi = (const _Float16 *)f.hi.p;

@@ -4,15 +4,15 @@
 // fmt=4 and fmt=7) with the weights read once per 64 rows instead of once per
 // 16.
 //
-// Work item = (problem, 64-row tile, output block). A workgroup of
-// COLI_GM_WAVES waves owns 2 row tiles per wave (DUAL: the gate tile and the up
-// tile of the same 16 rows, SwiGLU in the epilogue) over the full K, one
-// 128-column quad per step:
+// Work item = (problem, 64-row tile, output block of COLI_GM_BLOCK_TILES row
+// tiles). A workgroup of COLI_GM_W waves gives each wave R = COLI_GM_BLOCK_TILES
+// / COLI_GM_W weight tiles (DUAL: gate/up pairs of the same 16 output rows,
+// SwiGLU in the epilogue) over the full K, one 128-column quad per step:
 //  * every load of the main loop is an LDS DMA into a ring of PD stages: each
-//    wave's two weight tiles and their scales (private to the wave), and the
-//    quad's activation fragments of the 64 rows (fp16 hi + lo of x * 2^-E,
-//    built by coli_prep_frag; shared by the workgroup, each wave fetching two
-//    (hi) or four (hi + lo) of the 16 chunks). No load of the loop writes a
+//    wave's weight tiles and their scales (private to the wave), and the
+//    quad's activation fragments of the tile's rows (fp16 hi + lo of x * 2^-E,
+//    built by coli_prep_frag; shared by the workgroup, each wave fetching a
+//    fixed number of the 1 KiB chunks). No load of the loop writes a
 //    register, so the compiler inserts no wait of its own: the loop waits with
 //    exact s_waitcnt vmcnt(N) for its oldest stage and synchronizes with a
 //    bare s_barrier (the fence of __syncthreads() would drain the ring). The
@@ -20,42 +20,67 @@
 //    in order, so a shallower activation ring would retire the weights with it;
 //  * the chunks are laid out in the MFMA A-operand order (lane l of a DMA
 //    fetches the 16 B lane l of the MFMA reads), so the reads are free of bank
-//    conflicts; chunks of dead 16-row subtiles re-read the tile's last row (one
-//    cache line), which keeps the count of loads per stage fixed;
+//    conflicts; chunks of dead 16-row subtiles read the tile's last row (one
+//    cache line) into a trash slot, which keeps the count of loads per stage
+//    fixed;
+//  * the loop is specialized per (lo parts present, folded scales, live
+//    16-row subtiles NM): the stage holds only NM subtiles' activations, so
+//    short tiles (the common prefill case of a few rows per expert) stream
+//    through a deeper ring, and the MFMA schedule is straight-line code;
 //  * each 32-column group is one v_mfma_f32_16x16x32_f16 per (weight tile,
 //    live 16-row subtile) -- two with the lo fragments -- its result scaled by
 //    the group scale and accumulated in f32. The unpacked B operand of a group
-//    is reused by the 4 row subtiles. MXFP4 matrices whose e8m0 scales keep
+//    is reused by the row subtiles. MXFP4 matrices whose e8m0 scales keep
 //    every e2m1 value times its scale a normal fp16 (fold) take the scale into
 //    the unpack instead (exact) and accumulate inside the MFMA: no per-group
 //    VALU work beyond the conversion.
-// The ring is 4 stages deep when no lo part is set (the common case of
-// activations exact in fp16 after the row exponent), 3 with lo parts.
+// Measured limits: the LDS carries the DMA writes and every wave's operand
+// reads, and its capacity bounds the ring depth; more tiles per wave (fewer
+// activation reads) costs ring depth and occupancy and was slower.
 #include <type_traits>
+
+// waves per workgroup; each owns COLI_GM_BLOCK_TILES / COLI_GM_W weight tiles
+#ifndef COLI_GM_W
+#define COLI_GM_W 8
+#endif
 
 #include "coli_device.h"
 
-// per-wave weight slot: 2 tiles + their scales (one or two dword DMAs)
+// Ring geometry. A stage holds the activation chunks of the tile's live
+// 16-row subtiles (NM of them, 4 KiB each for the hi half, as much again for
+// lo) and each wave's weight tiles + scales; the ring takes as many stages as
+// the LDS of a CU holds (at most 6), so short tiles stream deeper. One 1 KiB
+// trash slot takes the DMAs of dead chunks (their count per wave stays fixed).
 template <int KIND>
 struct GmGeom {
-    static constexpr int kScaleInst = (2 + ScaleGeom<KIND>::kPerInst - 1) / ScaleGeom<KIND>::kPerInst;
-    static constexpr int kWSlot = 2 * COLI_TILE_BYTES + kScaleInst * 256;
-    static constexpr int kActHi = 16384;   // 64 rows x 128 columns x fp16
-    static constexpr int kPdHi = 4, kPdLo = 3;
-    static constexpr int bytes(bool lo) {
-        return (lo ? kPdLo : kPdHi) * ((lo ? 2 : 1) * kActHi + COLI_GM_WAVES * kWSlot);
+    static constexpr int kMt = COLI_GM_ROWS / 16;                 // 16-row subtiles per tile
+    static constexpr int kChunks = 4 * kMt;                        // 1 KiB activation chunks per stage half
+    static constexpr int kW = COLI_GM_W, kR = COLI_GM_BLOCK_TILES / COLI_GM_W;   // waves, tiles per wave
+    static constexpr int scale_inst(int rn) { return (rn + ScaleGeom<KIND>::kPerInst - 1) / ScaleGeom<KIND>::kPerInst; }
+    static constexpr int wslot(int rn) { return rn * COLI_TILE_BYTES + scale_inst(rn) * 256; }
+    static constexpr int kTrash = 0;                               // the trash slot, then the ring
+    static constexpr int kRing = 1024;
+    static constexpr int kLds = 159 * 1024;
+    static constexpr int act(int nm, bool lo) { return nm * 4096 * (lo ? 2 : 1); }
+    static constexpr int stage(int nm, bool lo, int rn) { return act(nm, lo) + kW * wslot(rn); }
+    static constexpr int pd(int nm, bool lo, int rn) {
+        return (kLds - kRing) / stage(nm, lo, rn) > 6 ? 6 : (kLds - kRing) / stage(nm, lo, rn);
     }
-    static constexpr int kLds = bytes(true) > bytes(false) ? bytes(true) : bytes(false);
+    // tiles per pass: all of the wave's tiles when three stages fit, else two
+    // passes over K of half as many (the activations are staged twice)
+    static constexpr int passes(int nm, bool lo) { return pd(nm, lo, kR) >= 3 ? 1 : 2; }
 };
-static_assert(GmGeom<COLI_KIND_I4_F>::kLds <= 160 * 1024, "ring exceeds the LDS of a CU");
+static_assert(GmGeom<COLI_KIND_I4_F>::pd(COLI_GM_ROWS / 16, true, GmGeom<COLI_KIND_I4_F>::kR / 2) >= 3,
+              "the ring needs three stages");
 
 template <int KIND, bool DUAL>
-__global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmArgs a) {
+__global__ __launch_bounds__(64 * COLI_GM_W) void coli_gemm_tiles(ColiGemmArgs a) {
     using G = GmGeom<KIND>;
     using SG = ScaleGeom<KIND>;
-    constexpr int W = COLI_GM_WAVES;
-    constexpr int R = 2;                 // weight tiles per wave
-    constexpr int RT = DUAL ? 1 : 2;     // distinct output row tiles per wave
+    constexpr int W = G::kW;
+    constexpr int R = G::kR;                  // weight tiles per wave
+    constexpr int RT = DUAL ? R / 2 : R;      // distinct output row tiles per wave
+    static_assert(W * R == COLI_GM_BLOCK_TILES && R % 2 == 0, "a block covers COLI_GM_BLOCK_TILES weight tiles");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     // readfirstlane: the wave index is wave-uniform, so everything derived from it
     // (tile indices, validity, base pointers) stays in scalar registers.
@@ -77,10 +102,10 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
     const uint8_t *wr[R], *sr[R];   // tile (rt, 0) of the wave's weights and scales
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const int rr = DUAL ? 0 : r;
+        const int rr = DUAL ? r >> 1 : r;   // DUAL: tiles 2i, 2i + 1 = gate, up of row tile i
         rt[r] = (rb * W + wave) * RT + rr;
         live[r] = rt[r] < a.nrt;
-        const bool second = DUAL && r == 1;
+        const bool second = DUAL && (r & 1);
         const uint8_t *w = (const uint8_t *)(second ? pr.w1 : pr.w0);
         const uint8_t *sc = (const uint8_t *)(second ? pr.s1 : pr.s0);
         // a dead tile re-reads tile (0, q) of the problem: the count of loads
@@ -95,11 +120,12 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
     // Activation chunks of this wave: c = wave + W k (m = c / 4, j = c % 4);
     // lane l fetches row 16 m + (l & 15) (clamped to the tile's last row),
     // columns 32 j + 8 (l >> 4) .. + 7.
-    static_assert(W == 8, "the chunk assignment is written for 8 waves");
-    int xoff[2];
+    constexpr int CPW = G::kChunks / W;   // chunks per wave and stage half
+    static_assert(G::kChunks % W == 0 && W % 4 == 0, "chunks must spread evenly over the waves");
+    int xoff[CPW];
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int r = min(16 * ((wave >> 2) + 2 * k) + (lane & 15), nrows - 1);
+    for (int k = 0; k < CPW; k++) {
+        const int r = min(16 * ((wave + W * k) >> 2) + (lane & 15), nrows - 1);
         const int br = pr.xrow_off + m0 + r;
         const int fr = a.xrows ? a.xrows[br] : br;
         xoff[k] = fr * a.xstride + 32 * (wave & 3) + 8 * (lane >> 4);
@@ -110,86 +136,122 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
     // reads of one step)
     asm volatile("" ::"v"(lds) : "memory");
 
-    floatx4 acc[R][4];
+    floatx4 acc[R][G::kMt];
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
-        for (int m = 0; m < 4; m++) acc[r][m] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < G::kMt; m++) acc[r][m] = (floatx4){0.f, 0.f, 0.f, 0.f};
 
-    auto run = [&](auto lo_tag, auto fold_tag) {
+    // One pass over K for the wave's tiles RB .. RB + RN - 1.
+    auto run = [&](auto lo_tag, auto fold_tag, auto nm_tag, auto rb_tag, auto rn_tag) {
         constexpr bool LO = decltype(lo_tag)::value;
         constexpr bool FOLD = decltype(fold_tag)::value;
-        constexpr int PD = LO ? G::kPdLo : G::kPdHi;
-        constexpr int ACT = (LO ? 2 : 1) * G::kActHi;   // activation bytes of one stage
-        constexpr int L = R + G::kScaleInst + (LO ? 4 : 2);   // DMA instructions per wave and stage
-        uint8_t *const wring = lds + PD * ACT + wave * PD * G::kWSlot;
+        constexpr int NM = decltype(nm_tag)::value;     // live 16-row subtiles
+        constexpr int RB = decltype(rb_tag)::value, RN = decltype(rn_tag)::value;
+        constexpr int PD = G::pd(NM, LO, RN);
+        constexpr int ACT = G::act(NM, LO);             // activation bytes of one stage
+        constexpr int LOFF = G::act(NM, false);         // lo half of the stage
+        constexpr int SI = G::scale_inst(RN);
+        constexpr int WS = G::wslot(RN);
+        static_assert(PD >= 3, "the ring needs three stages");
+        constexpr int L = RN + SI + (LO ? 2 : 1) * CPW;   // DMA instructions per wave and stage
+        uint8_t *const ring = lds + G::kRing;
+        uint8_t *const wring = ring + PD * ACT + wave * PD * WS;
         auto issue = [&](int q, int slot) {
-            uint8_t *ws = wring + slot * G::kWSlot;
+            uint8_t *ws = wring + slot * WS;
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                __builtin_amdgcn_global_load_lds((const void *)(wr[r] + (size_t)q * COLI_TILE_BYTES + lane * 16),
-                                                 (lds_void *)(ws + r * COLI_TILE_BYTES), 16, 0, 0);
+            for (int t = 0; t < RN; t++)
+                __builtin_amdgcn_global_load_lds((const void *)(wr[RB + t] + (size_t)q * COLI_TILE_BYTES + lane * 16),
+                                                 (lds_void *)(ws + t * COLI_TILE_BYTES), 16, 0, 0);
 #pragma unroll
-            for (int k = 0; k < G::kScaleInst; k++) {
-                const int r = min(R - 1, k * SG::kPerInst + lane / SG::kLanes);
-                const uint8_t *base = r == 0 ? sr[0] : sr[1];
+            for (int k = 0; k < SI; k++) {
+                const int t = min(RN - 1, k * SG::kPerInst + lane / SG::kLanes);
+                const uint8_t *base = sr[RB];   // (branch-free: a per-lane select between RN bases)
+#pragma unroll
+                for (int tt = 1; tt < RN; tt++)
+                    if (t == tt) base = sr[RB + tt];
                 __builtin_amdgcn_global_load_lds((const void *)(base + (size_t)q * SG::kBytes + (lane % SG::kLanes) * 4),
-                                                 (lds_void *)(ws + 2 * COLI_TILE_BYTES + k * 256), 4, 0, 0);
+                                                 (lds_void *)(ws + RN * COLI_TILE_BYTES + k * 256), 4, 0, 0);
             }
-            uint8_t *xs = lds + slot * ACT;
+            uint8_t *xs = ring + slot * ACT;
 #pragma unroll
-            for (int k = 0; k < 2; k++) {
+            for (int k = 0; k < CPW; k++) {
                 const size_t o = (size_t)xoff[k] + (size_t)q * 128;
-                uint8_t *dst = xs + (wave + W * k) * 1024;
+                const int c = wave + W * k;
+                // chunks of dead subtiles read the clamped last row into the trash slot
+                uint8_t *dst = c < 4 * NM ? xs + c * 1024 : lds + G::kTrash;
                 __builtin_amdgcn_global_load_lds((const void *)(a.xhi + o), (lds_void *)dst, 16, 0, 0);
                 if constexpr (LO)
-                    __builtin_amdgcn_global_load_lds((const void *)(a.xlo + o), (lds_void *)(dst + G::kActHi), 16,
-                                                     0, 0);
+                    __builtin_amdgcn_global_load_lds((const void *)(a.xlo + o),
+                                                     (lds_void *)(c < 4 * NM ? dst + LOFF : dst), 16, 0, 0);
             }
         };
         auto compute = [&](int slot) {
-            const uint8_t *ws = wring + slot * G::kWSlot;
-            const uint8_t *xs = lds + slot * ACT;
-            u32x4 w[R];
-            ScaleRegs<KIND> sc[R];
+            const uint8_t *ws = wring + slot * WS;
+            const uint8_t *xs = ring + slot * ACT;
+            u32x4 w[RN];
+            ScaleRegs<KIND> sc[RN];
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                w[r] = *(const u32x4 *)(ws + r * COLI_TILE_BYTES + lane * 16);
-                sc[r].v = *(const decltype(sc[r].v) *)(ws + 2 * COLI_TILE_BYTES + r * SG::kBytes +
-                                                       (lane & 15) * sizeof(sc[r].v));
+            for (int t = 0; t < RN; t++) {
+                w[t] = *(const u32x4 *)(ws + t * COLI_TILE_BYTES + lane * 16);
+                sc[t].v = *(const decltype(sc[t].v) *)(ws + RN * COLI_TILE_BYTES + t * SG::kBytes +
+                                                       (lane & 15) * sizeof(sc[t].v));
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                half8v bw[R];
-                float scl[R];
+                half8v bw[RN];
+                float scl[RN];
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    scl[r] = sc[r].get(j);
-                    if constexpr (FOLD) bw[r] = unpack_fp4_scaled(w[r][j], scl[r]);
-                    else bw[r] = unpack_b<KIND>(w[r][j]);
+                for (int t = 0; t < RN; t++) {
+                    scl[t] = sc[t].get(j);
+                    if constexpr (FOLD) bw[t] = unpack_fp4_scaled(w[t][j], scl[t]);
+                    else bw[t] = unpack_b<KIND>(w[t][j]);
                 }
+                half8v xh[NM], xl[NM];
 #pragma unroll
-                for (int m = 0; m < 4; m++) {
-                    if (m >= nm) break;
+                for (int m = 0; m < NM; m++) {
                     const uint8_t *fo = xs + (m * 4 + j) * 1024 + lane * 16;
-                    const half8v xh = *(const half8v *)fo;
-                    half8v xl = xh;
-                    if constexpr (LO) xl = *(const half8v *)(fo + G::kActHi);
+                    xh[m] = *(const half8v *)fo;
+                    if constexpr (LO) xl[m] = *(const half8v *)(fo + LOFF);
+                }
+                if constexpr (FOLD) {
+                    // the operand carries the group scale: accumulate in the MFMA
 #pragma unroll
-                    for (int r = 0; r < R; r++) {
-                        if constexpr (FOLD) {
-                            // the operand carries the group scale: accumulate in the MFMA
-                            acc[r][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[r], acc[r][m], 0, 0, 0);
-                            if constexpr (LO)
-                                acc[r][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[r], acc[r][m], 0, 0, 0);
-                        } else {
-                            floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw[r],
-                                                                              (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                            if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bw[r], d, 0, 0, 0);
+                    for (int m = 0; m < NM; m++)
 #pragma unroll
-                            for (int i = 0; i < 4; i++) acc[r][m][i] = fmaf(d[i], scl[r], acc[r][m][i]);
-                        }
+                        for (int t = 0; t < RN; t++)
+                            acc[RB + t][m] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[m], bw[t], acc[RB + t][m], 0, 0, 0);
+                    if constexpr (LO) {
+#pragma unroll
+                        for (int m = 0; m < NM; m++)
+#pragma unroll
+                            for (int t = 0; t < RN; t++)
+                                acc[RB + t][m] =
+                                    __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[m], bw[t], acc[RB + t][m], 0, 0, 0);
                     }
+                } else {
+                    floatx4 d[RN][NM];
+#pragma unroll
+                    for (int m = 0; m < NM; m++)
+#pragma unroll
+                        for (int t = 0; t < RN; t++)
+                            d[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[m], bw[t],
+                                                                             (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    if constexpr (LO) {
+#pragma unroll
+                        for (int m = 0; m < NM; m++)
+#pragma unroll
+                            for (int t = 0; t < RN; t++)
+                                d[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[m], bw[t], d[t][m], 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int m = 0; m < NM; m++)
+#pragma unroll
+                        for (int t = 0; t < RN; t++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                acc[RB + t][m][i] = fmaf(d[t][m][i], scl[t], acc[RB + t][m][i]);
                 }
             }
         };
@@ -212,24 +274,46 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
             slot = slot == PD - 1 ? 0 : slot + 1;
         }
     };
+    // one specialization per (lo parts, folded scales, live subtiles); one
+    // pass over K when the ring fits three stages of all the wave's tiles,
+    // else one pass per half of them (the next pass refills the ring only
+    // after every wave is done with the last one)
+    auto by_nm = [&](auto lo_tag, auto fold_tag) {
+        auto go = [&](auto nm_tag) {
+            constexpr bool LO = decltype(lo_tag)::value;
+            constexpr int NM = decltype(nm_tag)::value;
+            using C0 = std::integral_constant<int, 0>;
+            if constexpr (G::passes(NM, LO) == 1) {
+                run(lo_tag, fold_tag, nm_tag, C0{}, std::integral_constant<int, R>{});
+            } else {
+                using H = std::integral_constant<int, R / 2>;
+                run(lo_tag, fold_tag, nm_tag, C0{}, H{});
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                run(lo_tag, fold_tag, nm_tag, H{}, H{});
+            }
+        };
+        static_assert(G::kMt == 4, "the subtile dispatch is written for 64-row tiles");
+        if (nm == 1) go(std::integral_constant<int, 1>{});
+        else if (nm == 2) go(std::integral_constant<int, 2>{});
+        else if (nm == 3) go(std::integral_constant<int, 3>{});
+        else go(std::integral_constant<int, 4>{});
+    };
+    auto by_lo = [&](auto fold_tag) {
+        if (use_lo) by_nm(std::true_type{}, fold_tag);
+        else by_nm(std::false_type{}, fold_tag);
+    };
     if constexpr (KIND == COLI_KIND_FP4) {
-        if (a.fold) {
-            if (use_lo) run(std::true_type{}, std::true_type{});
-            else run(std::false_type{}, std::true_type{});
-        } else if (use_lo) {
-            run(std::true_type{}, std::false_type{});
-        } else {
-            run(std::false_type{}, std::false_type{});
-        }
-    } else if (use_lo) {
-        run(std::true_type{}, std::false_type{});
+        if (a.fold) by_lo(std::true_type{});
+        else by_lo(std::false_type{});
     } else {
-        run(std::false_type{}, std::false_type{});
+        by_lo(std::false_type{});
     }
 
     // epilogue: batch row m0 + 16 m + 4 (lane / 16) + i, output row rt * 16 + lane % 16
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
+    for (int m = 0; m < G::kMt; m++) {
         if (m >= nm) break;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -239,12 +323,13 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
             const int E = a.xexp[a.xrows ? a.xrows[br] : br];
             float *orow = a.out + (size_t)(pr.out_row0 + m0 + bl) * a.ldo;
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
+            for (int t = 0; t < RT; t++) {
+                const int r = DUAL ? 2 * t : t;   // the gate (DUAL) or the plain tile of row tile t
                 if (!live[r]) continue;
                 const int o = rt[r] * 16 + (lane & 15);
                 if (o >= a.O) continue;
                 if constexpr (DUAL)
-                    orow[o] = swiglu_out(ldexpf(acc[0][m][i], E), ldexpf(acc[1][m][i], E), a.swiglu_limit);
+                    orow[o] = swiglu_out(ldexpf(acc[r][m][i], E), ldexpf(acc[r + 1][m][i], E), a.swiglu_limit);
                 else orow[o] = ldexpf(acc[r][m][i], E);
             }
         }
@@ -253,14 +338,14 @@ __global__ __launch_bounds__(64 * COLI_GM_WAVES) void coli_gemm_tiles(ColiGemmAr
 
 template <int KIND>
 static hipError_t launch_gemm_kind(const ColiGemmArgs &a, bool dual, hipStream_t st) {
-    const dim3 grid((unsigned)a.n_mt * a.rb_per_prob), block(64 * COLI_GM_WAVES);
+    const dim3 grid((unsigned)a.n_mt * a.rb_per_prob), block(64 * COLI_GM_W);
     const size_t shm = GmGeom<KIND>::kLds;
     if (dual) hipLaunchKernelGGL((coli_gemm_tiles<KIND, true>), grid, block, shm, st, a);
     else hipLaunchKernelGGL((coli_gemm_tiles<KIND, false>), grid, block, shm, st, a);
     return hipGetLastError();
 }
 
-// rb_per_prob must cover the output rows: COLI_GM_WAVES x (dual ? 1 : 2) row tiles per block.
+// rb_per_prob must cover the output rows: 8 (dual) or 16 row tiles per block.
 extern "C" hipError_t coli_launch_gemm(int kind, int dual, const ColiGemmArgs *a, hipStream_t st) {
     if (a->n_mt <= 0 || a->rb_per_prob <= 0) return hipSuccess;
     if ((long)a->n_mt * a->rb_per_prob > 0x7fffffffL || !a->mt_list) return hipErrorInvalidValue;
