@@ -531,40 +531,50 @@ def issue_take(bench, name, fmt, D, I, count=8, reps=200):
             "serial_us": round(2 * cpu * 1e6, 1)}
 
 
-def moe_layers(bench):
-    """The MoE-layer measurements of configs[0], [2], [3] and [4]."""
-    res = {
-        "configs[0]_olmoe_int4": bench.moe("olmoe", 4, 2048, 1024, 64, 8, 0, False, (1,), 10, False),
-        "configs[2]_dsv3_mxfp4": bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 16), 1, True),
-    }
+MOE_PARTS = ("olmoe", "dsv3", "verify", "issue_take", "kimi", "kimi_mx")
+
+
+def moe_layers(bench, only=None):
+    """The MoE-layer measurements of configs[0], [2], [3] and [4] (only: the
+    subset of MOE_PARTS to run, a profiling aid)."""
+    want = lambda part: only is None or part in only
+    res = {}
+    if want("olmoe"):
+        res["configs[0]_olmoe_int4"] = bench.moe("olmoe", 4, 2048, 1024, 64, 8, 0, False, (1,), 10, False)
+    if want("dsv3"):
+        res["configs[2]_dsv3_mxfp4"] = bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 16), 1, True)
     # configs[3]: one verification step of 21 rows (16-node tree + 5-token
     # draft) on the configs[2] layer shape, union GEMM vs 21 per-token passes
-    ver = {}
-    for fmt, tag in ((7, "mxfp4"), (4, "int4")):
-        r = bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True, steps=20)
-        r.update({k + "": v for k, v in bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True,
-                                                      steps=5, per_token=True).items() if k.startswith("B")})
-        ver[tag] = r
-    res["configs[3]_verification_21rows"] = ver
+    if want("verify"):
+        ver = {}
+        for fmt, tag in ((7, "mxfp4"), (4, "int4")):
+            r = bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True, steps=20)
+            r.update({k + "": v for k, v in bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True,
+                                                          steps=5, per_token=True).items() if k.startswith("B")})
+            ver[tag] = r
+        res["configs[3]_verification_21rows"] = ver
     # the async issue/take split at decode, overlapped with host work
-    res["issue_take"] = {"olmoe_int4": issue_take(bench, "olmoe", 4, 2048, 1024),
-                         "dsv3_mxfp4": issue_take(bench, "dsv3", 7, 7168, 2048)}
+    if want("issue_take"):
+        res["issue_take"] = {"olmoe_int4": issue_take(bench, "olmoe", 4, 2048, 1024),
+                             "dsv3_mxfp4": issue_take(bench, "dsv3", 7, 7168, 2048)}
     # configs[4]: Kimi-shaped prefill chunk, 512 tokens, 384 experts top-8,
     # router logits ~N(0,1) with a Zipf(1.1) selection bias
-    res["configs[4]_kimi_prefill_512"] = {
-        tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
-                       w_std=1.0 / math.sqrt(7168))
-        for fmt, tag in ((7, "mxfp4"), (4, "int4"))}
+    if want("kimi"):
+        res["configs[4]_kimi_prefill_512"] = {
+            tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+                           w_std=1.0 / math.sqrt(7168))
+            for fmt, tag in ((7, "mxfp4"), (4, "int4"))}
     # the opt-in MXFP4 GEMM on the block-scaled MFMA (COLI_HIP_MX=1; not
     # fp32-exact: the hardware's per-block summation error is ~2^-15 of the
     # block's magnitude sum)
-    os.environ["COLI_HIP_MX"] = "1"
-    try:
-        res["configs[4]_kimi_prefill_512"]["mxfp4_block_scaled_mfma_optin"] = bench.moe(
-            "kimi", 7, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
-            w_std=1.0 / math.sqrt(7168))
-    finally:
-        del os.environ["COLI_HIP_MX"]
+    if want("kimi_mx"):
+        os.environ["COLI_HIP_MX"] = "1"
+        try:
+            res.setdefault("configs[4]_kimi_prefill_512", {})["mxfp4_block_scaled_mfma_optin"] = bench.moe(
+                "kimi", 7, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+                w_std=1.0 / math.sqrt(7168))
+        finally:
+            del os.environ["COLI_HIP_MX"]
     return res
 
 
@@ -611,6 +621,8 @@ def main():
     ap.add_argument("--skip-dense", action="store_true",
                     help="run only the MoE-layer measurements (profiling aid; prints the moe_layer object)")
     ap.add_argument("--moe-steps", type=int, default=50)
+    ap.add_argument("--moe-only", default=None,
+                    help="with --skip-dense: comma-separated subset of " + ",".join(MOE_PARTS))
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy 256 MiB device-to-device 4 times (the known-size reference that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -631,7 +643,12 @@ def main():
         print(json.dumps({"copy_calib_bytes": nb, "copies": 4}))
         return
     if args.skip_dense:
-        print(json.dumps({"moe_layer": moe_layers(bench)}))
+        only = None
+        if args.moe_only:
+            only = set(args.moe_only.split(","))
+            if not only <= set(MOE_PARTS):
+                ap.error(f"--moe-only: parts are {','.join(MOE_PARTS)}")
+        print(json.dumps({"moe_layer": moe_layers(bench, only)}))
         bench.close()
         return
     bench.dense()
