@@ -35,14 +35,30 @@ def test_int4_g32_fp16_scales(session, O, I, S):
     check(y, ref, magnitude(x, deq_i4(q4, sc, I, 32)))
 
 
+def error_stats(tag, got, ref, mag):
+    """Print the error distribution three ways: the test metric (|ref| with a
+    floor of 1e-2 of the magnitude sum), |ref| alone, and the magnitude sum
+    alone (the reference's own c/tests/test_i4_grouped.c metric)."""
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    r = np.abs(ref.astype(np.float64))
+    m = rel_err(got, ref, mag)
+    pure = d / np.where(r > 0, r, np.inf)
+    print(f"\n[err] {tag}: metric max {m.max():.2e} p50 {np.median(m):.2e}; "
+          f"|err|/|ref| max {pure.max():.2e} p99 {np.quantile(pure, 0.99):.2e} "
+          f"(|ref| >= 1e-2 sum|t|: max {pure[r >= 1e-2 * mag].max():.2e}); "
+          f"|err|/sum|t| max {(d / mag).max():.2e}; under the floor {(r < 1e-2 * mag).mean():.1%}")
+
+
 # The dense benchmark shapes (configs[1]): the up projection runs one group per
-# row block, the down projection splits K across workgroups.
+# row block, the down projection splits K across workgroups. bf16-exact
+# activations as the benchmark feeds them, and full f32 ones (lo parts).
 @pytest.mark.parametrize("O,I", [(14336, 4096), (4096, 14336)])
 @pytest.mark.parametrize("S", [1, 4, 8, 16])
-def test_int4_dense_bench_shapes(session, O, I, S):
-    rng = np.random.default_rng(O + I + S)
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+def test_int4_dense_bench_shapes(session, O, I, S, act):
+    rng = np.random.default_rng(O + I + S + (7 if act == "f32" else 0))
     q4, sc = rand_i4(rng, O, I, 32)
-    x = rand_x(rng, S, I)
+    x = rand_x(rng, S, I) if act == "bf16" else rng.standard_normal((S, I)).astype(np.float32)
     h = session.upload(q4, sc, 4, I, O, 32)
     try:
         y = session.matmul(h, x, 4, I, O, 32)
@@ -51,7 +67,28 @@ def test_int4_dense_bench_shapes(session, O, I, S):
         session.free(h)
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))   # run-to-run bitwise
     ref = cref.matmul_i4_grouped(x, q4, sc, O, I, 32)
-    check(y, ref, magnitude(x, deq_i4(q4, sc, I, 32)))
+    mag = magnitude(x, deq_i4(q4, sc, I, 32))
+    error_stats(f"int4 {O}x{I} S={S} {act}", y, ref, mag)
+    check(y, ref, mag)
+
+
+# The MXFP4 expert shapes of configs[2] (DeepSeek-V3: gate/up 2048 x 7168, down
+# 7168 x 2048) at decode batches, full f32 activations.
+@pytest.mark.parametrize("O,I", [(2048, 7168), (7168, 2048)])
+@pytest.mark.parametrize("S", [1, 16])
+def test_mxfp4_expert_shapes(session, O, I, S):
+    rng = np.random.default_rng(O * 3 + I + S)
+    q4, e8 = rand_mxfp4(rng, O, I)
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    h = session.upload_mxfp4(q4, e8, I, O)
+    try:
+        y = session.matmul(h, x, 7, I, O)
+    finally:
+        session.free(h)
+    ref = cref.matmul_mxfp4(x, q4, e8, O, I)
+    mag = magnitude(x, deq_mxfp4(q4, e8, I))
+    error_stats(f"mxfp4 {O}x{I} S={S} f32", y, ref, mag)
+    check(y, ref, mag)
 
 
 @pytest.mark.parametrize("gs", [32, 64, 128])
