@@ -50,6 +50,7 @@ struct ColiHipMoe {
     int *uniq = nullptr, *xrows = nullptr, *slotrow = nullptr, *mt = nullptr;
     ColiProb *pdual = nullptr, *pdown = nullptr;
     int *route_cnt = nullptr;   // arrival counter of coli_moe_route (zero between launches)
+    bool route_cnt_dirty = false;   // a forward failed part-way: clear the counter before the next
 };
 
 // ---------------------------------------------------------------------------
@@ -600,11 +601,27 @@ static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
     return hip_check(hipGetLastError(), "moe selection + union");
 }
 
+static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, float *out_dev, int S);
+
 extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float *out_dev, int S) {
     if (fault_injected()) return 0;
     if (!m || !x_dev || !out_dev || S < 1 || S > COLI_MOE_MAX_ROWS || S * m->cfg.K > COLI_MOE_MAX_SEL) return 0;
     DevCtx *ctx = ctx_of(m->device);
-    if (!bind_ctx(ctx) || !moe_reserve(ctx, m, S)) return 0;
+    if (!bind_ctx(ctx)) return 0;
+    // The routing kernels count arrivals on route_cnt and the last workgroup
+    // resets it; a forward that failed after its routing launch was queued
+    // may leave it non-zero, so it is cleared (fill kernel) before the next.
+    if (m->route_cnt_dirty) {
+        if (!hip_check(coli_launch_zero_i32(m->route_cnt, 1, ctx->stream), "routing counter reset")) return 0;
+        m->route_cnt_dirty = false;
+    }
+    const int ok = moe_forward_impl(m, ctx, x_dev, out_dev, S);
+    if (!ok) m->route_cnt_dirty = true;
+    return ok;
+}
+
+static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, float *out_dev, int S) {
+    if (!moe_reserve(ctx, m, S)) return 0;
     const ColiHipMoeConfig &c = m->cfg;
     const int P = moe_problems(c, S), rows = moe_rows(c, S);
     const int nq_d = (c.D + 127) / 128, nq_i = (c.I + 127) / 128;
