@@ -412,6 +412,119 @@ __global__ __launch_bounds__(256) void coli_moe_route(const float *__restrict__ 
     moe_union_body(sidx, skeff, S, K, E, has_shared, tab, pdual, pdown, uniq, xrows, slotrow, mt, state, work);
 }
 
+// ---------------------------------------------------------------------------
+// Decode (one token): the down projection of every problem and the weighted
+// combine in one launch. Workgroup = one 16-row output tile; wave j = problem
+// j (the routed experts in union order, then the shared expert), whose one
+// row of SwiGLU output h (f32, row j) it multiplies with its expert's tile on
+// the VALU in f32: at one row an MFMA would compute 16 rows for one, and the
+// f32 dot needs no hi / lo fragments. Lane l owns the tile's 16 B of row
+// l % 16 and k-slice l / 16 (8 columns of each 32-column group); the four
+// k-slices are summed with lane swaps. The products are summed per group
+// and scaled by the group scale (folded into the e2m1 conversion for MXFP4;
+// for int4, sum n x - 8 sum x). The waves' outputs meet in LDS and one wave
+// forms out = sum over slots in slot order of w * y (+ the shared expert's y)
+// with the same arithmetic as coli_moe_combine.
+// ---------------------------------------------------------------------------
+
+template <int KIND>
+__device__ __forceinline__ float dc_group(uint32_t wd, const ScaleRegs<KIND> &sc, int j, const float *xp) {
+    float x[8];
+    const floatx4 a = *(const floatx4 *)xp, b = *(const floatx4 *)(xp + 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        x[i] = a[i];
+        x[i + 4] = b[i];
+    }
+    if constexpr (KIND == COLI_KIND_FP4) {
+        typedef float float2v __attribute__((ext_vector_type(2)));
+        const float s = sc.get(j);
+        const float2v w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 0);
+        const float2v w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 1);
+        const float2v w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 2);
+        const float2v w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 3);
+        const float wv[8] = {w0[0], w0[1], w1[0], w1[1], w2[0], w2[1], w3[0], w3[1]};
+        float p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) p = fmaf(wv[i], x[i], p);
+        return p;
+    } else {
+        // nibble i = column i (offset binary, value n - 8)
+        float p = 0.0f, sx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            p = fmaf((float)((wd >> (4 * i)) & 15u), x[i], p);
+            sx += x[i];
+        }
+        return (p - 8.0f * sx) * sc.get(j);
+    }
+}
+
+// NQ: the tile's 128-column quads (the expert's intermediate size is
+// exactly NQ x 128), all held in registers. At most COLI_DC_WAVES problems (routed + shared).
+#define COLI_DC_WAVES 10
+template <int KIND, int NQ>
+__global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(const ColiProb *__restrict__ pdown,
+                                                               const int *__restrict__ state,
+                                                               const float *__restrict__ h, int D,
+                                                               const float *__restrict__ w, const int *__restrict__ keff,
+                                                               const int *__restrict__ slotrow, int K, int has_shared,
+                                                               float *__restrict__ out) {
+    __shared__ float ys[COLI_DC_WAVES][16];   // [problem][tile row]
+    extern __shared__ __attribute__((aligned(16))) float hsm[];   // [wave][NQ * 128]: the wave's row of h
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rb = blockIdx.x;
+    const int P = state[0];
+    if (wave < P) {
+        const ColiProb pr = uniform_prob(pdown[wave]);
+        const float *hr = h + (size_t)pr.xrow_off * (NQ * 128);
+        float *hs = hsm + wave * (NQ * 128);
+        const size_t t0 = (size_t)rb * NQ;
+        const uint8_t *wt = pr.w0 + t0 * COLI_TILE_BYTES;
+        const int ks = lane >> 4, r16 = lane & 15;
+        // the row of h into LDS (one 1 KiB DMA per 256 columns) and every
+        // weight quad of the tile into registers: all in flight at once
+        asm volatile("" ::"v"(hs) : "memory");
+#pragma unroll
+        for (int k = 0; k < NQ / 2; k++)
+            __builtin_amdgcn_global_load_lds((const void *)(hr + k * 256 + lane * 4), (lds_void *)(hs + k * 256), 16,
+                                             0, 0);
+        u32x4 wq[NQ];
+        ScaleRegs<KIND> sq[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            wq[q] = __builtin_nontemporal_load(GPTR(u32x4, wt + (size_t)q * COLI_TILE_BYTES) + lane);
+            sq[q].load(pr.s0, t0 + q, r16);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            // one quad's activations at a time (not every quad's hoisted)
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int col = 32 * (4 * q + j) + 8 * ks;
+                acc += dc_group<KIND>(wq[q][j], sq[q], j, hs + col);
+            }
+        }
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 32);
+        if (lane < 16) ys[wave][lane] = acc;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        const int d = rb * 16 + lane;
+        if (d < D) {
+            const int ke = keff[0];
+            float acc = 0.0f;
+            for (int kk = 0; kk < ke; kk++) acc = fmaf(w[kk], ys[slotrow[kk]][lane], acc);
+            if (has_shared) acc += ys[P - 1][lane];
+            out[d] = acc;
+        }
+    }
+}
+
 // out[t, d] = sum_{kk < keff[t]} w[t, kk] * y[slotrow[t, kk], d]  (+ y[shared row of t])
 __global__ void coli_moe_combine(const float *__restrict__ y, int D, const float *__restrict__ w,
                                  const int *__restrict__ keff, const int *__restrict__ slotrow, int K,
@@ -603,6 +716,13 @@ static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
 
 static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, float *out_dev, int S);
 
+// COLI_HIP_DOWNCOMBINE=0: at one token, the down projection and the combine
+// run as separate launches (the GEMV of any batch size, then the combine).
+static bool down_combine_enabled() {
+    const char *e = std::getenv("COLI_HIP_DOWNCOMBINE");
+    return !(e && e[0] == '0');
+}
+
 extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float *out_dev, int S) {
     if (fault_injected()) return 0;
     if (!m || !x_dev || !out_dev || S < 1 || S > COLI_MOE_MAX_ROWS || S * m->cfg.K > COLI_MOE_MAX_SEL) return 0;
@@ -667,6 +787,24 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I,
                          nullptr, c.swiglu_limit)) {
         return 0;
+    }
+    // decode, one token: down projection and combine in one launch
+    const int pmax = c.K + (c.has_shared ? 1 : 0);
+    if (!gemm && S == 1 && pmax <= COLI_DC_WAVES && (c.I == 1024 || c.I == 2048) && down_combine_enabled()) {
+        const dim3 grid((unsigned)nrt_d), block(64 * pmax);
+#define COLI_DC_LAUNCH(KD, NQ)                                                                                  \
+    hipLaunchKernelGGL((coli_moe_down_combine1<KD, NQ>), grid, block, (size_t)pmax * c.I * 4, st, m->pdown,  \
+                       m->state, m->h, c.D,                                                                \
+                       m->wsel, m->keff, m->slotrow, c.K, c.has_shared, out_dev)
+#define COLI_DC_KIND(KD)                \
+    if (nq_i == 8) COLI_DC_LAUNCH(KD, 8); \
+    else COLI_DC_LAUNCH(KD, 16)
+        if (m->kind == COLI_KIND_I4_H) { COLI_DC_KIND(COLI_KIND_I4_H); }
+        else if (m->kind == COLI_KIND_I4_F) { COLI_DC_KIND(COLI_KIND_I4_F); }
+        else { COLI_DC_KIND(COLI_KIND_FP4); }
+#undef COLI_DC_KIND
+#undef COLI_DC_LAUNCH
+        return hip_check(hipGetLastError(), "moe down + combine");
     }
     if (!(mx ? make_frags8(ctx, fh, m->h, c.I, rows, c.I, nullptr, m->state + 1)
              : make_frags(ctx, fh, m->h, c.I, rows, c.I, int4, nullptr, m->state + 1)))

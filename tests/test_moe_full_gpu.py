@@ -90,6 +90,31 @@ def test_dsv3_layer_full_size(session, S):
     run_layer(session, layer, x, W, b, K, 2)
 
 
+# One token at the benchmark shapes: the down projection and the combine as
+# one launch (the default at S = 1 for I of 1024 / 2048) and as the separate
+# GEMV + combine launches (COLI_HIP_DOWNCOMBINE=0); both against the oracle, and
+# the two within f32 rounding of each other. int4 fp16 scales, int4 f32
+# scales (DSV3 shape) and MXFP4 with the shared expert.
+@pytest.mark.parametrize("shape", ["olmoe", "dsv3_fp4", "dsv3_i4f"])
+def test_decode_down_combine_paths(session, monkeypatch, shape):
+    rng = np.random.default_rng(4100 + len(shape))
+    if shape == "olmoe":
+        D, I, E, K, fmt, mode, shared = 2048, 1024, 64, 8, 4, 0, False
+    else:
+        D, I, E, K, mode, shared = 7168, 2048, 256, 8, 2, True
+        fmt = 7 if shape == "dsv3_fp4" else 4
+    layer = Layer(rng, fmt, D, I, E, shared=shared, distinct=6)
+    if shape == "dsv3_i4f":   # f32 (not fp16-exact) group scales: the I4_F storage, every expert
+        f32s = lambda trip: tuple((q, (sc * np.float32(1.0 + 1e-6)).astype(np.float32)) for q, sc in trip)
+        layer.experts = [f32s(t) for t in layer.experts]
+        layer.shared = f32s(layer.shared)
+    x, W, b = make_router_inputs(rng, 1, D, E, K, mode, bias=(mode != 0))
+    e1 = run_layer(session, layer, x, W, b, K, mode)
+    monkeypatch.setenv("COLI_HIP_DOWNCOMBINE", "0")
+    e2 = run_layer(session, layer, x, W, b, K, mode)
+    assert e1 <= TOL and e2 <= TOL
+
+
 # one verification step (16-node draft tree + 5-token linear
 # draft = 21 rows) on the configs[2] layer, MXFP4 and int4
 @pytest.mark.parametrize("fmt", [7, 4])
