@@ -482,13 +482,13 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
         const size_t t0 = (size_t)rb * NQ;
         const uint8_t *wt = pr.w0 + t0 * COLI_TILE_BYTES;
         const int ks = lane >> 4, r16 = lane & 15;
-        // the row of h into LDS (one 1 KiB DMA per 256 columns) and every
-        // weight quad of the tile into registers: all in flight at once
-        asm volatile("" ::"v"(hs) : "memory");
+        // the row of h (issued first, through registers into LDS: an LDS DMA
+        // would make the compiler drain every load before the first LDS
+        // read) and every weight quad of the tile: all in flight at once;
+        // the LDS writes wait for h only, and each quad for its own weights
+        floatx4 hv[NQ / 2];
 #pragma unroll
-        for (int k = 0; k < NQ / 2; k++)
-            __builtin_amdgcn_global_load_lds((const void *)(hr + k * 256 + lane * 4), (lds_void *)(hs + k * 256), 16,
-                                             0, 0);
+        for (int k = 0; k < NQ / 2; k++) hv[k] = *GPTR(floatx4, hr + (k * 64 + lane) * 4);
         u32x4 wq[NQ];
         ScaleRegs<KIND> sq[NQ];
 #pragma unroll
@@ -496,7 +496,8 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
             wq[q] = __builtin_nontemporal_load(GPTR(u32x4, wt + (size_t)q * COLI_TILE_BYTES) + lane);
             sq[q].load(pr.s0, t0 + q, r16);
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < NQ / 2; k++) *(floatx4 *)(hs + (k * 64 + lane) * 4) = hv[k];
         float acc = 0.0f;
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
