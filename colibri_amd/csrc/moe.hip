@@ -526,6 +526,91 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode (one token): gate/up of every problem with the SwiGLU epilogue.
+// Workgroup = (problem, 16-row tile of the intermediate); its W waves split K
+// (wave w takes quads w, w + W, ...), each holding every weight quad of its
+// share (gate and up tiles) in registers at once; the token's row of x is
+// staged in LDS once per workgroup. f32 VALU dots as in
+// coli_moe_down_combine1, then the waves' sums meet in LDS in fixed wave order
+// and wave 0 applies SwiGLU and writes the tile's 16 values of h.
+// ---------------------------------------------------------------------------
+template <int KIND, int W, int NQW>
+__global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restrict__ pdual,
+                                                         const int *__restrict__ state, const float *__restrict__ x,
+                                                         int D, int nrt, float *__restrict__ h, int I,
+                                                         float swiglu_limit) {
+    constexpr int NQ = W * NQW;   // the row's 128-column quads (D = NQ x 128)
+    __shared__ __attribute__((aligned(16))) float xs[NQ * 128];
+    __shared__ float red[W][2][16];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
+    if (p >= state[0]) return;
+    const ColiProb pr = uniform_prob(pdual[p]);
+    const int ks = lane >> 4, r16 = lane & 15;
+    const size_t t0 = (size_t)rt * NQ;
+    // x (issued first; each wave moves its NQW quads' 512 floats x ... into
+    // LDS through registers) and every weight quad of this wave's share
+    floatx4 xv[NQW / 2 + 1];
+    constexpr int XF4 = NQ * 32;   // float4s in the row
+#pragma unroll
+    for (int k = 0; k < NQW / 2 + 1; k++) {
+        const int i = (wave + W * k) * 64 + lane;
+        xv[k] = i < XF4 ? *GPTR(floatx4, x + (size_t)i * 4) : (floatx4){0.f, 0.f, 0.f, 0.f};
+    }
+    u32x4 wg[NQW], wu[NQW];
+    ScaleRegs<KIND> sg[NQW], su[NQW];
+#pragma unroll
+    for (int i = 0; i < NQW; i++) {
+        const int q = wave + W * i;
+        wg[i] = __builtin_nontemporal_load(GPTR(u32x4, pr.w0 + (t0 + q) * COLI_TILE_BYTES) + lane);
+        wu[i] = __builtin_nontemporal_load(GPTR(u32x4, pr.w1 + (t0 + q) * COLI_TILE_BYTES) + lane);
+        sg[i].load(pr.s0, t0 + q, r16);
+        su[i].load(pr.s1, t0 + q, r16);
+    }
+#pragma unroll
+    for (int k = 0; k < NQW / 2 + 1; k++) {
+        const int i = (wave + W * k) * 64 + lane;
+        if (i < XF4) *(floatx4 *)(xs + (size_t)i * 4) = xv[k];
+    }
+    // every wave's share of x is in LDS (a bare barrier: the weight loads in
+    // flight are not drained)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    float ag = 0.0f, au = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NQW; i++) {
+        asm volatile("" ::: "memory");
+        const int q = wave + W * i;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float *xp = xs + 32 * (4 * q + j) + 8 * ks;
+            ag += dc_group<KIND>(wg[i][j], sg[i], j, xp);
+            au += dc_group<KIND>(wu[i][j], su[i], j, xp);
+        }
+    }
+    ag += __shfl_xor(ag, 16);
+    ag += __shfl_xor(ag, 32);
+    au += __shfl_xor(au, 16);
+    au += __shfl_xor(au, 32);
+    if (lane < 16) {
+        red[wave][0][lane] = ag;
+        red[wave][1][lane] = au;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        float g = red[0][0][lane], u = red[0][1][lane];
+#pragma unroll
+        for (int w = 1; w < W; w++) {
+            g += red[w][0][lane];
+            u += red[w][1][lane];
+        }
+        const int o = rt * 16 + lane;
+        if (o < I) h[(size_t)pr.out_row0 * I + o] = swiglu_out(g, u, swiglu_limit);
+    }
+}
+
 // out[t, d] = sum_{kk < keff[t]} w[t, kk] * y[slotrow[t, kk], d]  (+ y[shared row of t])
 __global__ void coli_moe_combine(const float *__restrict__ y, int D, const float *__restrict__ w,
                                  const int *__restrict__ keff, const int *__restrict__ slotrow, int K,
@@ -717,6 +802,32 @@ static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
 
 static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, float *out_dev, int S);
 
+// COLI_HIP_DUAL1=0: at one token, gate/up run on the decode GEMV instead.
+static bool dual1_enabled() {
+    const char *e = std::getenv("COLI_HIP_DUAL1");
+    return !(e && e[0] == '0');
+}
+
+// One token's gate/up + SwiGLU for the hidden sizes it is built for (2048:
+// 4 waves x 4 quads, 7168: 8 waves x 7 quads); false: not launched.
+static bool launch_dual1(ColiHipMoe *m, hipStream_t st, const float *x, int nrt, int nq, int P) {
+    const ColiHipMoeConfig &c = m->cfg;
+    const dim3 grid((unsigned)(P * nrt));
+#define COLI_D1(KD, W, NQW)                                                                                   \
+    hipLaunchKernelGGL((coli_moe_dual1<KD, W, NQW>), grid, dim3(64 * W), 0, st, m->pdual, m->state, x, c.D, nrt, \
+                       m->h, c.I, c.swiglu_limit)
+#define COLI_D1_KIND(W, NQW)                                                  \
+    if (m->kind == COLI_KIND_I4_H) COLI_D1(COLI_KIND_I4_H, W, NQW);          \
+    else if (m->kind == COLI_KIND_I4_F) COLI_D1(COLI_KIND_I4_F, W, NQW);     \
+    else COLI_D1(COLI_KIND_FP4, W, NQW);                                     \
+    return true
+    if (c.D == 2048 && nq == 16) { COLI_D1_KIND(4, 4); }
+    if (c.D == 7168 && nq == 56) { COLI_D1_KIND(8, 7); }
+#undef COLI_D1_KIND
+#undef COLI_D1
+    return false;
+}
+
 // COLI_HIP_DOWNCOMBINE=0: at one token, the down projection and the combine
 // run as separate launches (the GEMV of any batch size, then the combine).
 static bool down_combine_enabled() {
@@ -785,6 +896,8 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
         if (!run_gemm(ctx, m->kind, true, m->pdual, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_i, nq_d,
                       c.I, fx, m->xrows, m->h, c.I, c.swiglu_limit, fold))
             return 0;
+    } else if (S == 1 && dual1_enabled() && launch_dual1(m, st, x_dev, nrt_i, nq_d, P)) {
+        if (!hip_check(hipGetLastError(), "moe gate/up")) return 0;
     } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I,
                          nullptr, c.swiglu_limit)) {
         return 0;

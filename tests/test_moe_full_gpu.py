@@ -90,10 +90,11 @@ def test_dsv3_layer_full_size(session, S):
     run_layer(session, layer, x, W, b, K, 2)
 
 
-# One token at the benchmark shapes: the down projection and the combine as
-# one launch (the default at S = 1 for I of 1024 / 2048) and as the separate
-# GEMV + combine launches (COLI_HIP_DOWNCOMBINE=0); both against the oracle, and
-# the two within f32 rounding of each other. int4 fp16 scales, int4 f32
+# One token at the benchmark shapes: gate/up on the one-token kernel and the
+# down projection and the combine as one launch (the defaults at S = 1 for
+# these sizes), then the separate down GEMV + combine (COLI_HIP_DOWNCOMBINE=0),
+# then gate/up on the decode GEMV too (COLI_HIP_DUAL1=0); each against the
+# oracle. int4 fp16 scales, int4 f32
 # scales (DSV3 shape) and MXFP4 with the shared expert.
 @pytest.mark.parametrize("shape", ["olmoe", "dsv3_fp4", "dsv3_i4f"])
 def test_decode_down_combine_paths(session, monkeypatch, shape):
@@ -112,7 +113,9 @@ def test_decode_down_combine_paths(session, monkeypatch, shape):
     e1 = run_layer(session, layer, x, W, b, K, mode)
     monkeypatch.setenv("COLI_HIP_DOWNCOMBINE", "0")
     e2 = run_layer(session, layer, x, W, b, K, mode)
-    assert e1 <= TOL and e2 <= TOL
+    monkeypatch.setenv("COLI_HIP_DUAL1", "0")   # and gate/up on the decode GEMV
+    e3 = run_layer(session, layer, x, W, b, K, mode)
+    assert max(e1, e2, e3) <= TOL
 
 
 # one verification step (16-node draft tree + 5-token linear
