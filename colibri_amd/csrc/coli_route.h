@@ -146,36 +146,26 @@ __device__ __forceinline__ int wave_min_i(int v) {
     return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
                min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
-// Argmax over (key, then lowest index) carrying a payload; uniform result.
-__device__ __forceinline__ void wave_argmax(unsigned &k, int &e, float &w) {
-    auto step = [&](unsigned ok, int oe, float ow) {
-        if (ok > k || (ok == k && oe < e)) {
-            k = ok;
-            e = oe;
-            w = ow;
-        }
-    };
-#define COLI_ARGMAX_STEP(CTRL) \
-    step((unsigned)dpp_mov<CTRL>((int)k), dpp_mov<CTRL>(e), __int_as_float(dpp_mov<CTRL>(__float_as_int(w))))
-    COLI_ARGMAX_STEP(COLI_DPP_XOR1);
-    COLI_ARGMAX_STEP(COLI_DPP_XOR2);
-    COLI_ARGMAX_STEP(COLI_DPP_ROR4);
-    COLI_ARGMAX_STEP(COLI_DPP_ROR8);
-#undef COLI_ARGMAX_STEP
-    unsigned rk[4];
-    int re[4];
-    float rw[4];
+// Maximum of a 64-bit value over the wave (DPP steps on both halves inside
+// each 16-lane row, then the four rows); uniform result.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    auto step = [&](unsigned long long o) { v = o > v ? o : v; };
+#define COLI_MAX64_STEP(CTRL)                                                                  \
+    step(((unsigned long long)(unsigned)dpp_mov<CTRL>((int)(v >> 32)) << 32) |                 \
+         (unsigned)dpp_mov<CTRL>((int)(unsigned)v))
+    COLI_MAX64_STEP(COLI_DPP_XOR1);
+    COLI_MAX64_STEP(COLI_DPP_XOR2);
+    COLI_MAX64_STEP(COLI_DPP_ROR4);
+    COLI_MAX64_STEP(COLI_DPP_ROR8);
+#undef COLI_MAX64_STEP
+    unsigned long long r = 0ull;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        rk[r] = (unsigned)__builtin_amdgcn_readlane((int)k, 16 * r);
-        re[r] = __builtin_amdgcn_readlane(e, 16 * r);
-        rw[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), 16 * r));
+    for (int q = 0; q < 4; q++) {
+        const unsigned long long o = ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(v >> 32), 16 * q) << 32) |
+                                     (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, 16 * q);
+        r = o > r ? o : r;
     }
-    k = rk[0];
-    e = re[0];
-    w = rw[0];
-#pragma unroll
-    for (int r = 1; r < 4; r++) step(rk[r], re[r], rw[r]);
+    return r;
 }
 
 #define COLI_SEL_BATCH 4   // experts per lane whose chunk partials are loaded together (JM >= 4)
@@ -346,86 +336,70 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
     // in lane kk for slot kk.
     int my_e = 0;
     float my_w = 0.0f;
-    if (JM * K <= 64) {
-        // Ranks by comparison instead of K serial rounds. Entries are ordered
-        // by c = key << 32 | ~index (a larger c ranks first; keys are unique
-        // per index, so c is a strict total order). Stage 1 ranks each lane's
-        // entry of register group j among the 64 of that group (the group
-        // broadcast through LDS); the top K of every group are candidates
-        // (the overall top K lies among them); stage 2 ranks the JM * K
-        // candidates, one per lane.
+    if (JM == 1 && K <= 64) {
+        // One entry per lane: ranks by comparison instead of K serial rounds.
+        // Entries are ordered by c = key << 32 | ~index (a larger c ranks
+        // first; keys are unique per index, so c is a strict total order);
+        // the entry of rank r < K goes to slot r.
         __shared__ __attribute__((aligned(16))) unsigned long long rk_c[4][64], rk_sel[4][64];
         const int wv = (threadIdx.x >> 6) & 3;
         unsigned long long *cb = rk_c[wv], *sel = rk_sel[wv];
-        int ncand = 0;
-#pragma unroll
-        for (int j = 0; j < JM; j++) {
-            if (j < jmax) {   // wave-uniform
-            const int e = lane + 64 * j;
-            const unsigned long long c =
-                key[j] ? ((unsigned long long)key[j] << 32) | (0xFFFFFFFFu - (unsigned)e) : 0ull;
-            cb[lane] = c;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            // all 64 entries read before the first comparison (32 reads of
-            // two entries in flight together)
-            unsigned long long v[64];
-#pragma unroll
-            for (int i = 0; i < 64; i += 2) {
-                const ulonglong2 t2 = *(const ulonglong2 *)(cb + i);
-                v[i] = t2.x;
-                v[i + 1] = t2.y;
-            }
-            int r = 0;
-#pragma unroll
-            for (int i = 0; i < 64; i++) r += v[i] > c;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            const int nj = min(K, wave_sum_i(c != 0ull ? 1 : 0));   // valid entries of the group, capped
-            if (c != 0ull && r < K) sel[ncand + r] = c;
-            ncand += nj;
-            }
-        }
+        unsigned long long c = key[0] ? ((unsigned long long)key[0] << 32) | (0xFFFFFFFFu - (unsigned)lane) : 0ull;
+        cb[lane] = c;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        unsigned long long c = lane < ncand ? sel[lane] : 0ull;
-        if (JM > 1) {
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            int r = 0;
+        // all 64 entries read before the first comparison (32 reads of two
+        // entries in flight together)
+        unsigned long long v[64];
 #pragma unroll
-            for (int i = 0; i < 64; i += 2) {
-                const ulonglong2 t2 = *(const ulonglong2 *)(sel + i);
-                r += (i < ncand && t2.x > c) + (i + 1 < ncand && t2.y > c);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            if (lane < ncand && r < K) cb[r] = c;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            c = lane < want ? cb[lane] : 0ull;
+        for (int i = 0; i < 64; i += 2) {
+            const ulonglong2 t2 = *(const ulonglong2 *)(cb + i);
+            v[i] = t2.x;
+            v[i + 1] = t2.y;
         }
+        int r = 0;
+#pragma unroll
+        for (int i = 0; i < 64; i++) r += v[i] > c;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (c != 0ull && r < K) sel[r] = c;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        c = lane < want ? sel[lane] : 0ull;
         if (lane < want) {
             my_e = (int)(0xFFFFFFFFu - (unsigned)(c & 0xFFFFFFFFull));
             my_w = p[my_e];
         }
     } else {
-        // K rounds of a wave-wide argmax (largest key, then lowest expert
-        // index): round kk yields the expert of rank kk (and its weight
-        // source), which its owner lane then retires; lane kk keeps slot kk.
-        for (int kk = 0; kk < want; kk++) {
-            unsigned bk = 0;
-            int be = 0x7fffffff;
-            float bw = 0.0f;
+        // K rounds over the lanes' sorted lists: every lane sorts its JM
+        // entries once (c descending), then round kk takes the wave maximum
+        // of the lanes' heads (the entry of rank kk) and its owner pops it.
+        // c = key << 32 | ~index as above; 0 marks no entry.
+        unsigned long long c[JM];
 #pragma unroll
-            for (int j = 0; j < JM; j++)
-                if (key[j] > bk) {   // strict: the lower index (smaller j) wins a tie
-                    bk = key[j];
-                    be = lane + 64 * j;
-                    bw = pv[j];
+        for (int j = 0; j < JM; j++)
+            c[j] = (j < jmax && key[j]) ? ((unsigned long long)key[j] << 32) | (0xFFFFFFFFu - (unsigned)(lane + 64 * j))
+                                        : 0ull;
+#pragma unroll
+        for (int i = 1; i < JM; i++)
+#pragma unroll
+            for (int j = i; j > 0; j--)
+                if (c[j] > c[j - 1]) {
+                    const unsigned long long t = c[j];
+                    c[j] = c[j - 1];
+                    c[j - 1] = t;
                 }
-            wave_argmax(bk, be, bw);
+        unsigned long long mine = 0ull;
+        for (int kk = 0; kk < want; kk++) {
+            const unsigned long long m = wave_max_u64(c[0]);
+            if (c[0] == m) {   // one lane: the entries are distinct
 #pragma unroll
-            for (int j = 0; j < JM; j++)
-                if (lane + 64 * j == be) key[j] = 0;
-            if (lane == kk) {
-                my_e = be;
-                my_w = bw;
+                for (int j = 0; j + 1 < JM; j++) c[j] = c[j + 1];
+                c[JM - 1] = 0ull;
             }
+            if (lane == kk) mine = m;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // p[] written by all lanes
+        if (lane < want) {
+            my_e = (int)(0xFFFFFFFFu - (unsigned)(mine & 0xFFFFFFFFull));
+            my_w = p[my_e];
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // p[] written by all lanes

@@ -474,9 +474,24 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
     extern __shared__ __attribute__((aligned(16))) float hsm[];   // [wave][NQ * 128]: the wave's row of h
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rb = blockIdx.x;
+    // the live count, this wave's descriptor (the array holds one per wave
+    // of the block) and the combine's inputs are loaded together: one round
+    // trip before the weights, none before the combine
     const int P = state[0];
+    const ColiProb pd = pdown[wave];
+    float wk[COLI_DC_WAVES];
+    int sk[COLI_DC_WAVES];
+    int ke = 0;
+    if (wave == 0) {
+        ke = keff[0];
+#pragma unroll
+        for (int kk = 0; kk < COLI_DC_WAVES; kk++) {
+            wk[kk] = kk < K ? w[kk] : 0.0f;
+            sk[kk] = kk < K ? slotrow[kk] : 0;
+        }
+    }
     if (wave < P) {
-        const ColiProb pr = uniform_prob(pdown[wave]);
+        const ColiProb pr = uniform_prob(pd);
         const float *hr = h + (size_t)pr.xrow_off * (NQ * 128);
         float *hs = hsm + wave * (NQ * 128);
         const size_t t0 = (size_t)rb * NQ;
@@ -517,9 +532,10 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
     if (wave == 0 && lane < 16) {
         const int d = rb * 16 + lane;
         if (d < D) {
-            const int ke = keff[0];
             float acc = 0.0f;
-            for (int kk = 0; kk < ke; kk++) acc = fmaf(w[kk], ys[slotrow[kk]][lane], acc);
+#pragma unroll
+            for (int kk = 0; kk < COLI_DC_WAVES; kk++)
+                if (kk < ke) acc = fmaf(wk[kk], ys[sk[kk]][lane], acc);
             if (has_shared) acc += ys[P - 1][lane];
             out[d] = acc;
         }
@@ -545,8 +561,12 @@ __global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restr
     __shared__ float red[W][2][16];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
-    if (p >= state[0]) return;
-    const ColiProb pr = uniform_prob(pdual[p]);
+    // the live count and the descriptor (in the array: p < the launch's
+    // problem count) in one round trip
+    const int np = state[0];
+    const ColiProb pd = pdual[p];
+    if (p >= np) return;
+    const ColiProb pr = uniform_prob(pd);
     const int ks = lane >> 4, r16 = lane & 15;
     const size_t t0 = (size_t)rt * NQ;
     // x (issued first; each wave moves its NQW quads' 512 floats x ... into
