@@ -542,6 +542,145 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
     }
 }
 
+// The same launch on the matrix cores (used at an intermediate size of 1024,
+// OLMoE's: 7.1 -> 6.6 us a layer; at 2048 the f32 form above measured
+// faster): each wave converts its row of h once into fp16 hi / lo fragments in
+// LDS (one exponent for the row, the column order and factors of
+// coli_prep_frag), then runs two v_mfma_f32_16x16x32_f16 per 32-column group
+// (hi, and lo when the row has any), the token's row in every row of the A
+// operand: lane l ends with output row l % 16 of the tile, no lane sums
+// needed. MXFP4 tensors whose scales fold exactly into the fp16 operand (FOLD)
+// accumulate inside the MFMA; otherwise the group's result is scaled and
+// accumulated on the VALU, one sum per group position.
+template <bool INT4, int NCL>
+__device__ __forceinline__ bool row_to_frags(const floatx4 (&v)[2 * NCL], _Float16 *dst, int ncol, int lane,
+                                             int *E_out) {
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2 * NCL; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) m = fmaxf(m, fabsf(v[k][i]));
+    m = wave_max64(m);
+    int E = 0;
+    if (m > 0.0f && isfinite(m)) {
+        frexpf(m, &E);
+        E -= 15;
+    }
+    bool any = false;
+#pragma unroll
+    for (int c = 0; c < NCL; c++) {
+        const float u[8] = {v[2 * c][0], v[2 * c][1], v[2 * c][2], v[2 * c][3],
+                            v[2 * c + 1][0], v[2 * c + 1][1], v[2 * c + 1][2], v[2 * c + 1][3]};
+        half8v hh, ll;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int off = INT4 ? (t < 4 ? 2 * t : 2 * (t - 4) + 1) : t;
+            float y = ldexpf(u[off], -E);
+            if (INT4 && (off & 1)) y *= 0.0625f;
+            hh[t] = (_Float16)y;
+            ll[t] = (_Float16)(y - (float)hh[t]);
+            any |= ll[t] != (_Float16)0.0f;
+        }
+        const int ch = c * 64 + lane;   // 8-column chunk
+        *(half8v *)(dst + ch * 8) = hh;
+        *(half8v *)(dst + ncol + ch * 8) = ll;
+    }
+    *E_out = E;
+    return __builtin_amdgcn_ballot_w64(any) != 0;
+}
+
+template <int KIND, int NQ, bool FOLD>
+__global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1m(const ColiProb *__restrict__ pdown,
+                                                                const int *__restrict__ state,
+                                                                const float *__restrict__ h, int D,
+                                                                const float *__restrict__ w,
+                                                                const int *__restrict__ keff,
+                                                                const int *__restrict__ slotrow, int K,
+                                                                int has_shared, float *__restrict__ out) {
+    static_assert(!FOLD || KIND == COLI_KIND_FP4, "folded scales: MXFP4 only");
+    constexpr int NC = NQ * 128;   // columns of the row of h
+    constexpr int NCL = NQ / 4;    // 8-column chunks per lane
+    __shared__ float ys[COLI_DC_WAVES][16];   // [problem][tile row]
+    extern __shared__ __attribute__((aligned(16))) _Float16 hfr[];   // [wave][hi NC | lo NC]
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rb = blockIdx.x;
+    const int P = state[0];
+    const ColiProb pd = pdown[wave];
+    float wk[COLI_DC_WAVES];
+    int sk[COLI_DC_WAVES];
+    int ke = 0;
+    if (wave == 0) {
+        ke = keff[0];
+#pragma unroll
+        for (int kk = 0; kk < COLI_DC_WAVES; kk++) {
+            wk[kk] = kk < K ? w[kk] : 0.0f;
+            sk[kk] = kk < K ? slotrow[kk] : 0;
+        }
+    }
+    if (wave < P) {
+        const ColiProb pr = uniform_prob(pd);
+        const float *hr = h + (size_t)pr.xrow_off * NC;
+        _Float16 *hs = hfr + wave * (2 * NC);
+        const size_t t0 = (size_t)rb * NQ;
+        const uint8_t *wt = pr.w0 + t0 * COLI_TILE_BYTES;
+        const int ks = lane >> 4, r16 = lane & 15;
+        // the row of h (8-column chunks c * 64 + lane), then every weight quad
+        floatx4 hv[2 * NCL];
+#pragma unroll
+        for (int c = 0; c < NCL; c++) {
+            hv[2 * c] = *GPTR(floatx4, hr + (size_t)(c * 64 + lane) * 8);
+            hv[2 * c + 1] = *GPTR(floatx4, hr + (size_t)(c * 64 + lane) * 8 + 4);
+        }
+        u32x4 wq[NQ];
+        ScaleRegs<KIND> sq[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            wq[q] = __builtin_nontemporal_load(GPTR(u32x4, wt + (size_t)q * COLI_TILE_BYTES) + lane);
+            sq[q].load(pr.s0, t0 + q, r16);
+        }
+        int E;
+        // the wave reads back only its own LDS writes: in order, no barrier
+        const bool lo = row_to_frags<KIND != COLI_KIND_FP4, NCL>(hv, hs, NC, lane, &E);
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        float acc0[4] = {0.f, 0.f, 0.f, 0.f};   // unfolded: one VALU sum per group position
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int col = 32 * (4 * q + j) + 8 * ks;
+                const half8v xh = *(const half8v *)(hs + col);
+                const float scl = sq[q].get(j);
+                half8v bw;
+                if constexpr (FOLD) bw = unpack_fp4_scaled(wq[q][j], scl);
+                else bw = unpack_b<KIND>(wq[q][j]);
+                if constexpr (FOLD) {
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw, acc, 0, 0, 0);
+                    if (lo) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8v *)(hs + NC + col), bw, acc, 0, 0, 0);
+                } else {
+                    floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    if (lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8v *)(hs + NC + col), bw, d, 0, 0, 0);
+                    acc0[j] = fmaf(d[0], scl, acc0[j]);
+                }
+            }
+        }
+        const float y = FOLD ? acc[0] : (acc0[0] + acc0[1]) + (acc0[2] + acc0[3]);
+        if (lane < 16) ys[wave][lane] = ldexpf(y, E);
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+        const int d = rb * 16 + lane;
+        if (d < D) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < COLI_DC_WAVES; kk++)
+                if (kk < ke) acc = fmaf(wk[kk], ys[sk[kk]][lane], acc);
+            if (has_shared) acc += ys[P - 1][lane];
+            out[d] = acc;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Decode (one token): gate/up of every problem with the SwiGLU epilogue.
 // Workgroup = (problem, 16-row tile of the intermediate); its W waves split K
@@ -855,6 +994,12 @@ static bool down_combine_enabled() {
     return !(e && e[0] == '0');
 }
 
+// COLI_HIP_DC_MFMA=0: the one-token down + combine takes its f32 VALU form.
+static bool dc_mfma_enabled() {
+    const char *e = std::getenv("COLI_HIP_DC_MFMA");
+    return !(e && e[0] == '0');
+}
+
 extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float *out_dev, int S) {
     if (fault_injected()) return 0;
     if (!m || !x_dev || !out_dev || S < 1 || S > COLI_MOE_MAX_ROWS || S * m->cfg.K > COLI_MOE_MAX_SEL) return 0;
@@ -924,6 +1069,28 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     }
     // decode, one token: down projection and combine in one launch
     const int pmax = c.K + (c.has_shared ? 1 : 0);
+    // (the matrix-core form at an intermediate size of 1024; at 2048 its
+    // registers left no more occupancy and the f32 form measured faster)
+    bool fold_all = m->kind == COLI_KIND_FP4;
+    for (size_t i = 0; fold_all && i < m->mats.size(); i++) fold_all = m->mats[i]->e8_fold != 0;
+    if (!gemm && S == 1 && pmax <= COLI_DC_WAVES && c.I == 1024 && down_combine_enabled() && dc_mfma_enabled()) {
+        const dim3 grid((unsigned)nrt_d), block(64 * pmax);
+        const size_t shm = (size_t)pmax * c.I * 4;
+#define COLI_DCM_LAUNCH(KD, NQ, FD)                                                                         \
+    hipLaunchKernelGGL((coli_moe_down_combine1m<KD, NQ, FD>), grid, block, shm, st, m->pdown, m->state, m->h, \
+                       c.D, m->wsel, m->keff, m->slotrow, c.K, c.has_shared, out_dev)
+        if (fold_all) {
+            COLI_DCM_LAUNCH(COLI_KIND_FP4, 8, true);
+        } else if (m->kind == COLI_KIND_I4_H) {
+            COLI_DCM_LAUNCH(COLI_KIND_I4_H, 8, false);
+        } else if (m->kind == COLI_KIND_I4_F) {
+            COLI_DCM_LAUNCH(COLI_KIND_I4_F, 8, false);
+        } else {
+            COLI_DCM_LAUNCH(COLI_KIND_FP4, 8, false);
+        }
+#undef COLI_DCM_LAUNCH
+        return hip_check(hipGetLastError(), "moe down + combine");
+    }
     if (!gemm && S == 1 && pmax <= COLI_DC_WAVES && (c.I == 1024 || c.I == 2048) && down_combine_enabled()) {
         const dim3 grid((unsigned)nrt_d), block(64 * pmax);
 #define COLI_DC_LAUNCH(KD, NQ)                                                                                  \

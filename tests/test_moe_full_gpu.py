@@ -96,26 +96,36 @@ def test_dsv3_layer_full_size(session, S):
 # then gate/up on the decode GEMV too (COLI_HIP_DUAL1=0); each against the
 # oracle. int4 fp16 scales, int4 f32
 # scales (DSV3 shape) and MXFP4 with the shared expert.
-@pytest.mark.parametrize("shape", ["olmoe", "dsv3_fp4", "dsv3_i4f"])
+@pytest.mark.parametrize("shape", ["olmoe", "dsv3_fp4", "dsv3_i4f", "mx1024_fold", "mx1024_wide"])
 def test_decode_down_combine_paths(session, monkeypatch, shape):
     rng = np.random.default_rng(4100 + len(shape))
+    e8 = (119, 123)
     if shape == "olmoe":
         D, I, E, K, fmt, mode, shared = 2048, 1024, 64, 8, 4, 0, False
+    elif shape.startswith("mx1024"):
+        # MXFP4 at an intermediate size of 1024: the matrix-core down +
+        # combine, with scales that fold into the fp16 operand and with
+        # exponents too wide for it
+        D, I, E, K, fmt, mode, shared = 2048, 1024, 64, 8, 7, 2, True
+        if shape == "mx1024_wide":
+            e8 = (100, 150)
     else:
         D, I, E, K, mode, shared = 7168, 2048, 256, 8, 2, True
         fmt = 7 if shape == "dsv3_fp4" else 4
-    layer = Layer(rng, fmt, D, I, E, shared=shared, distinct=6)
+    layer = Layer(rng, fmt, D, I, E, shared=shared, distinct=6, e8_range=e8)
     if shape == "dsv3_i4f":   # f32 (not fp16-exact) group scales: the I4_F storage, every expert
         f32s = lambda trip: tuple((q, (sc * np.float32(1.0 + 1e-6)).astype(np.float32)) for q, sc in trip)
         layer.experts = [f32s(t) for t in layer.experts]
         layer.shared = f32s(layer.shared)
     x, W, b = make_router_inputs(rng, 1, D, E, K, mode, bias=(mode != 0))
     e1 = run_layer(session, layer, x, W, b, K, mode)
-    monkeypatch.setenv("COLI_HIP_DOWNCOMBINE", "0")
+    monkeypatch.setenv("COLI_HIP_DC_MFMA", "0")   # the f32 VALU down + combine
     e2 = run_layer(session, layer, x, W, b, K, mode)
-    monkeypatch.setenv("COLI_HIP_DUAL1", "0")   # and gate/up on the decode GEMV
+    monkeypatch.setenv("COLI_HIP_DOWNCOMBINE", "0")
     e3 = run_layer(session, layer, x, W, b, K, mode)
-    assert max(e1, e2, e3) <= TOL
+    monkeypatch.setenv("COLI_HIP_DUAL1", "0")   # and gate/up on the decode GEMV
+    e4 = run_layer(session, layer, x, W, b, K, mode)
+    assert max(e1, e2, e3, e4) <= TOL
 
 
 # one verification step (16-node draft tree + 5-token linear
