@@ -12,7 +12,7 @@ import pytest
 
 from colibri_amd import hiprt
 from colibri_amd.backend import ColiHipMoeConfig, f32p, i32p, tensor_array
-from moe_ref import Layer, make_router_inputs
+from moe_ref import Layer, free_handles, make_router_inputs
 from quant_util import rand_i4, rand_mxfp4
 
 pytestmark = pytest.mark.gpu
@@ -77,22 +77,30 @@ def test_gemm_graph_replays_match_eager(session, fmt, O, I, S):
 # (256, 16): routing in one launch; (1536, 256): router partials, then the
 # selection and union in one launch (both with arrival counters that must be
 # back at zero after every replay)
-@pytest.mark.parametrize("D,E", [(256, 16), (1536, 256)])
-def test_moe_graph_replays_match_eager(session, D, E):
+# The last case is one token at OLMoE's shapes (routing in one launch, the
+# one-token gate/up and down + combine kernels).
+@pytest.mark.parametrize("D,E,I,K,S,olmoe", [(256, 16, 128, 4, 5, False), (1536, 256, 128, 4, 5, False),
+                                             (2048, 64, 1024, 8, 1, True)])
+def test_moe_graph_replays_match_eager(session, D, E, I, K, S, olmoe):
     b = session.b
     st = b.hip_stream(0)
     rng = np.random.default_rng(61 + E)
-    I, K, S = 128, 4, 5
-    layer = Layer(rng, 7, D, I, E, shared=True)
-    x, W, bias = make_router_inputs(rng, S, D, E, K, 1, bias=True)
+    fmt, mode = (4, 0) if olmoe else (7, 1)
+    layer = Layer(rng, fmt, D, I, E, shared=not olmoe, distinct=4 if olmoe else None)
+    x, W, bias = make_router_inputs(rng, S, D, E, K, mode, bias=not olmoe)
     hs = layer.upload(session)
     g_, ga = tensor_array([t[0] for t in hs[:E]])
     u_, ua = tensor_array([t[1] for t in hs[:E]])
     d_, da = tensor_array([t[2] for t in hs[:E]])
-    cfg = ColiHipMoeConfig(D, I, E, K, 1, 1, 0.0, 2.5, 1)
-    m = C.c_void_p()
-    assert b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(W), f32p(bias), g_, u_, d_, hs[E][0], hs[E][1],
-                            hs[E][2])
+    if olmoe:
+        cfg = ColiHipMoeConfig(D, I, E, K, 0, 0, 0.0, 1.0, 0)
+        m = C.c_void_p()
+        assert b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(W), None, g_, u_, d_, None, None, None)
+    else:
+        cfg = ColiHipMoeConfig(D, I, E, K, 1, 1, 0.0, 2.5, 1)
+        m = C.c_void_p()
+        assert b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(W), f32p(bias), g_, u_, d_, hs[E][0], hs[E][1],
+                                hs[E][2])
     xd = _dev(b, np.ascontiguousarray(x))
     x2d = _dev(b, np.ascontiguousarray(x[::-1] * 2))
     od = b.cuda_pipe_alloc(0, S * D * 4)
@@ -115,6 +123,4 @@ def test_moe_graph_replays_match_eager(session, D, E):
         b.hip_moe_free(m)
         for p in (xd, x2d, od, o2d):
             b.cuda_pipe_free(0, p)
-        for t in hs:
-            for hh in t:
-                session.free(hh)
+        free_handles(session, hs)
