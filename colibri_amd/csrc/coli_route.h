@@ -269,8 +269,9 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
             lg[j0 + jj] = v;
         }
     }
-    // weight source pv (also in LDS, for the fallback slots) and selection score cv
-    float cv[JM], pv[JM];
+    // the weight source of each expert goes to LDS (p, read back for the
+    // selected slots), its selection score to cv
+    float cv[JM];
     if (mode == 0) {
         float m = -1e30f;
 #pragma unroll
@@ -289,7 +290,6 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
             const float v = lg[j] / sum;
             if (j < nmine) p[lane + 64 * j] = v;
             cv[j] = v;
-            pv[j] = v;
         }
     } else if (mode == 3) {
         // DeepSeek-V4: sqrt of the stable softplus (c/deepseek_v4.c:1368-1392)
@@ -299,7 +299,6 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
             const float v = sqrtf(fmaxf(z, 0.0f) + log1pf(expf(-fabsf(z))));
             if (j < nmine) p[lane + 64 * j] = v;
             cv[j] = v + bs[j];
-            pv[j] = v;
         }
     } else {
 #pragma unroll
@@ -307,7 +306,6 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
             const float v = 1.0f / (1.0f + expf(-lg[j]));
             if (j < nmine) p[lane + 64 * j] = v;
             cv[j] = v + bs[j];
-            pv[j] = v;
         }
     }
     if (!live) return;
