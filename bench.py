@@ -132,9 +132,12 @@ class Bench:
                 c = state["c"] % copies
                 state["c"] += 1
                 ok = b.hip_gemm_prep_dev(ups[c], xd, B)
-                ok &= b.hip_gemm_run_dev(ups[c], hd, B)
-                ok &= b.hip_gemm_prep_dev(downs[c], hd, B)
-                ok &= b.hip_gemm_run_dev(downs[c], yd, B)
+                # the up GEMV also writes h as the down GEMV's fragments
+                # (from its epilogue) where that replaces a fragment build
+                # (returns 2 then, 1 when it ran alone)
+                ok = ok and b.hip_gemm_run_dev_emit(ups[c], hd, B, downs[c])
+                ok = ok and b.hip_gemm_prep_dev(downs[c], hd, B)
+                ok = ok and b.hip_gemm_run_dev(downs[c], yd, B)
                 if not ok:
                     raise RuntimeError("GEMV launch failed")
 
@@ -171,12 +174,20 @@ class Bench:
         for B in BATCHES:
             rec = {}
             for name, mats, (O, I), xin, yout in (("up", ups, UP, xd, hd), ("down", downs, DOWN, hd, yd)):
+                # each kernel as the step runs it: up with its epilogue
+                # emitting h, down on the emitted fragments (where the step
+                # emits them)
+                if name == "down":
+                    assert b.hip_gemm_prep_dev(ups[0], xd, B)
+                    assert b.hip_gemm_run_dev_emit(ups[0], hd, B, downs[0])
                 assert b.hip_gemm_prep_dev(mats[0], xin, B)
+                run = ((lambda m: b.hip_gemm_run_dev_emit(m, yout, B, downs[0])) if name == "up"
+                       else (lambda m: b.hip_gemm_run_dev(m, yout, B)))
                 # the first run launches any deferred fragment prep, outside the graph
-                assert b.hip_gemm_run_dev(mats[0], yout, B)
+                assert run(mats[0])
                 with hrt.Graph(self.stream) as g2:
                     for c in range(copies):
-                        assert b.hip_gemm_run_dev(mats[c], yout, B)
+                        assert run(mats[c])
                 g2.launch()
                 hrt.device_sync()
                 a0, a1 = hrt.Event(), hrt.Event()

@@ -111,6 +111,7 @@ _SIGS = {
     "coli_hip_gemm_prep_dev": ([_tp, _vp, _i], _i),
     "coli_hip_pipe_gemm_noalloc": ([_tp, _vp, _vp, _i], _i),
     "coli_hip_gemm_run_dev": ([_tp, _vp, _i], _i),
+    "coli_hip_gemm_run_dev_emit": ([_tp, _vp, _i, _tp], _i),
     "coli_hip_tensor_stream_bytes": ([_tp], _sz),
     "coli_hip_tensor_kind": ([_tp], _i),
 }

@@ -169,7 +169,12 @@ __device__ __forceinline__ float swiglu_out(float g, float u, float limit) {
 
 // Output of one lane for batch row `brow` of the problem: output row
 // rt*16 + (lane & 15) of every live tile, scaled back by the row's 2^E; for
-// DUAL, silu(gate) * up of the paired tiles.
+// DUAL, silu(gate) * up of the paired tiles. With a.ehi (plain matrix, R
+// even), the outputs are also written as the consuming GEMV's activation
+// fragments: tiles r, r + 1 (rt[r] even) are one 32-column group of its
+// input, whose exponent E' (max|y| * 2^-E' in [2^14, 2^15) over the group,
+// as coli_prep_frag takes it over a row) the sixteen lanes of the row agree
+// on by a DPP maximum; hi / lo are split and placed as coli_prep_frag does.
 template <int R, bool DUAL>
 __device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiProb &pr, int bt, const int (&rt)[R],
                                               const bool (&live)[R], const float (&v)[R], int brow, int lane,
@@ -177,19 +182,59 @@ __device__ __forceinline__ void gemv_epilogue(const ColiGemvArgs &a, const ColiP
     constexpr int RT = DUAL ? R / 2 : R;
     const int nb = min(16, pr.nrows - 16 * bt);
     if (brow >= nb) return;
-    float *orow = a.out + (size_t)(pr.out_row0 + 16 * bt + brow) * a.ldo;
+    const int orow_i = pr.out_row0 + 16 * bt + brow;
+    float *orow = a.out + (size_t)orow_i * a.ldo;
+    float y[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) {
-        if (!live[r]) continue;
         const int o = rt[r] * 16 + (lane & 15);
-        if (o >= a.O) continue;
+        y[r] = 0.0f;
+        if (!live[r] || o >= a.O) continue;
         if constexpr (DUAL) {
             float gv = ldexpf(v[r], E), uv = ldexpf(v[r + RT], E);
-            orow[o] = swiglu_out(gv, uv, a.swiglu_limit);
+            y[r] = swiglu_out(gv, uv, a.swiglu_limit);
         } else {
-            orow[o] = ldexpf(v[r], E);
+            y[r] = ldexpf(v[r], E);
+        }
+        orow[o] = y[r];
+    }
+    if constexpr (!DUAL && R % 2 == 0) {
+        if (!a.ehi) return;
+#pragma unroll
+        for (int r = 0; r < R; r += 2) {
+            if (!live[r]) continue;   // wave-uniform
+            float m = dpp_max16(fmaxf(fabsf(y[r]), fabsf(y[r + 1])));
+            int Eg = 0;
+            if (m > 0.0f && isfinite(m)) {
+                frexpf(m, &Eg);
+                Eg -= 15;
+            }
+            Eg = min(113, max(-126, Eg));
+            const int g = rt[r] >> 1;
+            const size_t rbase = (size_t)orow_i * a.estride + (size_t)g * 32;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int c = 16 * h + (lane & 15), off = c & 7;
+                float yy = ldexpf(y[r + h], -Eg);
+                int t = off;
+                if (a.eint4) {
+                    t = (off & 1) ? 4 + (off >> 1) : (off >> 1);
+                    if (off & 1) yy *= 0.0625f;
+                }
+                const _Float16 hi = (_Float16)yy;
+                const size_t idx = rbase + (c >> 3) * 8 + t;
+                a.ehi[idx] = hi;
+                a.elo[idx] = (_Float16)(yy - (float)hi);
+            }
+            if ((lane & 15) == 0) a.eexp[((size_t)(g >> 2) * a.erows + orow_i) * 4 + (g & 3)] = (uint8_t)(int8_t)Eg;
         }
     }
+}
+
+// Group exponent j (signed byte j of the row's word) and its 2^E.
+__device__ __forceinline__ int gexp_of(uint32_t word, int j) { return (int)(int8_t)(word >> (8 * j)); }
+__device__ __forceinline__ float gexp_pow2(uint32_t word, int j) {
+    return __uint_as_float((uint32_t)(gexp_of(word, j) + 127) << 23);
 }
 
 // ---- LDS DMA rings (gemv_dma.hip, gemm.hip) ----

@@ -53,6 +53,14 @@ struct FragSet {
     const float *px = nullptr;
     int pld = 0, pnrows = 0, pK = 0, pint4 = 0;
     const int *psrc = nullptr, *pnrows_dev = nullptr;
+    // Fragments emitted by a GEMV's epilogue (coli_hip_gemm_run_dev_emit):
+    // rows [0, erows) of the output esrc, K = eK, one exponent per (row,
+    // group) in gexp ([quad][erows_pad][4] signed bytes). Any other use of
+    // the set clears `emitted`.
+    DevBuf gexp;
+    bool emitted = false;
+    const float *esrc = nullptr;
+    int erows = 0, erows_pad = 0, eK = 0;
 };
 
 struct DevCtx {
@@ -64,6 +72,7 @@ struct DevCtx {
     DevBuf x, h, y, g, u, partial, prob, zeros, stage_w, stage_s, qdq, flags;
     DevBuf rslot, rw, tmp_tiles, tmp_scales, split_cnt, idot_y, idot_sx;
     FragSet frag[4];                   // 0/1: inputs (int4 / fp4 order), 2/3: hidden rows
+    int dense_set[2] = {0, 1};         // set the next coli_hip_gemm_run_dev reads, per order (gemm_prep)
     DevBuf pipe[COLI_PIPE_SLOTS];
     // pinned staging
     PinBuf host_x, host_y, host_prob, host_small;
@@ -176,9 +185,18 @@ struct GemvScratch {
 // One tiled GEMV over `nprob` problems (descriptors on the device, or one
 // inline problem) reading fragment set `set` (or ws's buffers, allocating
 // nothing, when ws is given).
+// Emission request of run_gemv: write the output also as fragment set
+// `set` for a consumer of the given order (see ColiGemvArgs::ehi); `done`
+// reports whether the launch could (plain inline matrix, R even, no K split).
+struct GemvEmit {
+    int set;
+    int int4_order;
+    bool done;
+};
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
-             const ColiProb *inline_prob = nullptr, float swiglu_limit = 0.0f, const GemvScratch *ws = nullptr);
+             const ColiProb *inline_prob = nullptr, float swiglu_limit = 0.0f, const GemvScratch *ws = nullptr,
+             GemvEmit *emit = nullptr);
 // One grouped GEMM over a device work list of (problem << 16 | 64-row tile).
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,

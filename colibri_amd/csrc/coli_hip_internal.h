@@ -84,6 +84,19 @@ struct ColiGemvArgs {
     float swiglu_limit;       // > 0: DeepSeek-V4 clamped SwiGLU in the DUAL epilogue
     float *partial;           // split-K partials: [instance][split][R][NB4][64]
     int *split_cnt;           // split-K arrival counters, one per instance; zero between launches
+    // Fragments emitted by the GEMV that produced x (coli_hip_gemm_run_dev_emit):
+    // one exponent per (fragment row, 32-column group) instead of xexp, as
+    // signed bytes E (-126 .. 113), laid out [quad][gexp_rows][4 groups].
+    // Null: per-row xexp.
+    const uint8_t *gexp;
+    int gexp_rows;
+    // Emission of this GEMV's output (single plain matrix, R even, no K
+    // split) as the fragments of the GEMV that consumes it: hi / lo halves
+    // [row][estride] in that GEMV's A-operand order (eint4: int4 order with
+    // the high-nibble columns scaled by 1/16), exponents as gexp above.
+    _Float16 *ehi, *elo;
+    uint8_t *eexp;
+    int estride, erows, eint4;
 };
 
 

@@ -135,6 +135,7 @@ static int ngp_of(int K) { return (K + 127) / 128 * 4; }
 static int record_frags(FragSet &f, const float *x, int ld, int nrows, int K, int int4_order, const int *src_rows,
                         const int *nrows_dev) {
     if (!x || nrows < 0 || K < 1 || ld < K) return 0;
+    f.emitted = false;
     f.pending = true;
     f.px = x;
     f.pld = ld;
@@ -220,11 +221,20 @@ static bool xstage_enabled() {
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
-             const ColiProb *inline_prob, float swiglu_limit, const GemvScratch *ws) {
+             const ColiProb *inline_prob, float swiglu_limit, const GemvScratch *ws, GemvEmit *emit) {
+    if (emit) emit->done = false;
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
-    GemvLaunchPlan pl = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
+    const GemvLaunchPlan tiles_plan = plan_gemv(ctx, nprob, n_bt, nrt, nq, dual, max_rows);
+    GemvLaunchPlan pl = tiles_plan;
     plan_dma(ctx, pl, kind, nprob, n_bt, nrt, nq, dual, max_rows);
+    // emitted fragments on the LDS-ring kernel: their exponents are staged
+    // beside the ring, which must still fit
+    if (pl.dma && !ws && ctx->frag[set].emitted &&
+        (long)pl.W * pl.PD * dma_slot_bytes(kind, pl.R, max_rows) +
+                ((long)nq * 4 * ((std::min(16, max_rows) + 3) / 4) + 63) / 64 * 256 >
+            160 * 1024)
+        pl = tiles_plan;
     size_t inst = (size_t)nprob * n_bt * pl.rbpp;
     const size_t part_bytes = inst * pl.splits * pl.R * 4 * 64 * sizeof(float);
     if (pl.splits > 1) {
@@ -303,6 +313,36 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.swiglu_limit = swiglu_limit;
     a.partial = ws ? ws->partial : (float *)ctx->partial.p;
     a.split_cnt = ws ? ws->split_cnt : (int *)ctx->split_cnt.p;
+    if (f.emitted && !ws) {
+        // fragments emitted by the producing GEMV: per-group exponents, lo
+        // parts always taken (a lo_gen of 0 passes every flag)
+        a.gexp = (const uint8_t *)f.gexp.p;
+        a.gexp_rows = f.erows_pad;
+        a.lo_gen = 0;
+    }
+    if (emit && !ws && inline_prob && !dual && pl.splits == 1 && pl.R % 2 == 0 && O % 128 == 0 && max_rows <= 16) {
+        FragSet &e = ctx->frag[emit->set];
+        const int rows_pad = (max_rows + 15) / 16 * 16;
+        const size_t halves = (size_t)max_rows * O;
+        if (!reserve(ctx, &e.hi, halves * 2, 0) || !reserve(ctx, &e.lo, halves * 2, 0) ||
+            !reserve(ctx, &e.gexp, (size_t)(O / 128) * rows_pad * 4, 0))
+            return 0;
+        e.pending = false;
+        e.px = nullptr;
+        e.psrc = nullptr;
+        e.emitted = false;   // set by the caller once the launch is queued
+        e.erows = max_rows;
+        e.erows_pad = rows_pad;
+        e.eK = O;
+        e.esrc = out;
+        a.ehi = (_Float16 *)e.hi.p;
+        a.elo = (_Float16 *)e.lo.p;
+        a.eexp = (uint8_t *)e.gexp.p;
+        a.estride = O;
+        a.erows = rows_pad;
+        a.eint4 = emit->int4_order;
+        emit->done = true;
+    }
     if (pl.dma) return hip_check(coli_launch_gemv_dma(kind, &a, pl.R, dual ? 1 : 0, pl.W, pl.PD, max_rows, ctx->stream),
                               "gemv launch");
     return hip_check(coli_launch_gemv(kind, &a, pl.R, dual ? 1 : 0, pl.W, max_rows, ctx->stream), "gemv launch");
@@ -697,16 +737,45 @@ extern "C" int coli_cuda_shared_mlp_w4a16(ColiCudaTensor *gate, ColiCudaTensor *
 // single-matrix GEMV / GEMM
 // ---------------------------------------------------------------------------
 // Fragments of x_dev[S, I] for tensor t (input set of t's kind).
+// Records x_dev's S rows as t's input. When the GEMV that wrote x_dev
+// emitted them as fragments of t's order (coli_hip_gemm_run_dev_emit), the
+// next gemm_run reads those instead and no prep runs.
 static int gemm_prep(DevCtx *ctx, ColiCudaTensor *t, const float *x_dev, int S) {
+    const int order = t->kind == COLI_KIND_FP4 ? 1 : 0;
+    const int hidden = frag_set_of(t->kind, true);
+    const FragSet &h = ctx->frag[hidden];
+    if (h.emitted && h.esrc == x_dev && h.erows == S && h.eK == t->I) {
+        ctx->dense_set[order] = hidden;
+        return 1;
+    }
+    ctx->dense_set[order] = frag_set_of(t->kind, false);
     return make_frags(ctx, frag_set_of(t->kind, false), x_dev, t->I, S, t->I, t->kind != COLI_KIND_FP4);
+}
+
+// A write to y_dev by our own GEMV makes fragments emitted from it stale.
+static void invalidate_emitted(DevCtx *ctx, const float *y_dev) {
+    for (int s = 2; s < 4; s++)
+        if (ctx->frag[s].emitted && ctx->frag[s].esrc == y_dev) ctx->frag[s].emitted = false;
 }
 
 // GEMV of t over the prepared fragments of S rows -> y_dev[S, O]; the
 // problem travels in the kernel arguments (no descriptor, no host sync).
-static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S) {
+// With next: y_dev is also emitted as next's input fragments (set 2 / 3).
+static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S, const ColiCudaTensor *next = nullptr) {
     const ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
-    return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, frag_set_of(t->kind, false),
-                    nullptr, y_dev, t->O, &p);
+    const int set = ctx->dense_set[t->kind == COLI_KIND_FP4 ? 1 : 0];
+    invalidate_emitted(ctx, y_dev);
+    if (!next) {
+        return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O,
+                        &p);
+    }
+    GemvEmit em = {frag_set_of(next->kind, true), next->kind != COLI_KIND_FP4, false};
+    if (em.set == set) return 0;   // the set read by this launch cannot be written by it
+    if (!run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O, &p,
+                  0.0f, nullptr, &em))
+        return 0;
+    ctx->frag[em.set].emitted = em.done;
+    return em.done ? 2 : 1;
 }
 
 // y_dev[S, O] = x_dev[S, I] W^T on the stream (tensor already resident).
@@ -728,6 +797,30 @@ extern "C" int coli_hip_gemm_run_dev(ColiCudaTensor *t, float *y_dev, int S) {
     DevCtx *ctx = ctx_of(t->device);
     if (!bind_ctx(ctx)) return 0;
     return gemm_run(ctx, t, y_dev, S);
+}
+
+// As coli_hip_gemm_run_dev, and the output rows are also written as the
+// activation fragments of `next` (next->I == t->O), which a following
+// coli_hip_gemm_prep_dev(next, y_dev, S) then uses without a prep launch.
+// Emitted only where it pays and the launch allows (2..16 rows whose f32
+// form the consumer would not convert itself, t->O a multiple of 128, a
+// plain launch with an even number of row tiles per wave and no K split);
+// otherwise the prep runs as usual. The caller must not modify y_dev before
+// that prep's GEMV has run. Returns 2 when the fragments were emitted, 1 when
+// only the GEMV ran, 0 on failure.
+extern "C" int coli_hip_gemm_run_dev_emit(ColiCudaTensor *t, float *y_dev, int S, const ColiCudaTensor *next) {
+    if (!t || !y_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
+    if (!next || next->kind == COLI_KIND_GENERIC || next->I != t->O || next->device != t->device) return 0;
+    DevCtx *ctx = ctx_of(t->device);
+    if (!bind_ctx(ctx)) return 0;
+    // the consumer converts up to 32768 f32 activations of 1..4 rows itself.
+    // COLI_HIP_EMIT=0 never emits, =force emits wherever the launch allows
+    // (tests and measurements).
+    const char *e = std::getenv("COLI_HIP_EMIT");
+    bool worth = S > 1 && S <= 16 && (long)S * next->I > 32768;
+    if (e && e[0] == '0') worth = false;
+    if (e && std::strcmp(e, "force") == 0) worth = S <= 16;
+    return gemm_run(ctx, t, y_dev, S, worth ? next : nullptr);
 }
 
 // fmt=2 with int8 activations (c/colibri.c:937-945, matmul_i4_idot): the

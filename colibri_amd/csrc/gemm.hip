@@ -46,6 +46,11 @@
 
 #include "coli_device.h"
 
+// deepest ring a short tile gets
+#ifndef COLI_GM_PDMAX
+#define COLI_GM_PDMAX 6
+#endif
+
 // Ring geometry. A stage holds the activation chunks of the tile's live
 // 16-row subtiles (NM of them, 4 KiB each for the hi half, as much again for
 // lo) and each wave's weight tiles + scales; the ring takes as many stages as
@@ -64,7 +69,7 @@ struct GmGeom {
     static constexpr int act(int nm, bool lo) { return nm * 4096 * (lo ? 2 : 1); }
     static constexpr int stage(int nm, bool lo, int rn) { return act(nm, lo) + kW * wslot(rn); }
     static constexpr int pd(int nm, bool lo, int rn) {
-        return (kLds - kRing) / stage(nm, lo, rn) > 6 ? 6 : (kLds - kRing) / stage(nm, lo, rn);
+        return (kLds - kRing) / stage(nm, lo, rn) > COLI_GM_PDMAX ? COLI_GM_PDMAX : (kLds - kRing) / stage(nm, lo, rn);
     }
     // tiles per pass: all of the wave's tiles when three stages fit, else two
     // passes over K of half as many (the activations are staged twice)

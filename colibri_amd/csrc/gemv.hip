@@ -233,6 +233,7 @@ struct Stage {
     ScaleRegs<KIND> sc[R];
     half8v xh[4];
     half8v xl[LO ? 4 : 1];   // unused (and dead) unless the lo pass runs
+    u32x4 gx;                // group exponents of the lane's four result rows (GX only)
 };
 
 #ifndef COLI_PD
@@ -273,10 +274,15 @@ __device__ __forceinline__ void load_weights(Stage<KIND, R, true> &sg, bool vali
 // of iteration 0 into st[0] (before it knew whether lo fragments exist), so
 // the first requests leave the CU as early as possible. xoff = the lane's
 // byte offset of its fragment row and k-slice inside xh / xl.
-template <int KIND, int R, int NB4, int W, bool LO, bool PEEL>
+// GX: the fragments carry one exponent per (row, group) (emitted by the GEMV
+// that produced x): gx + q * gxq holds the four group exponents of the
+// lane's result rows 4 (lane / 16) + i, and each group's MFMA result is
+// scaled by 2^E of its row along with the group scale.
+template <int KIND, int R, int NB4, int W, bool LO, bool PEEL, bool GX = false>
 __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, true> (&st)[COLI_PD], int q_first, int Q1,
                                            const TileRows<KIND, R> &rows, const uint8_t *xh, const uint8_t *xl,
-                                           uint32_t xoff, const void *zero, int lane) {
+                                           uint32_t xoff, const void *zero, int lane, const uint8_t *gx = nullptr,
+                                           size_t gxq = 0) {
     constexpr int PD = COLI_PD;
     if (q_first >= Q1) return;
     const int nit = (Q1 - q_first + W - 1) / W;
@@ -288,6 +294,7 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
             sg.xh[j] = *GPTR(half8v, qh + xoff + j * 64);
             if constexpr (LO) sg.xl[j] = *GPTR(half8v, ql + xoff + j * 64);
         }
+        if constexpr (GX) sg.gx = *GPTR(u32x4, gx + (size_t)q * gxq);
     };
     auto load = [&](Stage<KIND, R, true> &sg, int it) {
         const bool valid = it < nit;
@@ -298,6 +305,11 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
     auto compute = [&](const Stage<KIND, R, true> &sg) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
+            float f[NB4];
+            if constexpr (GX) {
+#pragma unroll
+                for (int i = 0; i < NB4; i++) f[i] = gexp_pow2(sg.gx[i], j);
+            }
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 half8v bw = unpack_b<KIND>(sg.w[r][j]);
@@ -305,7 +317,7 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
                 if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg.xl[j], bw, d, 0, 0, 0);
                 float scl = sg.sc[r].get(j);
 #pragma unroll
-                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
+                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], GX ? scl * f[i] : scl, acc[r][i]);
             }
         }
     };
@@ -314,6 +326,7 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
 #pragma unroll
         for (int j = 0; j < 4; j++) st[0].xl[j] = *GPTR(half8v, ql + xoff + j * 64);
     }
+    if constexpr (GX) st[0].gx = *GPTR(u32x4, gx + (size_t)q_first * gxq);
     if constexpr (PEEL) {
         // Two-stage ring unrolled by two, with a tail that issues no load past
         // the wave's last quad. Every path leaves the loop with the same loads
@@ -439,9 +452,13 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     }
 
     const bool use_lo = *a.haslo >= a.lo_gen;  // >=: stays correct under graph replay
+    // emitted fragments: exponents per (row, group), read with the fragments
+    const bool gx = INL && !DUAL && a.gexp;
+    const uint8_t *gxp = a.gexp + ((size_t)pr.xrow_off + 16 * bt + 4 * ks) * 4;
+    const size_t gxq = (size_t)a.gexp_rows * 4;
     // exponent of the batch row this wave finishes (used after the loop)
     int E_out = 0;
-    if (a.splits == 1 && wave < NB4) {
+    if (!gx && a.splits == 1 && wave < NB4) {
         const int brow = ks * 4 + wave;
         if (brow < nb) {
             const int br = pr.xrow_off + 16 * bt + brow;
@@ -454,8 +471,20 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
     for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
     // the peeled loop fits two waves per SIMD only in these variants
     constexpr bool PEEL = INL && W == 8 && KIND == COLI_KIND_I4_H && R >= 2;
-    if (use_lo) gemv_quads<KIND, R, NB4, W, true, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
-    else gemv_quads<KIND, R, NB4, W, false, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
+    if constexpr (INL && !DUAL) {
+        if (gx) {
+            // emitted fragments are f32 rows: their lo parts are always taken
+            gemv_quads<KIND, R, NB4, W, true, PEEL, true>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane, gxp,
+                                                          gxq);
+        } else if (use_lo) {
+            gemv_quads<KIND, R, NB4, W, true, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
+        } else {
+            gemv_quads<KIND, R, NB4, W, false, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
+        }
+    } else {
+        if (use_lo) gemv_quads<KIND, R, NB4, W, true, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
+        else gemv_quads<KIND, R, NB4, W, false, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
+    }
 
     // ---- intra-group reduction in fixed wave order; wave i finishes register i ----
 #pragma unroll
@@ -509,7 +538,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_tiles(ColiGemvArgs a) {
                 v[r] += __hip_atomic_load(a.partial + pbase + ((size_t)ss * R + r) * NB4 * 64, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
         const int brow = ks * 4 + i;
-        if (brow < nb) {
+        if (!gx && brow < nb) {
             const int br = pr.xrow_off + 16 * bt + brow;
             E_out = a.xexp[a.xrows ? a.xrows[br] : br];
         }

@@ -130,8 +130,10 @@ __device__ __forceinline__ bool f32_to_frags(uint8_t *x, int lane, int *E_out) {
 // (dynamic shared memory: hi [nq][256 B], lo [nq][256 B], exponents [nq]) while
 // its first weight stages are in flight; the stages then carry weights and
 // scales only.
-template <int KIND, int R, bool DUAL, int NB4, int W, int PD, int NXR, bool INL, bool F32, bool XS = false>
+template <int KIND, int R, bool DUAL, int NB4, int W, int PD, int NXR, bool INL, bool F32, bool XS = false,
+          bool GX = false>
 __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
+    static_assert(!GX || (INL && !F32 && !DUAL), "emitted fragments: one plain matrix, prepared fragments");
     using G = DmaGeom<KIND, R, NXR>;
     static_assert(!XS || (F32 && NXR == 1), "staged activations: f32, one row");
     static_assert(!F32 || NXR == 1 || NXR == 4, "f32 activations: one or four rows per stage");
@@ -280,9 +282,21 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
         return XF ? (uint32_t)(xrow * 16 + ((4 * j + ks) ^ xrow)) * 16 : (uint32_t)(j * 64 + ks * 16);
     };
 
-    auto compute = [&](int slot, auto lo_tag) {
+    // GX: prepared fragments emitted by the GEMV that produced x carry one
+    // exponent per (row, group); the exponents of the problem's rows of every
+    // quad are staged in LDS ([quad][gxs rows] words, gxs = the rows rounded
+    // up to a multiple of 4: little enough to keep two workgroups a CU) before
+    // the loop, and each group's MFMA result is scaled by 2^E of its row along
+    // with the group scale.
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs_lds[];
+    constexpr bool gx = GX;
+    const int gxs = 4 * ((nb + 3) >> 2);
+    auto compute = [&](int slot, auto lo_tag, int q) {
         constexpr bool LO = decltype(lo_tag)::value;
         const uint8_t *src = ring + slot * G::kSlot;
+        u32x4 ge = (u32x4){0u, 0u, 0u, 0u};
+        // (lanes of rows past the problem read the last group of four)
+        if constexpr (gx) ge = *(const u32x4 *)(xs_lds + ((size_t)q * gxs + 4 * min(ks, (gxs >> 2) - 1)) * 4);
         u32x4 w[R];
         ScaleRegs<KIND> sc[R];
         half8v xh[4], xl[LO ? 4 : 1];
@@ -304,8 +318,13 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
                 floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
                 const float scl = sc[r].get(j);
+                if constexpr (gx) {
 #pragma unroll
-                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
+                    for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(ldexpf(d[i], gexp_of(ge[i], j)), scl, acc[r][i]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
+                }
             }
         }
     };
@@ -355,8 +374,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
             for (int i = 0; i < NB4; i++) acc[r][i] += ldexpf(t[r][i], Ei[i]);
     };
 
-    // XS: the staged row (set up below, before the loop)
-    extern __shared__ __attribute__((aligned(16))) uint8_t xs_lds[];
+    // XS: the staged row (set up below, before the loop, in xs_lds)
     auto compute_xs = [&](int slot, int q, bool lo) {
         const uint8_t *src = ring + slot * G::kSlot;
         const uint8_t *xq = xs_lds + q * 256 + ks * 16;
@@ -480,9 +498,28 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
     auto run = [&](auto lo_tag) {
         constexpr bool LO = decltype(lo_tag)::value;
         constexpr int L = G::loads(LO);
+        // GX: the group exponents of the problem's rows, staged by LDS DMA
+        // (64 words per instruction, dealt over the waves) ahead of the first
+        // stages; one wait and barrier before the loop (every wave reaches it)
+        if constexpr (gx) {
+            const int words = nq * gxs;
+            for (int k = wave; k * 64 < words; k += W) {
+                const int e = k * 64 + lane, qe = min(e / gxs, nq - 1), row = min(e - (e / gxs) * gxs, nb - 1);
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)(a.gexp + ((size_t)qe * a.gexp_rows + pr.xrow_off + 16 * bt + row) * 4),
+                    (lds_void *)(xs_lds + k * 256), 4, 0, 0);
+            }
+        }
 #pragma unroll
         for (int s = 0; s < PD - 1; s++)
             if (s < nit) issue(s, s, LO);
+        if constexpr (gx) {
+            // the exponents went out first: at most the stages may remain
+            if (nit >= PD - 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PD - 1) * L) : "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
         for (int it0 = 0; it0 < nit; it0 += PD) {
 #pragma unroll
             for (int u = 0; u < PD; u++) {
@@ -494,18 +531,18 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
                 } else {
                     dma_wait_tail<L, PD>(nit - 1 - it);
                 }
-                compute(u, lo_tag);
+                compute(u, lo_tag, q_first + it * W);
             }
         }
     };
     if constexpr (XS) run_xs();
     else if constexpr (F32) run_f32();
-    else if (*a.haslo >= a.lo_gen) run(std::true_type{});   // >=: stays correct under graph replay
+    else if (gx || *a.haslo >= a.lo_gen) run(std::true_type{});   // >=: stays correct under graph replay
     else run(std::false_type{});
 
     // exponent of the batch row this wave finishes
     int E_out = 0;
-    if (!F32 && wave < NB4) {
+    if (!F32 && !gx && wave < NB4) {
         const int brow = ks * 4 + wave;
         if (brow < nb) {
             const int br = pr.xrow_off + 16 * bt + brow;
@@ -553,6 +590,17 @@ static hipError_t launch_dma6(const ColiGemvArgs &a, int blocks, hipStream_t st)
                 else
                     hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, false, F32, true>),
                                        dim3(blocks), dim3(64 * W), shm, st, a);
+                return hipGetLastError();
+            }
+        }
+        // emitted fragments: their group exponents staged in LDS
+        if constexpr (!F32 && !DUAL) {
+            if (a.gexp && !a.prob) {   // emitted fragments: their exponents staged beside the ring
+                const int gxs = 4 * ((min(16, a.prob0.nrows) + 3) / 4);
+                const size_t gshm = ((size_t)a.nq * gxs + 63) / 64 * 256;
+                if ((size_t)W * PD * G::kSlot + gshm > 160 * 1024) return hipErrorInvalidConfiguration;
+                hipLaunchKernelGGL((coli_gemv_dma<KIND, R, DUAL, NB4, W, PD, NXR, true, F32, false, true>),
+                                   dim3(a.rb_per_prob, 1, a.n_bt), dim3(64 * W), gshm, st, a);
                 return hipGetLastError();
             }
         }

@@ -135,6 +135,19 @@ int coli_hip_pipe_gemm_noalloc(ColiCudaTensor *tensor, float *y_dev, const float
  * of the same kind of tensor and the same S. */
 int coli_hip_gemm_prep_dev(ColiCudaTensor *tensor, const float *x_dev, int S);
 int coli_hip_gemm_run_dev(ColiCudaTensor *tensor, float *y_dev, int S);
+/* As coli_hip_gemm_run_dev, and the output rows are also written, from the
+ * GEMV's epilogue, as the activation fragments of `next` (next->I ==
+ * tensor->O, fp16 hi + lo with one exponent per row and 32-column group), so
+ * that a following coli_hip_gemm_prep_dev(next, y_dev, S) + run needs no
+ * fragment build (an FFN's up projection feeding its down projection).
+ * Emitted only where it pays and the launch allows it (2..16 rows whose f32
+ * form next's GEMV would not convert itself, tensor->O a multiple of 128, a
+ * plain launch with an even number of row tiles per wave and no K split);
+ * otherwise the later prep builds the fragments as usual. The caller must not
+ * modify y_dev between this call and that prep's run; another run writing
+ * y_dev drops the emitted fragments. Returns 2 when the fragments were
+ * emitted, 1 when only the GEMV ran, 0 on failure. */
+int coli_hip_gemm_run_dev_emit(ColiCudaTensor *tensor, float *y_dev, int S, const ColiCudaTensor *next);
 /* Fill n bytes of device memory with uniform pseudo-random bytes (seeded,
  * deterministic): synthetic weights for benchmarks without a host round trip. */
 int coli_hip_fill_random_u8(int device, void *dev, size_t n, unsigned long long seed);
