@@ -770,7 +770,11 @@ static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S, const C
                         &p);
     }
     GemvEmit em = {frag_set_of(next->kind, true), next->kind != COLI_KIND_FP4, false};
-    if (em.set == set) return 0;   // the set read by this launch cannot be written by it
+    // the set this launch reads (itself emitted) cannot be written by it: run
+    // without emitting, next's prep builds its fragments as usual
+    if (em.set == set)
+        return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O,
+                        &p);
     if (!run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O, &p,
                   0.0f, nullptr, &em))
         return 0;

@@ -159,3 +159,32 @@ def test_emitted_fragments_graph_replay(session, monkeypatch):
             b.cuda_pipe_free(0, p)
         session.free(up.h)
         session.free(down.h)
+
+
+def test_emitted_fragments_chain_of_three(session, monkeypatch):
+    """A -> B -> C with emission at every step: B reads the fragments A
+    emitted, so it cannot emit into the same set and runs without emitting
+    (returns 1); C's prep then builds its fragments. Every output within the
+    bar against the oracle on the GPU's own inputs."""
+    monkeypatch.setenv("COLI_HIP_EMIT", "force")
+    b = session.b
+    rng = np.random.default_rng(23)
+    D, H, S = 1024, 2048, 8
+    A, B, Cm = Mat(session, rng, "i4h", H, D), Mat(session, rng, "i4h", D, H), Mat(session, rng, "i4h", H, D)
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    xd = _dev(b, x)
+    ad, bd, cd = (b.cuda_pipe_alloc(0, S * n * 4) for n in (H, D, H))
+    try:
+        assert b.hip_gemm_prep_dev(A.h, xd, S) and b.hip_gemm_run_dev_emit(A.h, ad, S, B.h) == 2
+        assert b.hip_gemm_prep_dev(B.h, ad, S) and b.hip_gemm_run_dev_emit(B.h, bd, S, Cm.h) == 1
+        assert b.hip_gemm_prep_dev(Cm.h, bd, S) and b.hip_gemm_run_dev(Cm.h, cd, S)
+        a_out, b_out, c_out = _get(b, ad, (S, H)), _get(b, bd, (S, D)), _get(b, cd, (S, H))
+    finally:
+        for p in (xd, ad, bd, cd):
+            b.cuda_pipe_free(0, p)
+        for m in (A, B, Cm):
+            session.free(m.h)
+    for m, inp, got in ((A, x, a_out), (B, a_out, b_out), (Cm, b_out, c_out)):
+        ref, mag = m.ref(inp)
+        e = rel_err(got, ref, mag)
+        assert e.max() <= TOL, f"max rel err {e.max():.3e}"
