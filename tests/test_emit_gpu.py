@@ -188,3 +188,30 @@ def test_emitted_fragments_chain_of_three(session, monkeypatch):
         ref, mag = m.ref(inp)
         e = rel_err(got, ref, mag)
         assert e.max() <= TOL, f"max rel err {e.max():.3e}"
+
+
+@pytest.mark.parametrize("H,S", [(1000, 8), (2048, 1)])
+def test_emission_declined(session, monkeypatch, H, S):
+    """Where the launch cannot emit (up O not a multiple of 128) or it would
+    not pay (one row: the down GEMV converts its f32 row itself), the call
+    only runs the GEMV (returns 1) and the down GEMV's prep builds as usual."""
+    b = session.b
+    rng = np.random.default_rng(H + S)
+    D = 512
+    up, down = Mat(session, rng, "i4h", H, D), Mat(session, rng, "mx", D, H)
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    xd = _dev(b, x)
+    hd, yd = b.cuda_pipe_alloc(0, S * H * 4), b.cuda_pipe_alloc(0, S * D * 4)
+    try:
+        assert b.hip_gemm_prep_dev(up.h, xd, S) and b.hip_gemm_run_dev_emit(up.h, hd, S, down.h) == 1
+        assert b.hip_gemm_prep_dev(down.h, hd, S) and b.hip_gemm_run_dev(down.h, yd, S)
+        h, y = _get(b, hd, (S, H)), _get(b, yd, (S, D))
+    finally:
+        for p in (xd, hd, yd):
+            b.cuda_pipe_free(0, p)
+        session.free(up.h)
+        session.free(down.h)
+    for m, inp, got in ((up, x, h), (down, h, y)):
+        ref, mag = m.ref(inp)
+        e = rel_err(got, ref, mag)
+        assert e.max() <= TOL, f"max rel err {e.max():.3e}"
