@@ -736,8 +736,7 @@ extern "C" int coli_cuda_shared_mlp_w4a16(ColiCudaTensor *gate, ColiCudaTensor *
 // ---------------------------------------------------------------------------
 // single-matrix GEMV / GEMM
 // ---------------------------------------------------------------------------
-// Fragments of x_dev[S, I] for tensor t (input set of t's kind).
-// Records x_dev's S rows as t's input. When the GEMV that wrote x_dev
+// Records x_dev's S rows as t's input (fragment set of t's kind). When the GEMV that wrote x_dev
 // emitted them as fragments of t's order (coli_hip_gemm_run_dev_emit), the
 // next gemm_run reads those instead and no prep runs.
 static int gemm_prep(DevCtx *ctx, ColiCudaTensor *t, const float *x_dev, int S) {

@@ -459,7 +459,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
     const bool use_lo = *a.haslo >= a.lo_gen;  // >=: stays correct under graph replay
     // emitted fragments: exponents per (row, group), read with the fragments
     const bool gx = INL && !DUAL && a.gexp;
-    const uint8_t *gxp = a.gexp + ((size_t)pr.xrow_off + 16 * bt + 4 * ks) * 4;
+    const uint8_t *gxp = gx ? a.gexp + ((size_t)pr.xrow_off + 16 * bt + 4 * ks) * 4 : nullptr;
     const size_t gxq = (size_t)a.gexp_rows * 4;
     // exponent of the batch row this wave finishes (used after the loop)
     int E_out = 0;
