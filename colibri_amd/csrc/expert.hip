@@ -43,8 +43,14 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
     }
     p.rbpp = (nrt + RT - 1) / RT;
     long groups = (long)nprob * n_bt * p.rbpp;
+    // Many groups (the MoE layers of 16-21 rows: one per expert and row
+    // block): two waves each, whose longer share of K pipelines better
+    // (21-row verification 564 -> 552 us MXFP4, 709 -> 663 us int4 against
+    // four waves; DSV3 B16 unchanged at 445); few: four, or eight to split a
+    // long K.
     p.W = 4;
     if (groups * 4 < target_waves && nq >= 16) p.W = 8;
+    if (groups >= target_waves) p.W = 2;
     // K splits cost a partial round trip and a serial tail: only worth it
     // when the row tiles alone leave the chip under 4 waves per CU (long-K,
     // narrow-O shapes such as a dense down projection).
@@ -58,7 +64,7 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
     if (const char *ov = std::getenv("COLI_HIP_PLAN")) {
         int r = 0, w = 0, sp = 0;
         if (std::sscanf(ov, "%d,%d,%d", &r, &w, &sp) == 3 && (r == 1 || r == 2 || r == 4) &&
-            (w == 4 || w == 8 || w == 16) && sp >= 1 && !(dual && r == 1) && !(r == 4 && w == 16)) {
+            (w == 2 || w == 4 || w == 8 || w == 16) && sp >= 1 && !(dual && r == 1) && !(r == 4 && w == 16)) {
             p.R = r;
             RT = dual ? r / 2 : r;
             p.rbpp = (nrt + RT - 1) / RT;

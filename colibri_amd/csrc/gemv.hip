@@ -376,13 +376,13 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
 // no check precedes the first weight loads, so the kernel arguments arrive
 // as one batch of scalar loads and the HBM requests follow at once (early
 // exits split the scalar loads into dependent round trips).
-// MXFP4 on device descriptors with four waves (the MoE layers of 16-21 rows)
-// is held to 168 VGPRs, three waves a SIMD instead of two at 176: a few
-// registers spill, and the layers still run 4-7 % faster (DSV3 B16 460 ->
-// 444 us, 21-row verification 603 -> 564 us); int4 spills more there and
-// was slower (701 -> 750 us), so it keeps two.
+// MXFP4 on device descriptors with two or four waves (the MoE layers of
+// 16-21 rows) is held to 168 VGPRs, three waves a SIMD instead of two at
+// 176: a few registers spill, and the layers still ran 4-7 % faster (DSV3
+// B16 460 -> 444 us, 21-row verification 603 -> 564 us, four waves); int4
+// spills more there and was slower (701 -> 750 us), so it keeps two.
 template <int KIND, int R, bool DUAL, int NB4, int W, bool INL>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W == 4 && !INL ? 3 : 1, 8))) void coli_gemv_tiles(ColiGemvArgs a) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W <= 4 && !INL ? 3 : 1, 8))) void coli_gemv_tiles(ColiGemvArgs a) {
     constexpr int RT = DUAL ? R / 2 : R;
     __shared__ float red[W][R * NB4][64];
     __shared__ int split_last;
@@ -461,13 +461,20 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
     const bool gx = INL && !DUAL && a.gexp;
     const uint8_t *gxp = gx ? a.gexp + ((size_t)pr.xrow_off + 16 * bt + 4 * ks) * 4 : nullptr;
     const size_t gxq = (size_t)a.gexp_rows * 4;
-    // exponent of the batch row this wave finishes (used after the loop)
-    int E_out = 0;
-    if (!gx && a.splits == 1 && wave < NB4) {
-        const int brow = ks * 4 + wave;
-        if (brow < nb) {
-            const int br = pr.xrow_off + 16 * bt + brow;
-            E_out = a.xexp[a.xrows ? a.xrows[br] : br];
+    // exponents of the batch rows this wave finishes (used after the loop):
+    // result registers wave, wave + W, ... (one unless W < NB4)
+    constexpr int NI = (NB4 + W - 1) / W;
+    int E_out[NI];
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        E_out[k] = 0;
+        const int ii = wave + k * W;
+        if (!gx && a.splits == 1 && ii < NB4) {
+            const int brow = ks * 4 + ii;
+            if (brow < nb) {
+                const int br = pr.xrow_off + 16 * bt + brow;
+                E_out[k] = a.xexp[a.xrows ? a.xrows[br] : br];
+            }
         }
     }
 
@@ -497,6 +504,25 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
 #pragma unroll
         for (int i = 0; i < NB4; i++) red[wave][r * NB4 + i][lane] = acc[r][i];
     __syncthreads();
+    if constexpr (W < NB4) {
+        // fewer waves than result registers (never with a K split across
+        // groups): each wave finishes registers wave, wave + W, ...
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int ii = wave + k * W;
+            if (ii >= NB4) break;
+            float vv[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float t = red[0][r * NB4 + ii][lane];
+#pragma unroll
+                for (int w = 1; w < W; w++) t += red[w][r * NB4 + ii][lane];
+                vv[r] = t;
+            }
+            gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, vv, ks * 4 + ii, lane, E_out[k]);
+        }
+        return;
+    }
     const int i = wave;
     float v[R];
     if (i < NB4) {
@@ -545,11 +571,11 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         const int brow = ks * 4 + i;
         if (!gx && brow < nb) {
             const int br = pr.xrow_off + 16 * bt + brow;
-            E_out = a.xexp[a.xrows ? a.xrows[br] : br];
+            E_out[0] = a.xexp[a.xrows ? a.xrows[br] : br];
         }
     }
     if (i >= NB4) return;
-    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, ks * 4 + i, lane, E_out);
+    gemv_epilogue<R, DUAL>(a, pr, bt, rt, live, v, ks * 4 + i, lane, E_out[0]);
 }
 
 // ---------------------------------------------------------------------------
@@ -701,6 +727,12 @@ static hipError_t launch_w(const ColiGemvArgs &a, int W, int blocks, hipStream_t
             else hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 16, false>), grid, dim3(1024), 0, st, a);
             return hipGetLastError();
         }
+    }
+    // two waves: on device descriptors and without a K split only (the
+    // split protocol has each wave finish one result register)
+    if (W == 2 && !inl && a.splits == 1) {
+        hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 2, false>), grid, dim3(128), 0, st, a);
+        return hipGetLastError();
     }
     if (W >= 8) {
         if (inl) hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 8, true>), grid, dim3(512), 0, st, a);
