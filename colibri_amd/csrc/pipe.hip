@@ -105,11 +105,15 @@ __global__ __launch_bounds__(256) void coli_router_gemm(const float *__restrict_
 #pragma unroll
         for (int b = 0; b < 2; b++) acc[a][b] = (floatx4){0.f, 0.f, 0.f, 0.f};
     const bool vec = (D & 3) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)W & 15) == 0;
-    for (int d0 = d_begin; d0 < d_end; d0 += COLI_RG_BK) {
-        // stage 64 rows x 32 columns of x and of W: thread t loads float4 t and t + 256
+    // 64 rows x COLI_RG_BK columns of x and of W per step: thread t loads
+    // float4 t, t + 256, ... of each, one step ahead of the MFMAs (the loads
+    // of the next step are in flight while this one is computed)
+    constexpr int NH = COLI_RG_BK / 16, CPR = COLI_RG_BK / 4;   // float4 per thread; per row
+    float4 xr[NH], wr4[NH];
+    auto load = [&](int d0) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int f = threadIdx.x + 256 * h, r = f >> 3, c = (f & 7) * 4;
+        for (int h = 0; h < NH; h++) {
+            const int f = threadIdx.x + 256 * h, r = f / CPR, c = (f % CPR) * 4;
             const int d = d0 + c;
             float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = xv;
             if (vec && d + 4 <= d_end) {
@@ -126,10 +130,20 @@ __global__ __launch_bounds__(256) void coli_router_gemm(const float *__restrict_
                 xv = make_float4(xa[0], xa[1], xa[2], xa[3]);
                 wv = make_float4(wa[0], wa[1], wa[2], wa[3]);
             }
-            xs[r][c] = xv.x; xs[r][c + 1] = xv.y; xs[r][c + 2] = xv.z; xs[r][c + 3] = xv.w;
-            ws[r][c] = wv.x; ws[r][c + 1] = wv.y; ws[r][c + 2] = wv.z; ws[r][c + 3] = wv.w;
+            xr[h] = xv;
+            wr4[h] = wv;
+        }
+    };
+    load(d_begin);
+    for (int d0 = d_begin; d0 < d_end; d0 += COLI_RG_BK) {
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            const int f = threadIdx.x + 256 * h, r = f / CPR, c = (f % CPR) * 4;
+            xs[r][c] = xr[h].x; xs[r][c + 1] = xr[h].y; xs[r][c + 2] = xr[h].z; xs[r][c + 3] = xr[h].w;
+            ws[r][c] = wr4[h].x; ws[r][c + 1] = wr4[h].y; ws[r][c + 2] = wr4[h].z; ws[r][c + 3] = wr4[h].w;
         }
         __syncthreads();
+        if (d0 + COLI_RG_BK < d_end) load(d0 + COLI_RG_BK);
         // A lane (m = lane % 16, k = lane / 16) of each 16 x 16 x 4 step; B likewise
 #pragma unroll
         for (int k0 = 0; k0 < COLI_RG_BK; k0 += 4) {
