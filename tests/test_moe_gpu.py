@@ -172,10 +172,18 @@ def make_moe(session, layer, W, b, K, mode, norm_topk=0, topp=0.0, routed_scale=
     return m, hs
 
 
-@pytest.mark.parametrize("fmt,mode,S,shared", [(4, 0, 1, False), (4, 0, 5, False), (7, 2, 1, True),
-                                               (7, 2, 16, True), (4, 1, 21, False), (7, 1, 3, False),
-                                               (4, 1, 80, True), (7, 2, 150, False)])
-def test_moe_layer(session, fmt, mode, S, shared):
+# plan: the GEMV decomposition pinned (COLI_HIP_PLAN "R,W,splits"; empty: the
+# planner's). Two waves per group is what the planner takes for the many
+# groups of full-size 16-21-row layers; each wave then finishes two of the
+# four result registers, pinned here at small sizes.
+@pytest.mark.parametrize("fmt,mode,S,shared,plan", [(4, 0, 1, False, ""), (4, 0, 5, False, ""),
+                                                    (7, 2, 1, True, ""), (7, 2, 16, True, ""),
+                                                    (4, 1, 21, False, ""), (7, 1, 3, False, ""),
+                                                    (4, 1, 80, True, ""), (7, 2, 150, False, ""),
+                                                    (7, 2, 16, True, "4,2,1"), (4, 1, 21, False, "4,2,1"),
+                                                    (4, 0, 5, False, "4,2,1")])
+def test_moe_layer(session, monkeypatch, fmt, mode, S, shared, plan):
+    monkeypatch.setenv("COLI_HIP_PLAN", plan)
     rng = np.random.default_rng(100 + fmt * 10 + mode + S)
     D, I, E, K = 512, 256, 32, 4
     layer = Layer(rng, fmt, D, I, E, shared=shared)
