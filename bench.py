@@ -61,6 +61,114 @@ def fp16_scales(rng, O, ng):
     return np.abs(rng.standard_normal((O, ng)) * 0.01).astype(np.float16).astype(np.float32)
 
 
+def cpu_baseline(secs):
+    """The reference's CPU path on this host (OpenMP over
+    the physical cores, OMP_PROC_BIND=close, set in main() before any OpenMP
+    library loads): the dense int4 step of configs[1] (`value`), plus an
+    MXFP4 expert GEMV leg (configs[2] shapes) and an OLMoE-shaped MoE layer
+    leg (configs[0], the reference's kernels composed in the order of
+    c/olmoe.c:645-697). It runs in a child process of its own that never
+    loads the HIP runtime (main()), so the OpenMP runtime and the GPU runtime
+    (and a profiler's preloaded tool library) never share a process. Inputs are
+    the workload's shapes and distributions from numpy's generator: the CPU
+    time does not depend on the values."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_lib import REF_PATH, Ref, Cref
+    kind = "reference" if os.path.exists(REF_PATH) else "port"
+    lib = Ref() if kind == "reference" else Cref()
+    cref = Cref()
+    rng = np.random.default_rng(4242)
+    (qu, su), (qd, sd) = [(rng.integers(0, 256, (O, I // 2), dtype=np.uint8), fp16_scales(rng, O, I // 32))
+                          for O, I in (UP, DOWN)]
+    cpu_x = bf16_exact(rng.standard_normal((16, UP[1])).astype(np.float32))
+    h = np.empty((16, UP[0]), np.float32)
+
+    def timed(fn):
+        fn()                          # warm the page cache / thread pool
+        t0 = time.perf_counter()
+        work, reps = 0, 0
+        while time.perf_counter() - t0 < secs:
+            work += fn()
+            reps += 1
+        return work, reps, time.perf_counter() - t0
+
+    def dense_pass():
+        nbytes = 0
+        for B in BATCHES:
+            xb = np.ascontiguousarray(cpu_x[:B])
+            h[:B] = lib.matmul_i4_grouped(xb, qu, su, UP[0], UP[1], 32)
+            lib.matmul_i4_grouped(np.ascontiguousarray(h[:B]), qd, sd, DOWN[0], DOWN[1], 32)
+            nbytes += bytes_i4(*UP, B) + bytes_i4(*DOWN, B)
+        return nbytes
+
+    nbytes, reps, dt = timed(dense_pass)
+    out = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": CPU_INFO["threads"], "kind": kind,
+           "sample": f"{reps} passes of the bench step (up+down GEMV at batch 1/4/8/16) over one "
+                     f"weight copy, {dt:.1f} s, c/quant.h matmul_i4_grouped (OpenMP)",
+           "ms_per_step": round(dt / reps * 1e3, 2), "cpu": CPU_INFO}
+    # MXFP4 expert GEMV, DeepSeek-V3 expert shapes (gate/up 2048x7168, down 7168x2048), batch 1
+    mats = [(rng.integers(0, 256, (O, I // 2), dtype=np.uint8), rng.integers(119, 124, (O, I // 32), dtype=np.uint8),
+             O, I) for O, I in ((2048, 7168), (7168, 2048))]
+    x1 = {I: bf16_exact(rng.standard_normal((1, I)).astype(np.float32)) for I in (7168, 2048)}
+
+    def mx_pass():
+        nb = 0
+        for q4, e8, O, I in mats:
+            lib.matmul_mxfp4(x1[I], q4, e8, O, I)
+            nb += bytes_fp4(O, I, 1)
+        return nb
+
+    nb, reps, dt = timed(mx_pass)
+    out["mxfp4_gemv"] = {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "kind": kind,
+                         "sample": f"{reps} x (2048x7168 + 7168x2048) matmul_mxfp4 at batch 1, {dt:.1f} s"}
+    # OLMoE-shaped MoE layer (configs[0]): 64 int4 experts, top-8 softmax, batch 1
+    D, I, E, K = 2048, 1024, 64, 8
+    experts = []
+    for _ in range(E):
+        trip = []
+        for O, II in ((I, D), (I, D), (D, I)):
+            trip.append((rng.integers(0, 256, (O, II // 2), dtype=np.uint8), fp16_scales(rng, O, II // 32)))
+        experts.append(tuple(trip))
+    W = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+    xs = bf16_exact(rng.standard_normal((64, D)).astype(np.float32))
+    state = {"i": 0}
+
+    def moe_pass():
+        # the reference's kernels for the router GEMV and the experts
+        # (c/olmoe.c:645-697 order): softmax top-8, silu(gate) * up, down,
+        # weighted sum in slot order
+        r = state["i"] % 64
+        state["i"] += 1
+        x = xs[r:r + 1]
+        logits = lib.matmul_f32(x, W)
+        idx, w, keff = cref.route(logits, K, 0)
+        acc = np.zeros(D, np.float32)
+        for kk in range(keff[0]):
+            (gq, gs), (uq, us), (dq, dsc) = experts[idx[0, kk]]
+            g = lib.matmul_i4_grouped(x, gq, gs, I, D, 32)
+            u = lib.matmul_i4_grouped(x, uq, us, I, D, 32)
+            hid = cref.swiglu(g, u)
+            acc += w[0, kk] * lib.matmul_i4_grouped(hid, dq, dsc, D, I, 32)[0]
+        return 1
+
+    toks, reps, dt = timed(moe_pass)
+    out["moe_layer_olmoe_int4"] = {"value": round(toks / dt, 1), "unit": "tokens/s", "kind": kind,
+                                   "sample": f"{reps} single-token layers (router GEMV + top-8 + 8 experts on "
+                                             f"the reference's c/quant.h kernels), {dt:.1f} s"}
+    return out
+
+
+def cpu_baseline_child(secs):
+    """Runs cpu_baseline() in a child process started before this process
+    touches the GPU, and returns its JSON result."""
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-child", "--cpu-seconds", str(secs)],
+                       capture_output=True, text=True, env=dict(os.environ), timeout=secs * 6 + 120)
+    if r.returncode != 0:
+        raise RuntimeError(f"CPU baseline child failed ({r.returncode}): {r.stderr[-2000:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 class Bench:
     def __init__(self, args):
         from colibri_amd.backend import Session
@@ -211,109 +319,8 @@ class Bench:
         self.dense_result = dict(value=value, wall=wall, gpu_ms=gpu_ms, K=K, W=W, by_batch=by_batch, copies=copies,
                                  kern_gbs=kern_gbs, kern_avg_us=kern_ms / kern_n * 1e3,
                                  kern_avg_bytes=kern_bytes / kern_n, pair=pair)
-        # host copy of copy 0 for the CPU baseline
-        if not self.args.skip_cpu:
-            self.cpu_inputs = {}
-            for name, (O, I), sc, seed in (("up", UP, sc_up, 1), ("down", DOWN, sc_dn, 2)):
-                nb = O * I // 2
-                assert b.hip_fill_random_u8(0, stage, nb, seed)
-                q = np.empty(nb, np.uint8)
-                assert b.cuda_pipe_download(0, stage, q.ctypes.data_as(C.c_void_p), nb)
-                self.cpu_inputs[name] = (q.reshape(O, I // 2), sc)
-            self.cpu_x = x
         for t in ups + downs:
             b.cuda_tensor_free(t)
-
-    # -- CPU baseline: the reference's own kernels ------------------------------
-    def cpu_baseline(self):
-        """The reference's CPU path on this host (OpenMP over
-        the physical cores, OMP_PROC_BIND=close, set in main() before any OpenMP
-        library loads): the dense int4 step of configs[1] (`value`), plus an
-        MXFP4 expert GEMV leg (configs[2] shapes) and an OLMoE-shaped MoE layer
-        leg (configs[0], the oracle's restatement of the composition)."""
-        sys.path.insert(0, os.path.join(ROOT, "tests"))
-        from oracle_lib import REF_PATH, Ref, Cref
-        kind = "reference" if os.path.exists(REF_PATH) else "port"
-        lib = Ref() if kind == "reference" else Cref()
-        cref = Cref()
-        secs = self.args.cpu_seconds
-        (qu, su), (qd, sd) = self.cpu_inputs["up"], self.cpu_inputs["down"]
-        h = np.empty((16, UP[0]), np.float32)
-
-        def timed(fn):
-            fn()                          # warm the page cache / thread pool
-            t0 = time.perf_counter()
-            work, reps = 0, 0
-            while time.perf_counter() - t0 < secs:
-                work += fn()
-                reps += 1
-            return work, reps, time.perf_counter() - t0
-
-        def dense_pass():
-            nbytes = 0
-            for B in BATCHES:
-                xb = np.ascontiguousarray(self.cpu_x[:B])
-                h[:B] = lib.matmul_i4_grouped(xb, qu, su, UP[0], UP[1], 32)
-                lib.matmul_i4_grouped(np.ascontiguousarray(h[:B]), qd, sd, DOWN[0], DOWN[1], 32)
-                nbytes += bytes_i4(*UP, B) + bytes_i4(*DOWN, B)
-            return nbytes
-
-        nbytes, reps, dt = timed(dense_pass)
-        out = {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": CPU_INFO["threads"], "kind": kind,
-               "sample": f"{reps} passes of the bench step (up+down GEMV at batch 1/4/8/16) over one "
-                         f"weight copy, {dt:.1f} s, c/quant.h matmul_i4_grouped (OpenMP)",
-               "ms_per_step": round(dt / reps * 1e3, 2), "cpu": CPU_INFO}
-        # MXFP4 expert GEMV, DeepSeek-V3 expert shapes (gate/up 2048x7168, down 7168x2048), batch 1
-        rng = np.random.default_rng(77)
-        mats = [(rng.integers(0, 256, (O, I // 2), dtype=np.uint8), rng.integers(119, 124, (O, I // 32), dtype=np.uint8),
-                 O, I) for O, I in ((2048, 7168), (7168, 2048))]
-        x1 = {I: bf16_exact(rng.standard_normal((1, I)).astype(np.float32)) for I in (7168, 2048)}
-
-        def mx_pass():
-            nb = 0
-            for q4, e8, O, I in mats:
-                lib.matmul_mxfp4(x1[I], q4, e8, O, I)
-                nb += bytes_fp4(O, I, 1)
-            return nb
-
-        nb, reps, dt = timed(mx_pass)
-        out["mxfp4_gemv"] = {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "kind": kind,
-                             "sample": f"{reps} x (2048x7168 + 7168x2048) matmul_mxfp4 at batch 1, {dt:.1f} s"}
-        # OLMoE-shaped MoE layer (configs[0]): 64 int4 experts, top-8 softmax, batch 1
-        D, I, E, K = 2048, 1024, 64, 8
-        experts = []
-        for _ in range(E):
-            trip = []
-            for O, II in ((I, D), (I, D), (D, I)):
-                trip.append((rng.integers(0, 256, (O, II // 2), dtype=np.uint8), fp16_scales(rng, O, II // 32)))
-            experts.append(tuple(trip))
-        W = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
-        xs = bf16_exact(rng.standard_normal((64, D)).astype(np.float32))
-        state = {"i": 0}
-
-        def moe_pass():
-            # the reference's kernels for the router GEMV and the experts
-            # (c/olmoe.c:645-697 order): softmax top-8, silu(gate) * up, down,
-            # weighted sum in slot order
-            r = state["i"] % 64
-            state["i"] += 1
-            x = xs[r:r + 1]
-            logits = lib.matmul_f32(x, W)
-            idx, w, keff = cref.route(logits, K, 0)
-            acc = np.zeros(D, np.float32)
-            for kk in range(keff[0]):
-                (gq, gs), (uq, us), (dq, dsc) = experts[idx[0, kk]]
-                g = lib.matmul_i4_grouped(x, gq, gs, I, D, 32)
-                u = lib.matmul_i4_grouped(x, uq, us, I, D, 32)
-                hid = cref.swiglu(g, u)
-                acc += w[0, kk] * lib.matmul_i4_grouped(hid, dq, dsc, D, I, 32)[0]
-            return 1
-
-        toks, reps, dt = timed(moe_pass)
-        out["moe_layer_olmoe_int4"] = {"value": round(toks / dt, 1), "unit": "tokens/s", "kind": kind,
-                                       "sample": f"{reps} single-token layers (router GEMV + top-8 + 8 experts on "
-                                                 f"the reference's c/quant.h kernels), {dt:.1f} s"}
-        return out
 
     # -- fused MoE layer (configs[0] and configs[2]) ------------------------------
     def moe(self, name, fmt, D, I, E, K, mode, shared, batches, layers_for_anticache, bias, zipf=None,
@@ -553,15 +560,17 @@ def moe_layers(bench, only=None):
     if want("olmoe"):
         res["configs[0]_olmoe_int4"] = bench.moe("olmoe", 4, 2048, 1024, 64, 8, 0, False, (1,), 10, False)
     if want("dsv3"):
-        res["configs[2]_dsv3_mxfp4"] = bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 16), 1, True)
+        # two layers cycled (each with its own router and shared expert): every
+        # call streams weights the previous call did not touch
+        res["configs[2]_dsv3_mxfp4"] = bench.moe("dsv3", 7, 7168, 2048, 256, 8, 2, True, (1, 4, 8, 16), 2, True)
     # one verification step of 21 rows (16-node tree + 5-token
     # draft) on the configs[2] layer shape, union GEMM vs 21 per-token passes
     if want("verify"):
         ver = {}
         for fmt, tag in ((7, "mxfp4"), (4, "int4")):
-            r = bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True, steps=20)
-            r.update({k + "": v for k, v in bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 1, True,
-                                                          steps=5, per_token=True).items() if k.startswith("B")})
+            r = bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 2, True, steps=20)
+            r.update({k + "": v for k, v in bench.moe("dsv3", fmt, 7168, 2048, 256, 8, 2, True, (21,), 2, True,
+                                                          steps=6, per_token=True).items() if k.startswith("B")})
             ver[tag] = r
         res["configs[3]_verification_21rows"] = ver
     # the async issue/take split at decode, overlapped with host work
@@ -572,7 +581,7 @@ def moe_layers(bench, only=None):
     # router logits ~N(0,1) with a Zipf(1.1) selection bias
     if want("kimi"):
         res["configs[4]_kimi_prefill_512"] = {
-            tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+            tag: bench.moe("kimi", fmt, 7168, 2048, 384, 8, 2, False, (512,), 2, True, zipf=1.1, steps=6,
                            w_std=1.0 / math.sqrt(7168))
             for fmt, tag in ((7, "mxfp4"), (4, "int4"))}
     # the opt-in MXFP4 GEMM on the block-scaled MFMA (COLI_HIP_MX=1; not
@@ -582,7 +591,7 @@ def moe_layers(bench, only=None):
         os.environ["COLI_HIP_MX"] = "1"
         try:
             res.setdefault("configs[4]_kimi_prefill_512", {})["mxfp4_block_scaled_mfma_optin"] = bench.moe(
-                "kimi", 7, 7168, 2048, 384, 8, 2, False, (512,), 1, True, zipf=1.1, steps=5,
+                "kimi", 7, 7168, 2048, 384, 8, 2, False, (512,), 2, True, zipf=1.1, steps=6,
                 w_std=1.0 / math.sqrt(7168))
         finally:
             del os.environ["COLI_HIP_MX"]
@@ -637,11 +646,21 @@ def main():
     ap.add_argument("--copy-calib", action="store_true",
                     help="only copy 256 MiB device-to-device 4 times (the known-size reference that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
+    ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_child:   # the CPU baseline alone, no GPU runtime in this process
+        print(json.dumps(cpu_baseline(args.cpu_seconds)))
+        sys.stdout.flush()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the expert path has no collectives; "
                                    "run with --gpus 1 (see DESIGN.md for how it would shard)"}))
         sys.exit(2)
+    # the CPU baseline first, in a child process, before this process loads
+    # the GPU runtime (and so before any GPU work that host load could disturb)
+    cpu = None
+    if not args.skip_cpu and not args.skip_dense and not args.copy_calib:
+        cpu = cpu_baseline_child(args.cpu_seconds)
     bench = Bench(args)
     if args.copy_calib:
         nb = 256 << 20
@@ -659,7 +678,7 @@ def main():
             only = set(args.moe_only.split(","))
             if not only <= set(MOE_PARTS):
                 ap.error(f"--moe-only: parts are {','.join(MOE_PARTS)}")
-        print(json.dumps({"moe_layer": moe_layers(bench, only)}))
+        print(json.dumps({"moe_layer": moe_layers(bench, only)}), flush=True)
         bench.close()
         return
     bench.dense()
@@ -681,10 +700,11 @@ def main():
     }
     if not args.skip_moe:
         out["moe_layer"] = moe_layers(bench)
-    if not args.skip_cpu:
-        out["cpu_baseline"] = bench.cpu_baseline()
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
+    # the result line goes out (flushed) before the backend is torn down
+    print(json.dumps(out), flush=True)
     bench.close()
-    print(json.dumps(out))
 
 
 if __name__ == "__main__":

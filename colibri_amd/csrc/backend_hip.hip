@@ -6,6 +6,8 @@
 // (router, elementwise) and moe.hip (fused MoE layer).
 #include "coli_hip_internal.h"
 
+#include <atomic>
+
 #include "coli_backend_abi.h"
 #include "coli_hip_ext.h"
 #include "coli_hip_host.h"
@@ -67,11 +69,17 @@ int bind_ctx(DevCtx *ctx) {
     return hip_check(hipSetDevice(ctx->device), "select device");
 }
 
-// Host-forced fault injection (c/backend_cuda.cu:1340-1348).
-static long g_gpu_calls;
+// Test hook of the reference ABI (c/backend_cuda.cu:1340-1348): while
+// COLI_GPU_FAIL_AFTER=N is set, every compute entry point reports failure
+// once N compute calls have been made with it set (N = 0: all of them);
+// uploads and queries are not gated, and unsetting it restores normal
+// operation. The count of armed calls is shared by all threads.
+static std::atomic<long> g_armed_compute_calls{0};
 int fault_injected(void) {
-    const char *fa = std::getenv("COLI_GPU_FAIL_AFTER");
-    return fa && g_gpu_calls++ >= std::atol(fa);
+    const char *budget = std::getenv("COLI_GPU_FAIL_AFTER");
+    if (budget == nullptr) return 0;
+    const long allowed = std::strtol(budget, nullptr, 10);
+    return g_armed_compute_calls.fetch_add(1, std::memory_order_relaxed) >= allowed;
 }
 
 // Grow-only device buffer. Growing waits for the stream first, because queued

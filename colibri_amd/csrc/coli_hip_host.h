@@ -46,6 +46,11 @@ struct FragSet {
     DevBuf p8, s8;    // e4m3 pieces + e8m0 scales for the MXFP4 GEMM (coli_prep_fp8)
     int prow = 0;     // rows per piece plane
     int gen8 = 0;     // generation of the last piece prep (flag slot 8 + set)
+    // The set holds hi parts only and its lo buffer is stale (the fmt=2 int8
+    // rows of idot_dev): GEMVs over it read a flag that is always zero, so
+    // they never take lo parts, also when a captured launch is replayed
+    // after a later prep raised the set's own flag.
+    bool nolo = false;
     // The rows the set was last asked for (make_frags): the prep is deferred
     // until a kernel needs fragments (flush_frags); a GEMV that converts f32
     // activations itself reads px directly and never needs it.
@@ -97,6 +102,7 @@ int bind_ctx(DevCtx *ctx);
 int fault_injected(void);
 int reserve(DevCtx *ctx, DevBuf *b, size_t bytes, int zero);
 int reserve_pinned(DevCtx *ctx, PinBuf *b, size_t bytes);
+void forget_emitted(DevCtx *ctx, const void *dst, size_t bytes);
 void note_group(DevCtx *ctx, int count, int total, double h2d, double ker, double d2h);
 int upload_impl(ColiCudaTensor **tensor, const void *weights, const float *scales, const uint8_t *e8,
                 int fmt, int I, int O, int device, int gs, int w_on_device);

@@ -142,6 +142,7 @@ static int record_frags(FragSet &f, const float *x, int ld, int nrows, int K, in
                         const int *nrows_dev) {
     if (!x || nrows < 0 || K < 1 || ld < K) return 0;
     f.emitted = false;
+    f.nolo = false;
     f.pending = true;
     f.px = x;
     f.pld = ld;
@@ -313,6 +314,10 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.xexp = (const int *)f.exp.p;
     a.haslo = flag;
     a.lo_gen = f.gen;
+    if (f.nolo) {   // a zero word never reaches generation 1
+        a.haslo = (const int *)zero;
+        a.lo_gen = 1;
+    }
     a.zero = (const _Float16 *)zero;
     a.out = out;
     a.ldo = ldo;
@@ -692,6 +697,7 @@ extern "C" int coli_cuda_expert_group(ColiCudaTensor *const *gates, ColiCudaTens
 extern "C" int coli_cuda_expert_group_issue(ColiCudaTensor *const *gates, ColiCudaTensor *const *ups,
                                             ColiCudaTensor *const *downs, const int *rows, int count,
                                             const float *x) {
+    if (fault_injected()) return 0;
     if (!x) return 0;
     std::vector<Member> mem;
     int total, D, I;
@@ -757,10 +763,20 @@ static int gemm_prep(DevCtx *ctx, ColiCudaTensor *t, const float *x_dev, int S) 
     return make_frags(ctx, frag_set_of(t->kind, false), x_dev, t->I, S, t->I, t->kind != COLI_KIND_FP4);
 }
 
-// A write to y_dev by our own GEMV makes fragments emitted from it stale.
-static void invalidate_emitted(DevCtx *ctx, const float *y_dev) {
-    for (int s = 2; s < 4; s++)
-        if (ctx->frag[s].emitted && ctx->frag[s].esrc == y_dev) ctx->frag[s].emitted = false;
+// Fragments emitted from a device buffer describe what it held when they
+// were written: every entry point that writes device memory calls this for
+// the bytes it writes, and an emitted set overlapping them is dropped (its
+// next prep builds fragments from the buffer again). bytes == SIZE_MAX: the
+// extent is not known on the host, every emitted set of the device goes.
+void forget_emitted(DevCtx *ctx, const void *dst, size_t bytes) {
+    const uintptr_t a = (uintptr_t)dst;
+    const uintptr_t b = bytes == SIZE_MAX ? UINTPTR_MAX : a + bytes;
+    for (int s = 2; s < 4; s++) {
+        FragSet &f = ctx->frag[s];
+        if (!f.emitted) continue;
+        const uintptr_t ea = (uintptr_t)f.esrc, eb = ea + (size_t)f.erows * f.eK * sizeof(float);
+        if (bytes == SIZE_MAX || (a < eb && ea < b)) f.emitted = false;
+    }
 }
 
 // GEMV of t over the prepared fragments of S rows -> y_dev[S, O]; the
@@ -769,7 +785,7 @@ static void invalidate_emitted(DevCtx *ctx, const float *y_dev) {
 static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S, const ColiCudaTensor *next = nullptr) {
     const ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
     const int set = ctx->dense_set[t->kind == COLI_KIND_FP4 ? 1 : 0];
-    invalidate_emitted(ctx, y_dev);
+    forget_emitted(ctx, y_dev, (size_t)S * t->O * sizeof(float));
     if (!next) {
         return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O,
                         &p);
@@ -784,17 +800,21 @@ static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S, const C
                   0.0f, nullptr, &em))
         return 0;
     ctx->frag[em.set].emitted = em.done;
+    ctx->frag[em.set].nolo = false;
     return em.done ? 2 : 1;
 }
 
 // y_dev[S, O] = x_dev[S, I] W^T on the stream (tensor already resident).
 static int gemm_dev(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, const float *x_dev, int S) {
-    if (t->kind == COLI_KIND_GENERIC)
+    if (t->kind == COLI_KIND_GENERIC) {
+        forget_emitted(ctx, y_dev, (size_t)S * t->O * sizeof(float));
         return hip_check(coli_launch_generic_i4(t, x_dev, t->I, y_dev, t->O, S, ctx->stream), "generic gemv");
+    }
     return gemm_prep(ctx, t, x_dev, S) && gemm_run(ctx, t, y_dev, S);
 }
 
 extern "C" int coli_hip_gemm_prep_dev(ColiCudaTensor *t, const float *x_dev, int S) {
+    if (fault_injected()) return 0;
     if (!t || !x_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
     DevCtx *ctx = ctx_of(t->device);
     if (!bind_ctx(ctx)) return 0;
@@ -802,6 +822,7 @@ extern "C" int coli_hip_gemm_prep_dev(ColiCudaTensor *t, const float *x_dev, int
 }
 
 extern "C" int coli_hip_gemm_run_dev(ColiCudaTensor *t, float *y_dev, int S) {
+    if (fault_injected()) return 0;
     if (!t || !y_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
     DevCtx *ctx = ctx_of(t->device);
     if (!bind_ctx(ctx)) return 0;
@@ -818,6 +839,7 @@ extern "C" int coli_hip_gemm_run_dev(ColiCudaTensor *t, float *y_dev, int S) {
 // that prep's GEMV has run. Returns 2 when the fragments were emitted, 1 when
 // only the GEMV ran, 0 on failure.
 extern "C" int coli_hip_gemm_run_dev_emit(ColiCudaTensor *t, float *y_dev, int S, const ColiCudaTensor *next) {
+    if (fault_injected()) return 0;
     if (!t || !y_dev || S < 1 || t->kind == COLI_KIND_GENERIC || !tensor_computable(t)) return 0;
     if (!next || next->kind == COLI_KIND_GENERIC || next->I != t->O || next->device != t->device) return 0;
     DevCtx *ctx = ctx_of(t->device);
@@ -857,8 +879,10 @@ static int idot_dev(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, const float *x
         !reserve(ctx, &f.exp, (size_t)S * sizeof(int), 0) || !reserve(ctx, &ctx->idot_y, (size_t)S * t->O * 4, 0) ||
         !reserve(ctx, &ctx->idot_sx, (size_t)S * 4, 0))
         return 0;
-    // a fresh generation with no lo part: the set's flag holds an older one
+    // hi parts only: the GEMVs over this set never read its lo buffer
     f.pending = false;
+    f.nolo = true;
+    f.emitted = false;
     f.px = nullptr;
     f.psrc = nullptr;
     f.gen = f.gen == 0x7fffffff ? 1 : f.gen + 1;
@@ -872,6 +896,7 @@ static int idot_dev(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, const float *x
     if (!run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr,
                   (float *)ctx->idot_y.p, t->O, &p))
         return 0;
+    forget_emitted(ctx, y_dev, (size_t)S * t->O * sizeof(float));
     return hip_check(coli_launch_idot_scale(y_dev, (const float *)ctx->idot_y.p, (const float *)ctx->idot_sx.p, t->sc,
                                             half, t->nq, t->O, S, ctx->stream),
                      "int8 activation scales");
@@ -1042,6 +1067,7 @@ extern "C" int coli_hip_pipe_gemm_noalloc(ColiCudaTensor *t, float *y_dev, const
     }
     DevCtx *ctx = ctx_of(t->device);
     if (!bind_ctx(ctx) || !ctx->scratch) return 0;
+    forget_emitted(ctx, y_dev, (size_t)S * t->O * sizeof(float));
     if (t->kind == COLI_KIND_GENERIC)
         return hip_check(coli_launch_generic_i4(t, x_dev, t->I, y_dev, t->O, S, ctx->stream), "generic gemv");
     uint8_t *sc = ctx->scratch;
@@ -1072,6 +1098,7 @@ extern "C" int coli_cuda_expert_group_resident_issue(ColiCudaTensor *const *gate
                                                      ColiCudaTensor *const *downs, const float *weights,
                                                      int count, int home_device, const float *x_src_dev,
                                                      float *partial_slot_dev) {
+    if (fault_injected()) return 0;
     if (!weights || count < 1 || count > 64 || !x_src_dev || !partial_slot_dev) return 0;
     std::vector<int> rows(count, 1);
     std::vector<Member> mem;
@@ -1105,6 +1132,7 @@ extern "C" int coli_cuda_expert_group_resident_issue(ColiCudaTensor *const *gate
         if (!hip_check(e, "resident input")) return 0;
     }
     if (!run_expert_group(ctx, mem.data(), count, total, D, I, (float *)ctx->y.p, xr, false)) return 0;
+    if (DevCtx *home = ctx_of(home_device)) forget_emitted(home, partial_slot_dev, (size_t)D * sizeof(float));
     float *local = home_device == ctx->device ? partial_slot_dev : (float *)ctx->rslot.p;
     if (!hip_check(coli_launch_weighted_sum_rows(local, (const float *)ctx->y.p, (const float *)ctx->rw.p, count, D,
                                               ctx->stream),
@@ -1128,15 +1156,16 @@ extern "C" int coli_cuda_expert_group_resident_take(int home_device, const int *
         if (!src || !src->ev_ok) return 0;
         if (!hip_check(hipStreamWaitEvent(home->stream, src->ev_done, 0), "resident take wait")) return 0;
     }
+    forget_emitted(home, acc_dev, (size_t)D * sizeof(float));
     return hip_check(coli_launch_sum_slots(acc_dev, slots_dev, n_issued, D, home->stream), "resident take reduce");
 }
 
 // ---------------------------------------------------------------------------
-// Router logits. Up to 64 rows use the chunked partial kernel (pipe.hip, in
-// passes of 16 rows; rocBLAS's sgemm took 60 us for 21 rows of the DSV3
-// router); larger batches are a plain f32 GEMM, logits[S, E] = x W^T,
-// which rocBLAS runs on the backend stream (col-major: C(E x S) = W^T(E x D)
-// x^T... i.e. op(A) = A^T with A = W as a D x E col-major matrix).
+// Router logits as per-chunk partials (one partial per 512-column chunk of
+// D, summed in chunk order by the selection). Up to 64 rows: the GEMV-shaped
+// partial kernel coli_router_partial (pipe.hip, passes of 16 rows). Beyond:
+// coli_router_gemm (pipe.hip), 64 x 64 output tiles per 512-column chunk on
+// the f32 MFMA, writing the same chunk partials. No vendor library is used.
 // ---------------------------------------------------------------------------
 int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int E, float *part) {
     // up to 64 rows: the GEMV-shaped partial kernel (passes of 16 rows);
@@ -1152,6 +1181,7 @@ int router_logits(DevCtx *ctx, const float *x, int S, const float *W, int D, int
 extern "C" int coli_cuda_pipe_router(int device, const float *x_dev, const void *rw_dev, const void *rb_dev, int D,
                                      int E, int Ksel, float topp, int norm_topk, float routed_scale, int *idx_host,
                                      float *w_host, int *keff_host) {
+    if (fault_injected()) return 0;
     DevCtx *ctx = ctx_of(device);
     if (!x_dev || !rw_dev || !rb_dev || D < 1 || E < 1 || E > 1024 || Ksel < 1 || Ksel > 64 || !idx_host ||
         !w_host || !keff_host || !bind_ctx(ctx))
@@ -1209,6 +1239,7 @@ extern "C" void coli_cuda_pipe_free(int device, void *p) {
 extern "C" int coli_cuda_pipe_upload(int device, void *dst, const void *src, size_t bytes) {
     DevCtx *ctx = ctx_of(device);
     if (!bind_ctx(ctx)) return 0;
+    forget_emitted(ctx, dst, bytes);
     return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "pipe upload") &&
            hip_check(hipStreamSynchronize(ctx->stream), "pipe upload sync");
 }
@@ -1224,6 +1255,7 @@ extern "C" int coli_cuda_pipe_silu_mul(int device, float *gate_dev, const float 
     if (fault_injected()) return 0;
     DevCtx *ctx = ctx_of(device);
     if (!n || !gate_dev || !up_dev || !bind_ctx(ctx)) return 0;
+    forget_emitted(ctx, gate_dev, n * sizeof(float));
     return hip_check(coli_launch_silu_mul(gate_dev, up_dev, n, ctx->stream), "pipe silu mul");
 }
 
@@ -1231,6 +1263,7 @@ extern "C" int coli_cuda_pipe_add(int device, float *x_dev, const float *t_dev, 
     if (fault_injected()) return 0;
     DevCtx *ctx = ctx_of(device);
     if (!n || !x_dev || !t_dev || !bind_ctx(ctx)) return 0;
+    forget_emitted(ctx, x_dev, n * sizeof(float));
     return hip_check(coli_launch_add_n(x_dev, t_dev, n, ctx->stream), "pipe add");
 }
 
@@ -1239,6 +1272,7 @@ extern "C" int coli_cuda_pipe_rows_add(int device, float *x_dev, const float *pa
     if (fault_injected()) return 0;
     DevCtx *ctx = ctx_of(device);
     if (nrows < 1 || D < 1 || !x_dev || !partial_dev || !rows_dev || !bind_ctx(ctx)) return 0;
+    forget_emitted(ctx, x_dev, SIZE_MAX);   // the rows written are known on the device only
     return hip_check(coli_launch_rows_add(x_dev, partial_dev, rows_dev, nrows, D, ctx->stream), "pipe rows add");
 }
 
@@ -1246,6 +1280,7 @@ extern "C" int coli_cuda_pipe_copy2d(int device, float *dst, int dpitch, const f
                                      int height) {
     DevCtx *ctx = ctx_of(device);
     if (!bind_ctx(ctx)) return 0;
+    if (height > 0) forget_emitted(ctx, dst, ((size_t)(height - 1) * dpitch + width) * sizeof(float));
     return hip_check(hipMemcpy2DAsync(dst, (size_t)dpitch * 4, src, (size_t)spitch * 4, (size_t)width * 4, height,
                                    hipMemcpyDeviceToDevice, ctx->stream),
                   "pipe copy2d") &&
@@ -1254,6 +1289,7 @@ extern "C" int coli_cuda_pipe_copy2d(int device, float *dst, int dpitch, const f
 
 extern "C" int coli_cuda_pipe_peer_copy(int dst_dev, float *dst, int src_dev, const float *src, size_t bytes) {
     if (!dst || !src) return 0;
+    if (DevCtx *d = ctx_of(dst_dev)) forget_emitted(d, dst, bytes);
     if (dst_dev == src_dev) {
         DevCtx *c = ctx_of(dst_dev);
         if (!bind_ctx(c)) return 0;

@@ -1012,6 +1012,7 @@ extern "C" int coli_hip_moe_forward_dev(ColiHipMoe *m, const float *x_dev, float
         if (!hip_check(coli_launch_zero_i32(m->route_cnt, 1, ctx->stream), "routing counter reset")) return 0;
         m->route_cnt_dirty = false;
     }
+    forget_emitted(ctx, out_dev, (size_t)S * m->cfg.D * sizeof(float));
     const int ok = moe_forward_impl(m, ctx, x_dev, out_dev, S);
     if (!ok) m->route_cnt_dirty = true;
     return ok;
@@ -1125,6 +1126,7 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
 
 extern "C" int coli_hip_moe_forward(ColiHipMoe *m, const float *x, float *out, int S, int *idx, float *w,
                                     int *keff) {
+    if (fault_injected()) return 0;
     if (!m || !x || !out || S < 1 || S > COLI_MOE_MAX_ROWS) return 0;
     DevCtx *ctx = ctx_of(m->device);
     if (!bind_ctx(ctx)) return 0;

@@ -63,3 +63,18 @@ def test_no_cpu_fallback_in_product_path():
     assert "cref_" not in out and "ref_matmul" not in out
     ldd = subprocess.run(["ldd", backend.LIB_PATH], capture_output=True, text=True).stdout
     assert "cpu_ref" not in ldd and "coli_ref" not in ldd
+
+
+def test_every_called_symbol_has_a_ctypes_signature():
+    """ctypes defaults a missing restype to a 32-bit int, which would cut a
+    returned pointer (pipe_alloc, pipe_scratch, expert_group_take,
+    hip_stream) and let a later call dereference a truncated address. Every
+    declared entry point except the attention-side stubs (which the tests and
+    the benchmark never call) carries an explicit signature."""
+    from colibri_amd.backend import _SIGS, declared_symbols
+    stubs = {n for n in declared_symbols() if n.startswith("coli_cuda_attention_") or
+             n.startswith("coli_cuda_pipe_rmsnorm") or n.startswith("coli_cuda_pipe_rope")}
+    missing = [n for n in declared_symbols() if n not in _SIGS and n not in stubs]
+    assert not missing, missing
+    for name in ("coli_cuda_pipe_alloc", "coli_cuda_pipe_scratch", "coli_cuda_expert_group_take", "coli_hip_stream"):
+        assert _SIGS[name][1] is not None and _SIGS[name][1] is not int, name

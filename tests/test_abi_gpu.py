@@ -285,3 +285,122 @@ def test_expert_group_staging_routes(session, monkeypatch, kcopy, rows):
         mag = magnitude(hid, np.abs(deq_i4(*layer.experts[e][2], I, 32)))
         assert rel_err(y[off:off + n], ref, mag).max() <= TOL
         off += n
+
+
+SENTINEL = np.uint32(0x7FC0DEAD)   # a quiet-NaN bit pattern no kernel writes
+
+
+def _sentinel(shape):
+    return np.full(shape, SENTINEL, np.uint32).view(np.float32)
+
+
+def _untouched(a):
+    return bool(np.all(a.view(np.uint32) == SENTINEL))
+
+
+def test_fault_injection_contract(session, monkeypatch):
+    """The ABI's failure contract on a live device (c/backend_cuda.cu:1340-1348,
+    1384-1385; exercised by c/tests/test_backend_cuda.cu:313-318): with
+    COLI_GPU_FAIL_AFTER=0 every compute entry point returns 0 (take: NULL)
+    and leaves its output bitwise untouched; once the variable is unset the
+    next call of each matches the oracle again."""
+    rng = np.random.default_rng(1340)
+    b = session.b
+    D, I, S = 256, 128, 2
+    q4, sc = rand_i4(rng, I, D, 32)
+    x = rand_x(rng, S, D)
+    layer = Layer(rng, 4, D, I, 2)
+    hs = layer.upload(session)
+    h = session.upload(q4, sc, 4, D, I, 32)
+    g, _ga = tensor_array([t[0] for t in hs])
+    u, _ua = tensor_array([t[1] for t in hs])
+    d, _da = tensor_array([t[2] for t in hs])
+    rows = np.ones(2, np.int32)
+    E, K = 16, 4
+    W = (rng.standard_normal((E, D)) * 0.02).astype(np.float32)
+    bias = np.zeros(E, np.float32)
+    xd, wd, bd, yd = (b.cuda_pipe_alloc(0, n) for n in (S * D * 4, E * D * 4, E * 4, S * I * 4))
+    try:
+        for p, a in ((xd, x), (wd, W), (bd, bias)):
+            assert b.cuda_pipe_upload(0, p, a.ctypes.data_as(C.c_void_p), a.nbytes)
+
+        def calls():
+            """(name, run) pairs; run() returns (ok, outputs...)."""
+            def matmul():
+                y = _sentinel((S, I))
+                hh = C.c_void_p(h.value)
+                return b.cuda_matmul(C.byref(hh), f32p(y), f32p(x), None, None, 4, S, D, I, 0, 32), y
+
+            def group():
+                y = _sentinel((2, D))
+                return b.cuda_expert_group(g, u, d, i32p(rows), 2, f32p(y), f32p(x)), y
+
+            def issue():
+                ok = b.cuda_expert_group_issue(g, u, d, i32p(rows), 2, f32p(x))
+                yp = b.cuda_expert_group_take(0)
+                y = (np.ctypeslib.as_array(yp, shape=(2 * D,)).reshape(2, D).copy() if yp else _sentinel((2, D)))
+                return bool(ok) and bool(yp), y
+
+            def pipe_gemm():
+                y = _sentinel((S, I))
+                assert b.cuda_pipe_upload(0, yd, y.ctypes.data_as(C.c_void_p), y.nbytes)
+                ok = b.cuda_pipe_gemm(h, yd, xd, S)
+                assert b.cuda_pipe_sync(0)
+                assert b.cuda_pipe_download(0, yd, y.ctypes.data_as(C.c_void_p), y.nbytes)
+                return ok, y
+
+            def router():
+                idx, w, keff = (np.full(K, SENTINEL, np.uint32).view(np.int32), _sentinel(K),
+                                np.full(1, SENTINEL, np.uint32).view(np.int32))
+                ok = b.cuda_pipe_router(0, xd, wd, bd, D, E, K, 0.0, 1, 1.0, i32p(idx), f32p(w), i32p(keff))
+                return ok, idx.view(np.float32), w, keff.view(np.float32)
+
+            return [("matmul", matmul), ("expert_group", group), ("expert_group_issue", issue),
+                    ("pipe_gemm", pipe_gemm), ("pipe_router", router)]
+
+        monkeypatch.setenv("COLI_GPU_FAIL_AFTER", "0")
+        for name, run in calls():
+            ok, *outs = run()
+            assert not ok, f"{name} ran with COLI_GPU_FAIL_AFTER=0"
+            assert all(_untouched(o) for o in outs), f"{name} wrote its output on a refused call"
+        monkeypatch.delenv("COLI_GPU_FAIL_AFTER")
+        res = {name: run() for name, run in calls()}
+        assert all(r[0] for r in res.values()), {n: r[0] for n, r in res.items()}
+    finally:
+        for p in (xd, wd, bd, yd):
+            b.cuda_pipe_free(0, p)
+        session.free(h)
+        for t3 in hs:
+            for t in t3:
+                session.free(t)
+    ref = cref.matmul_i4_grouped(x, q4, sc, I, D, 32)
+    mag = magnitude(x, deq_i4(q4, sc, D, 32))
+    assert rel_err(res["matmul"][1], ref, mag).max() <= TOL
+    assert rel_err(res["pipe_gemm"][1], ref, mag).max() <= TOL
+    for name in ("expert_group", "expert_group_issue"):
+        y = res[name][1]
+        for e in range(2):
+            hid, yr = layer.expert_forward(e, x[e:e + 1])
+            m = magnitude(hid, np.abs(deq_i4(*layer.experts[e][2], I, 32)))
+            assert rel_err(y[e:e + 1], yr, m).max() <= TOL, name
+    _, idx, w, keff = res["pipe_router"]
+    ri, rw, rk = cref.route(cref.matmul_f32(x[:1], W), K, 1, bias=bias, norm_topk=1, routed_scale=1.0)
+    assert keff.view(np.int32)[0] == rk[0]
+    assert np.array_equal(idx.view(np.int32)[:rk[0]], ri[0, :rk[0]])
+    assert np.allclose(w[:rk[0]], rw[0, :rk[0]], rtol=1e-5, atol=0)
+
+
+def test_fmt4_without_group_size_refused(session):
+    """fmt=4 carries [O, ceil(I/gs)] scales, so a call without a group size is
+    refused on a live device with the output untouched
+    (c/backend_cuda.cu:1355-1359)."""
+    rng = np.random.default_rng(1355)
+    O, I, S = 64, 256, 2
+    q4, sc = rand_i4(rng, O, I, 32)
+    x = rand_x(rng, S, I)
+    y = _sentinel((S, O))
+    h = C.c_void_p()
+    assert not session.b.cuda_matmul(C.byref(h), f32p(y), f32p(x), q4.ctypes.data_as(C.c_void_p), f32p(sc),
+                                     4, S, I, O, 0, 0)
+    assert not h.value
+    assert _untouched(y)

@@ -215,3 +215,55 @@ def test_emission_declined(session, monkeypatch, H, S):
         ref, mag = m.ref(inp)
         e = rel_err(got, ref, mag)
         assert e.max() <= TOL, f"max rel err {e.max():.3e}"
+
+
+@pytest.mark.parametrize("writer", ["noalloc", "idot", "silu_mul", "upload", "pipe_gemm"])
+def test_emitted_fragments_dropped_by_other_writers(session, monkeypatch, writer):
+    """Every entry point that writes a device buffer drops fragments emitted
+    from it (the allocation-free GEMV, the fmt=2 int8-activation GEMV, the
+    pipe element-wise ops and uploads, pipe_gemm): after the up GEMV emitted
+    from hd and `writer` rewrote hd, the down projection is that of the new
+    contents of hd, against the oracle."""
+    monkeypatch.setenv("COLI_HIP_EMIT", "force")
+    b = session.b
+    rng = np.random.default_rng(11 + len(writer))
+    D, H, S = 1024, 2048, 8
+    up, down = Mat(session, rng, "i4h", H, D), Mat(session, rng, "i4h", D, H)
+    x = rng.standard_normal((S, D)).astype(np.float32)
+    other = (rng.standard_normal((S, D)) * 3).astype(np.float32)
+    xd, od = _dev(b, x), _dev(b, other)
+    hd, yd = b.cuda_pipe_alloc(0, S * H * 4), b.cuda_pipe_alloc(0, S * D * 4)
+    extra = []
+    try:
+        assert b.hip_gemm_prep_dev(up.h, xd, S) and b.hip_gemm_run_dev_emit(up.h, hd, S, down.h) == 2
+        if writer == "noalloc":
+            assert b.hip_pipe_gemm_noalloc(up.h, hd, od, S)
+        elif writer == "pipe_gemm":
+            assert b.cuda_pipe_gemm(up.h, hd, od, S)
+        elif writer == "idot":
+            q2, s2 = rand_i4(rng, H, D, 0)
+            h2 = session.upload(q2, s2, 2, D, H)
+            extra.append(h2)
+            assert b.hip_matmul_i4_idot_dev(h2, hd, od, S)
+        elif writer == "silu_mul":
+            ud = _dev(b, (rng.standard_normal((S, H)) * 2).astype(np.float32))
+            extra.append(("dev", ud))
+            assert b.cuda_pipe_silu_mul(0, hd, ud, S * H)
+        else:
+            new = rng.standard_normal((S, H)).astype(np.float32)
+            assert b.cuda_pipe_upload(0, hd, new.ctypes.data_as(C.c_void_p), new.nbytes)
+        assert b.hip_gemm_prep_dev(down.h, hd, S) and b.hip_gemm_run_dev(down.h, yd, S)
+        h, y = _get(b, hd, (S, H)), _get(b, yd, (S, D))
+    finally:
+        for p in (xd, od, hd, yd):
+            b.cuda_pipe_free(0, p)
+        for e in extra:
+            if isinstance(e, tuple):
+                b.cuda_pipe_free(0, e[1])
+            else:
+                session.free(e)
+        session.free(up.h)
+        session.free(down.h)
+    ref, mag = down.ref(h)
+    e = rel_err(y, ref, mag)
+    assert e.max() <= TOL, f"{writer}: max rel err {e.max():.3e}"

@@ -124,3 +124,43 @@ def test_moe_graph_replays_match_eager(session, D, E, I, K, S, olmoe):
         for p in (xd, x2d, od, o2d):
             b.cuda_pipe_free(0, p)
         free_handles(session, hs)
+
+
+def test_idot_graph_replay_ignores_later_lo_flag(session):
+    """The fmt=2 int8-activation GEMV builds hi parts only; a captured call
+    replayed after eager GEMVs on the same fragment set raised that set's lo
+    flag (full f32 inputs) still takes no lo parts: every replay is bitwise
+    the eager result."""
+    b = session.b
+    st = b.hip_stream(0)
+    rng = np.random.default_rng(933)
+    O, I, S = 512, 1024, 3
+    q2, s2 = rand_i4(rng, O, I, 0)
+    h2 = session.upload(q2, s2, 2, I, O)
+    q4, s4 = rand_i4(rng, O, I, 32)
+    h4 = session.upload(q4, s4, 4, I, O, 32)
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    xf = rng.standard_normal((S, I)).astype(np.float32) * 3   # lo parts non-zero
+    xd, xfd = _dev(b, x), _dev(b, xf)
+    yd, y2d = b.cuda_pipe_alloc(0, S * O * 4), b.cuda_pipe_alloc(0, S * O * 4)
+    try:
+        assert b.hip_matmul_i4_idot_dev(h2, yd, xd, S)
+        hiprt.device_sync()
+        eager = _get(b, yd, (S, O))
+        with hiprt.Graph(st) as g:
+            assert b.hip_matmul_i4_idot_dev(h2, yd, xd, S)
+        for rep in range(3):
+            # eager GEMVs of the same input kind with lo parts: the set's flag moves on
+            assert b.hip_gemm_prep_dev(h4, xfd, S) and b.hip_gemm_run_dev(h4, y2d, S)
+            assert b.cuda_pipe_gemm(h4, y2d, xfd, S)
+            hiprt.device_sync()
+            b.hip_fill_random_u8(0, yd, S * O * 4, 7 + rep)
+            g.launch()
+            hiprt.device_sync()
+            got = _get(b, yd, (S, O))
+            assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {rep}"
+    finally:
+        for p in (xd, xfd, yd, y2d):
+            b.cuda_pipe_free(0, p)
+        session.free(h2)
+        session.free(h4)

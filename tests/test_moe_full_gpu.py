@@ -80,8 +80,8 @@ def test_olmoe_layer_full_size(session, S):
 
 
 # DeepSeek-V3-shaped layer in MXFP4 (e8m0 exponents -8..-4), 256
-# routed experts + 1 shared, top-8 sigmoid-normalized; decode batch 1 and 16
-@pytest.mark.parametrize("S", [1, 16])
+# routed experts + 1 shared, top-8 sigmoid-normalized; decode batches 1-16
+@pytest.mark.parametrize("S", [1, 2, 4, 8, 16])
 def test_dsv3_layer_full_size(session, S):
     rng = np.random.default_rng(3000 + S)
     D, I, E, K = 7168, 2048, 256, 8

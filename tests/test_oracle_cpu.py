@@ -276,6 +276,47 @@ def test_router_vs_sort(mode):
     assert np.allclose(rw, sw, rtol=2e-6, atol=0)
 
 
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_router_exact_ties_lowest_index(mode):
+    """Exactly tied scores: the selection is K rounds of a strict '>' argmax,
+    so among equal scores the lowest expert index wins (c/backend_cuda.cu:2176-2178,
+    c/olmoe.c:667-673), i.e. the order of a stable descending sort. Logits
+    come from four exactly representable values, so equal logits give equal
+    f32 scores and the ties are exact; tied experts are spread over the whole
+    index range (different lane groups of the GPU selection)."""
+    rng = np.random.default_rng(2176 + mode)
+    S, E, K = 16, 64, 8
+    levels = np.array([-1.5, -0.5, 0.25, 1.0], np.float32)
+    logits = levels[rng.integers(0, 4, (S, E))]
+    # the top level held by a few experts spread from 0 to E-1, the next one by
+    # more than the K - (their count) slots left, so the K boundary cuts a tie
+    for s in range(S):
+        top = rng.choice(E, 3, replace=False)
+        logits[s] = np.where(logits[s] == levels[3], levels[2], logits[s])
+        logits[s, top] = levels[3]
+    bias = None
+    if mode != 0:
+        bias = np.zeros(E, np.float32)
+        bias[rng.choice(E, 6, replace=False)] = 0.125   # exact; ties within each (logit, bias) class remain
+    norm = 1 if mode != 2 else 0
+    ri, rw, rk = cref.route(logits, K, mode, bias=bias, norm_topk=norm, routed_scale=1.0)
+    si, sw = sort_route(logits, K, mode, bias, norm, 1.0)
+    assert np.all(rk == K)
+    assert np.array_equal(ri, si)
+    assert np.allclose(rw, sw, rtol=2e-6, atol=0)
+    # spelled out: every tied class inside the selection is taken in index order
+    for s in range(S):
+        sel = ri[s]
+        z = logits[s].astype(np.float64) + (bias.astype(np.float64) if bias is not None else 0.0)
+        for a in range(K - 1):
+            if z[sel[a]] == z[sel[a + 1]]:
+                assert sel[a] < sel[a + 1]
+        # the tie at the boundary: no unselected expert with the K-th score has a lower index
+        kth = z[sel[-1]]
+        rest = [e for e in range(E) if e not in set(sel.tolist())]
+        assert all(not (z[e] == kth and e < sel[-1]) for e in rest)
+
+
 def test_router_topp_keeps_smallest_prefix():
     """TOPP (c/backend_cuda.cu:2180-2193): weights sorted descending, keep the
     shortest prefix whose mass reaches topp of the total."""

@@ -60,6 +60,46 @@ def test_noalloc_matches_pipe_gemm(session, kind, O, I, S1, S2):
         session.free(h)
 
 
+def test_noalloc_allocates_nothing(session):
+    """Called first on shapes this context has not run (larger than anything
+    pipe_gemm sized its buffers for here), the entry point leaves the device's
+    free memory unchanged: its fragments, lo flag and split-K partials and
+    counters are all in the static scratch. A small pipe_gemm first loads the
+    library's code and creates the context's (small) buffers, so growing them
+    would show as an allocation."""
+    b = session.b
+    rng = np.random.default_rng(5)
+    qs, ss = rand_i4(rng, 32, 128, 32)
+    hs = session.upload(qs, ss, 4, 128, 32, 32)
+    run(session, b.cuda_pipe_gemm, hs, rand_x(rng, 1, 128), 32)
+    session.free(hs)
+    O, I, S = 2048, 16384, 16           # split-K shape at the row and K limits
+    q4, sc = rand_i4(rng, O, I, 32)
+    h = session.upload(q4, sc, 4, I, O, 32)
+    x = rng.standard_normal((S, I)).astype(np.float32)
+    px, py = b.cuda_pipe_alloc(0, x.nbytes), b.cuda_pipe_alloc(0, S * O * 4)
+    try:
+        assert b.cuda_pipe_upload(0, px, x.ctypes.data_as(C.c_void_p), x.nbytes)
+        assert b.cuda_pipe_sync(0)
+        free0, free1, total = C.c_size_t(), C.c_size_t(), C.c_size_t()
+        assert b.cuda_mem_info(0, C.byref(free0), C.byref(total))
+        for _ in range(2):
+            assert b.hip_pipe_gemm_noalloc(h, py, px, S)
+        assert b.cuda_pipe_sync(0)
+        assert b.cuda_mem_info(0, C.byref(free1), C.byref(total))
+        assert free1.value == free0.value, (free0.value, free1.value)
+        got = np.empty((S, O), np.float32)
+        assert b.cuda_pipe_download(0, py, got.ctypes.data_as(C.c_void_p), got.nbytes)
+    finally:
+        b.cuda_pipe_free(0, px)
+        b.cuda_pipe_free(0, py)
+    try:
+        ref = run(session, b.cuda_pipe_gemm, h, x, O)
+    finally:
+        session.free(h)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_noalloc_refuses_beyond_limits(session):
     rng = np.random.default_rng(3)
     O, I = 64, 256
