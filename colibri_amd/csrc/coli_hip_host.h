@@ -202,7 +202,7 @@ struct GemvEmit {
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
              const ColiProb *inline_prob = nullptr, float swiglu_limit = 0.0f, const GemvScratch *ws = nullptr,
-             GemvEmit *emit = nullptr);
+             GemvEmit *emit = nullptr, bool fold = false);
 // One grouped GEMM over a device work list of (problem << 16 | 64-row tile).
 int run_gemm(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev,
              const int *mt_list_dev, const int *n_mt_dev, int n_mt, int nrt, int nq, int O, int set,

@@ -82,6 +82,13 @@ struct ColiGemvArgs {
     float *out;
     int ldo;
     float swiglu_limit;       // > 0: DeepSeek-V4 clamped SwiGLU in the DUAL epilogue
+    // MXFP4 whose every e8m0 byte lies in [114, 140] (ColiCudaTensor::e8_fold):
+    // each e2m1 value times its block scale is an exact normal fp16, produced
+    // by the conversion itself, so the MFMAs accumulate across groups with no
+    // per-group scale arithmetic. Taken by coli_gemv_dma (not with per-group
+    // activation exponents, gexp); coli_gemv_tiles keeps the per-group form
+    // (its folded variant spilled more registers and measured slower).
+    int fold;
     float *partial;           // split-K partials: [instance][split][R][NB4][64]
     int *split_cnt;           // split-K arrival counters, one per instance; zero between launches
     // Fragments emitted by the GEMV that produced x (coli_hip_gemm_run_dev_emit):

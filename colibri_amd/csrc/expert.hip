@@ -228,7 +228,7 @@ static bool xstage_enabled() {
 // Launch one tiled GEMV over `nprob` problems whose descriptors are on the device.
 int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int nprob, const int *nprob_dev, int nrt,
              int nq, int O, int max_rows, int set, const int *xrows_dev, float *out, int ldo,
-             const ColiProb *inline_prob, float swiglu_limit, const GemvScratch *ws, GemvEmit *emit) {
+             const ColiProb *inline_prob, float swiglu_limit, const GemvScratch *ws, GemvEmit *emit, bool fold) {
     if (emit) emit->done = false;
     if (nprob <= 0) return 1;
     int n_bt = (max_rows + 15) / 16;
@@ -322,6 +322,7 @@ int run_gemv(DevCtx *ctx, int kind, bool dual, const ColiProb *probs_dev, int np
     a.out = out;
     a.ldo = ldo;
     a.swiglu_limit = swiglu_limit;
+    a.fold = fold && kind == COLI_KIND_FP4;
     a.partial = ws ? ws->partial : (float *)ctx->partial.p;
     a.split_cnt = ws ? ws->split_cnt : (int *)ctx->split_cnt.p;
     if (f.emitted && !ws) {
@@ -548,7 +549,7 @@ static int run_expert_group(DevCtx *ctx, const Member *m, int count, int total, 
             return run_gemm(ctx, L.kind, dual, pdev + L.first, L.n, nullptr, mtdev + mt_first[l], nullptr,
                             mt_count[l], L.nrt, L.nq, L.O, L.set, nullptr, L.out, L.ldo, 0.0f, fold);
         return run_gemv(ctx, L.kind, dual, pdev + L.first, L.n, nullptr, L.nrt, L.nq, L.O, max_rows, L.set,
-                        nullptr, L.out, L.ldo);
+                        nullptr, L.out, L.ldo, nullptr, 0.0f, nullptr, nullptr, fold);
     };
 
     // gate/up: dual launches and split members
@@ -785,19 +786,20 @@ void forget_emitted(DevCtx *ctx, const void *dst, size_t bytes) {
 static int gemm_run(DevCtx *ctx, ColiCudaTensor *t, float *y_dev, int S, const ColiCudaTensor *next = nullptr) {
     const ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
     const int set = ctx->dense_set[t->kind == COLI_KIND_FP4 ? 1 : 0];
+    const bool fold = t->kind == COLI_KIND_FP4 && t->e8_fold;
     forget_emitted(ctx, y_dev, (size_t)S * t->O * sizeof(float));
     if (!next) {
         return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O,
-                        &p);
+                        &p, 0.0f, nullptr, nullptr, fold);
     }
     GemvEmit em = {frag_set_of(next->kind, true), next->kind != COLI_KIND_FP4, false};
     // the set this launch reads (itself emitted) cannot be written by it: run
     // without emitting, next's prep builds its fragments as usual
     if (em.set == set)
         return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O,
-                        &p);
+                        &p, 0.0f, nullptr, nullptr, fold);
     if (!run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, set, nullptr, y_dev, t->O, &p,
-                  0.0f, nullptr, &em))
+                  0.0f, nullptr, &em, fold))
         return 0;
     ctx->frag[em.set].emitted = em.done;
     ctx->frag[em.set].nolo = false;
@@ -1088,7 +1090,7 @@ extern "C" int coli_hip_pipe_gemm_noalloc(ColiCudaTensor *t, float *y_dev, const
                             COLI_NA_CNT_BYTES / sizeof(int)};
     const ColiProb p = {t->w, t->sc, nullptr, nullptr, S, 0, 0, 0};
     return run_gemv(ctx, t->kind, false, nullptr, 1, nullptr, t->nrt, t->nq, t->O, S, frag_set_of(t->kind, false),
-                    nullptr, y_dev, t->O, &p, 0.0f, &ws);
+                    nullptr, y_dev, t->O, &p, 0.0f, &ws, nullptr, t->kind == COLI_KIND_FP4 && t->e8_fold);
 }
 
 // ---------------------------------------------------------------------------

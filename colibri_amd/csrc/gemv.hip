@@ -469,7 +469,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
     for (int k = 0; k < NI; k++) {
         E_out[k] = 0;
         const int ii = wave + k * W;
-        if (!gx && a.splits == 1 && ii < NB4) {
+        if (!gx && ii < NB4) {   // (with a K split only the last arriver uses it)
             const int brow = ks * 4 + ii;
             if (brow < nb) {
                 const int br = pr.xrow_off + 16 * bt + brow;
@@ -563,15 +563,24 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         if (!split_last || i >= NB4) return;
 #pragma unroll
         for (int r = 0; r < R; r++) v[r] = 0.0f;
-        for (int ss = 0; ss < a.splits; ss++)
+        // the partials of up to eight splits requested together (one memory
+        // round trip), then summed in split order
+        constexpr int SB = 8;
+        for (int s0 = 0; s0 < a.splits; s0 += SB) {
+            float pv[SB][R];
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                v[r] += __hip_atomic_load(a.partial + pbase + ((size_t)ss * R + r) * NB4 * 64, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        const int brow = ks * 4 + i;
-        if (!gx && brow < nb) {
-            const int br = pr.xrow_off + 16 * bt + brow;
-            E_out[0] = a.xexp[a.xrows ? a.xrows[br] : br];
+            for (int ss = 0; ss < SB; ss++)
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    pv[ss][r] = s0 + ss < a.splits
+                                    ? __hip_atomic_load(a.partial + pbase + ((size_t)(s0 + ss) * R + r) * NB4 * 64,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0.0f;
+#pragma unroll
+            for (int ss = 0; ss < SB; ss++)
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    if (s0 + ss < a.splits) v[r] += pv[ss][r];
         }
     }
     if (i >= NB4) return;

@@ -290,6 +290,7 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
     // with the group scale.
     extern __shared__ __attribute__((aligned(16))) uint8_t xs_lds[];
     constexpr bool gx = GX;
+    const bool fold = KIND == COLI_KIND_FP4 && !gx && a.fold;
     const int gxs = 4 * ((nb + 3) >> 2);
     auto compute = [&](int slot, auto lo_tag, int q) {
         constexpr bool LO = decltype(lo_tag)::value;
@@ -309,6 +310,19 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
         for (int r = 0; r < R; r++) {
             w[r] = LDS_RD(u32x4, src + r * COLI_TILE_BYTES + lane * 16);
             scale_from_lds<KIND>(sc[r], src + G::kScaleOff + r * ScaleGeom<KIND>::kBytes, lane & 15);
+        }
+        if constexpr (KIND == COLI_KIND_FP4 && !gx) {
+            if (fold) {   // exact fp16 e2m1 x scale: the MFMAs accumulate
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        const half8v bw = unpack_fp4_scaled(w[r][j], sc[r].get(j));
+                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, acc[r], 0, 0, 0);
+                        if constexpr (LO) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, acc[r], 0, 0, 0);
+                    }
+                return;
+            }
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -356,16 +370,29 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
         floatx4 t[R];
 #pragma unroll
         for (int r = 0; r < R; r++) t[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        if (KIND == COLI_KIND_FP4 && fold) {   // exact fp16 e2m1 x scale: the MFMAs accumulate
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < 4; j++) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const half8v bw = unpack_b<KIND>(w[r][j]);
-                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                if (lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
-                const float scl = sc[r].get(j);
+                for (int r = 0; r < R; r++) {
+                    const half8v bw = unpack_fp4_scaled(w[r][j], sc[r].get(j));
+                    t[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, t[r], 0, 0, 0);
+                    if (lo) t[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, t[r], 0, 0, 0);
+                }
+            }
+        } else {
 #pragma unroll
-                for (int i = 0; i < NB4; i++) t[r][i] = fmaf(d[i], scl, t[r][i]);
+            for (int j = 0; j < 4; j++) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const half8v bw = unpack_b<KIND>(w[r][j]);
+                    floatx4 d =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    if (lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
+                    const float scl = sc[r].get(j);
+#pragma unroll
+                    for (int i = 0; i < NB4; i++) t[r][i] = fmaf(d[i], scl, t[r][i]);
+                }
             }
         }
 #pragma unroll
@@ -395,16 +422,29 @@ __global__ __launch_bounds__(64 * W) void coli_gemv_dma(ColiGemvArgs a) {
         floatx4 t[R];
 #pragma unroll
         for (int r = 0; r < R; r++) t[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        if (KIND == COLI_KIND_FP4 && fold) {   // exact fp16 e2m1 x scale: the MFMAs accumulate
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < 4; j++) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const half8v bw = unpack_b<KIND>(w[r][j]);
-                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                if (lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
-                const float scl = sc[r].get(j);
+                for (int r = 0; r < R; r++) {
+                    const half8v bw = unpack_fp4_scaled(w[r][j], sc[r].get(j));
+                    t[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, t[r], 0, 0, 0);
+                    if (lo) t[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, t[r], 0, 0, 0);
+                }
+            }
+        } else {
 #pragma unroll
-                for (int i = 0; i < NB4; i++) t[r][i] = fmaf(d[i], scl, t[r][i]);
+            for (int j = 0; j < 4; j++) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const half8v bw = unpack_b<KIND>(w[r][j]);
+                    floatx4 d =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    if (lo) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[j], bw, d, 0, 0, 0);
+                    const float scl = sc[r].get(j);
+#pragma unroll
+                    for (int i = 0; i < NB4; i++) t[r][i] = fmaf(d[i], scl, t[r][i]);
+                }
             }
         }
         const int Eq = ((const int *)(xs_lds + a.nq * 512))[q];

@@ -1055,7 +1055,7 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     // 5. gate/up + SwiGLU over the union, 6. hidden fragments, 7. down
     // (MXFP4 scales folded into the operand when every matrix allows it;
     // re-checked per call, since tensor_update may change the scales)
-    bool fold = gemm && m->kind == COLI_KIND_FP4;
+    bool fold = m->kind == COLI_KIND_FP4;
     for (size_t i = 0; fold && i < m->mats.size(); i++) fold = m->mats[i]->e8_fold != 0;
     const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
     if (gemm) {
@@ -1065,15 +1065,14 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     } else if (S == 1 && dual1_enabled() && launch_dual1(m, st, x_dev, nrt_i, nq_d, P)) {
         if (!hip_check(hipGetLastError(), "moe gate/up")) return 0;
     } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I,
-                         nullptr, c.swiglu_limit)) {
+                         nullptr, c.swiglu_limit, nullptr, nullptr, fold)) {
         return 0;
     }
     // decode, one token: down projection and combine in one launch
     const int pmax = c.K + (c.has_shared ? 1 : 0);
     // (the matrix-core form at an intermediate size of 1024; at 2048 its
     // registers left no more occupancy and the f32 form measured faster)
-    bool fold_all = m->kind == COLI_KIND_FP4;
-    for (size_t i = 0; fold_all && i < m->mats.size(); i++) fold_all = m->mats[i]->e8_fold != 0;
+    const bool fold_all = fold;
     if (!gemm && S == 1 && pmax <= COLI_DC_WAVES && c.I == 1024 && down_combine_enabled() && dc_mfma_enabled()) {
         const dim3 grid((unsigned)nrt_d), block(64 * pmax);
         const size_t shm = (size_t)pmax * c.I * 4;
@@ -1115,7 +1114,8 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
         if (!run_gemm(ctx, m->kind, false, m->pdown, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_d, nq_i,
                       c.D, fh, nullptr, m->y, c.D, 0.0f, fold))
             return 0;
-    } else if (!run_gemv(ctx, m->kind, false, m->pdown, P, m->state, nrt_d, nq_i, c.D, S, fh, nullptr, m->y, c.D)) {
+    } else if (!run_gemv(ctx, m->kind, false, m->pdown, P, m->state, nrt_d, nq_i, c.D, S, fh, nullptr, m->y, c.D,
+                         nullptr, 0.0f, nullptr, nullptr, fold)) {
         return 0;
     }
     // 8. combine
