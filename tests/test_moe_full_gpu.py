@@ -154,10 +154,10 @@ def test_kimi_prefill_512_full_size(session, fmt):
 # configs[4] on the opt-in block-scaled MFMA (COLI_HIP_MX=1): the MXFP4 prefill
 # GEMM on v_mfma_scale_f32_16x16x128_f8f6f4 with e4m3 activation pieces. The
 # hardware sums each 128-column block of products with an error of about
-# 2^-15 of the block's magnitude sum, so the bound is 2e-4 of the magnitude sum
-# of the layer output (not the 1e-3 north-star metric, which it can miss on
-# outputs that cancel); the routing stays bit-exact. Prints the distribution
-# of the north-star metric.
+# 2^-15 of the block's magnitude sum: the output is bounded at 2e-4 of its
+# magnitude sum and held to the north-star metric (<= 1e-3, relative to
+# max(|ref|, 0.01 sum|t|)) on the sampled rows; the routing stays bit-exact.
+# Prints the distribution of the north-star metric.
 def test_kimi_prefill_512_block_scaled_mfma(session, monkeypatch):
     monkeypatch.setenv("COLI_HIP_MX", "1")
     rng = np.random.default_rng(5007)
@@ -184,3 +184,4 @@ def test_kimi_prefill_512_block_scaled_mfma(session, monkeypatch):
           f"p99 {np.quantile(ns, 0.99):.3g} max {ns.max():.3g} (> 1e-3: {np.mean(ns > 1e-3) * 100:.3f} %); "
           f"|err|/|ref| median {np.median(absref):.3g} p99 {np.quantile(absref, 0.99):.3g}")
     assert err_mag.max() <= 2e-4
+    assert ns.max() <= 1e-3, f"north-star metric {ns.max():.3g}"
