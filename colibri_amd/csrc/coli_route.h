@@ -187,9 +187,21 @@ __device__ __forceinline__ void router_partial_block(const float *__restrict__ x
         const int d = d0 + step * 256 + lane * 4;
         wv[step] = (e < E && d < D) ? *(const floatx4 *)(W + (size_t)e * D + d) : (floatx4){0.f, 0.f, 0.f, 0.f};
     }
-    for (int v = threadIdx.x; v < SMAX * NV; v += blockDim.x) {
+    // the rows' chunk (SMAX x NV float4) staged by the 256 threads: every load
+    // issued before any is waited for (one memory round trip)
+    constexpr int PER = (SMAX * NV + 255) / 256;
+    floatx4 xv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int v = threadIdx.x + 256 * u;
         const int s = v / NV, c = v - s * NV, d = d0 + c * 4;
-        xs[s][c] = (s < S && d < D) ? *(const floatx4 *)(x + (size_t)s * D + d) : (floatx4){0.f, 0.f, 0.f, 0.f};
+        xv[u] = (v < SMAX * NV && s < S && d < D) ? *(const floatx4 *)(x + (size_t)s * D + d)
+                                                  : (floatx4){0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int v = threadIdx.x + 256 * u;
+        if (v < SMAX * NV) xs[v / NV][v % NV] = xv[u];
     }
     __syncthreads();
     if (e >= E) return;
