@@ -105,6 +105,11 @@ static bool plan_dma(const DevCtx *ctx, GemvLaunchPlan &p, int kind, int nprob, 
     if (force < 0 || max_rows > 16 || nq < 1) return false;
     // above four rows the staged activation block outweighs the tiles it feeds
     if (force == 0 && max_rows > 4) return false;
+    // many problems of two to four rows (MoE unions): each problem's K is
+    // short against the eight waves of a group; the register-ring kernel's
+    // two-wave groups win (DSV3 MXFP4 layer B2 114.8 -> 100.8 us, B4 191.4 ->
+    // 162.5 us; int4 B4 215.3 -> 189.1 us)
+    if (force == 0 && nprob > 1 && max_rows > 1) return false;
     if (force == 0 && tiles < cus) return false;
     int RT = 1;
     if (tiles >= 2 * cus) RT = 2;

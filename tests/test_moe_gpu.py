@@ -261,6 +261,31 @@ def test_pipe_router_ties_and_invalid(session, case):
         assert list(idx[3:]) == list(range(3, K))
 
 
+@pytest.mark.parametrize("fmt", [4, 7])
+def test_expert_group_without_lo_parts(session, fmt):
+    """Members of two to four rows (the register-ring GEMV over device
+    descriptors) on activations whose fragments have no lo parts (multiples
+    of 2^-6 below 1: exact in fp16), right after a call whose activations
+    have them: the lo products of the second call add exactly zero."""
+    rng = np.random.default_rng(40 + fmt)
+    D, I = 384, 256
+    layer = Layer(rng, fmt, D, I, 3)
+    hs = layer.upload(session)
+    rows = [2, 4, 3]
+    x_lo = rng.standard_normal((sum(rows), D)).astype(np.float32)
+    x_nolo = (rng.integers(-64, 65, (sum(rows), D)) / 64.0).astype(np.float32)
+    args = ([h[0] for h in hs], [h[1] for h in hs], [h[2] for h in hs], rows)
+    try:
+        for x in (x_lo, x_nolo, x_lo):
+            y = session.expert_group(*args, x)
+            ref = group_reference(layer, x, [0, 1, 2], rows)
+            assert rel_err(y, ref, group_mag(layer, x, [0, 1, 2], rows)).max() <= TOL
+    finally:
+        for h in hs:
+            for t in h:
+                session.free(t)
+
+
 @pytest.mark.parametrize("fmt,lo,e8", [(4, False, None), (7, False, None), (4, True, None), (7, True, None),
                                         (7, False, (114, 140)), (7, True, (114, 140)), (7, False, (100, 150)),
                                         (7, True, (100, 150))])
