@@ -72,6 +72,17 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
             p.splits = sp;
         }
     }
+    // COLI_HIP_PLAN_PLAIN="R,W": the same for plain matrices on device
+    // descriptors only (tuning the MoE down projections apart from gate/up).
+    if (const char *ov = std::getenv("COLI_HIP_PLAN_PLAIN"); ov && !dual && nprob > 1) {
+        int r = 0, w = 0;
+        if (std::sscanf(ov, "%d,%d", &r, &w) == 2 && (r == 1 || r == 2 || r == 4) && (w == 2 || w == 4 || w == 8)) {
+            p.R = r;
+            p.W = w;
+            p.rbpp = (nrt + r - 1) / r;
+            p.splits = 1;
+        }
+    }
     p.qps = (nq + p.splits - 1) / p.splits;
     p.splits = (nq + p.qps - 1) / p.qps;
     p.dma = 0;

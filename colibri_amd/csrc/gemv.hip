@@ -376,13 +376,14 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
 // no check precedes the first weight loads, so the kernel arguments arrive
 // as one batch of scalar loads and the HBM requests follow at once (early
 // exits split the scalar loads into dependent round trips).
-// MXFP4 on device descriptors with two or four waves (the MoE layers of
-// 16-21 rows) is held to 168 VGPRs, three waves a SIMD instead of two at
-// 176: a few registers spill, and the layers still ran 4-7 % faster (DSV3
-// B16 460 -> 444 us, 21-row verification 603 -> 564 us, four waves); int4
-// spills more there and was slower (701 -> 750 us), so it keeps two.
+// The MXFP4 gate/up pairs on device descriptors with two or four waves (the
+// MoE layers of 2-21 rows) are held to 168 VGPRs, three waves a SIMD instead
+// of two at 176: a few registers spill, and the layers still ran faster (DSV3
+// B16 460 -> 444 us, 21-row verification 603 -> 564 us, four waves). The
+// plain (down) matrices keep two waves without spills (DSV3 B8 282 -> 274 us,
+// B16 454 -> 440 us against three); int4 spills more and keeps two.
 template <int KIND, int R, bool DUAL, int NB4, int W, bool INL>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W <= 4 && !INL ? 3 : 1, 8))) void coli_gemv_tiles(ColiGemvArgs a) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W <= 4 && !INL && DUAL ? 3 : 1, 8))) void coli_gemv_tiles(ColiGemvArgs a) {
     constexpr int RT = DUAL ? R / 2 : R;
     __shared__ float red[W][R * NB4][64];
     __shared__ int split_last;
