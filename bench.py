@@ -694,7 +694,7 @@ def main():
         "frac_of_peak": round(r["value"] / PEAK_GBS, 3),
         "roofline": {"bound": "hbm", "achieved": round(r["kern_gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["kern_gbs"] / PEAK_GBS, 3), "traffic": measured_traffic(),
-                     "kernel": "coli_gemv_dma (B1, B4) + coli_gemv_tiles (B8, B16); up launches emit h as the down GEMV fragments (B4-B16)", "avg_launch_us": round(r["kern_avg_us"], 2),
+                     "kernel": "coli_gemv_dma (B1, B4) + coli_gemv_tiles (B8, B16); up launches emit h as the down GEMV fragments", "avg_launch_us": round(r["kern_avg_us"], 2),
                      "avg_launch_bytes": int(r["kern_avg_bytes"])},
         "gemv_by_batch": r["by_batch"],
     }

@@ -62,13 +62,14 @@ def _chain(b, up, down, xd, hd, yd, S, emit):
     assert b.hip_gemm_run_dev(down.h, yd, S)
 
 
-# (4096, 12288) at 2 and 4 rows: the LDS-ring kernel produces (f32 rows, two
-# row tiles per wave) and consumes (prepared fragments); the others: the tiled
+# (4096, 12288) and (4096, 14336) at 1 row and (4096, 12288) at 2 and 4 rows:
+# the LDS-ring kernel produces (f32 rows, two row tiles per wave) and consumes; the others: the tiled
 # kernel on both sides, the down projection with K split across workgroups at
 # the benchmark's shape (configs[1]: 4, 8 and 16 rows).
 @pytest.mark.parametrize("kinds", [("i4h", "i4h"), ("i4f", "mx"), ("mx", "i4h"), ("mx", "mx")])
-@pytest.mark.parametrize("D,H,S", [(4096, 12288, 2), (4096, 12288, 4), (1024, 2048, 5), (1024, 2048, 8),
-                                   (512, 1024, 16), (4096, 14336, 4), (4096, 14336, 8), (4096, 14336, 16)])
+@pytest.mark.parametrize("D,H,S", [(4096, 12288, 1), (4096, 12288, 2), (4096, 12288, 4), (1024, 2048, 5),
+                                   (1024, 2048, 8), (512, 1024, 16), (4096, 14336, 1), (4096, 14336, 4),
+                                   (4096, 14336, 8), (4096, 14336, 16)])
 def test_emitted_fragments_chain(session, monkeypatch, kinds, D, H, S):
     monkeypatch.setenv("COLI_HIP_EMIT", "force")
     b = session.b
