@@ -315,8 +315,27 @@ class Bench:
                 "frac_of_peak": round((bu + bd) / (mu + md) / 1e6 / PEAK_GBS, 3),
             }
         kern_gbs = kern_bytes / kern_ms / 1e6
+        # The same bytes as one plain streaming read per launch (no
+        # arithmetic, no dependency), over as many fresh buffers: what one
+        # launch of this size can read at all on this part.
+        nb = bytes_i4(*UP, 0)
+        nb -= nb % 16
+        bufs = [self.alloc(nb) for _ in range(copies)]
+        for p in bufs:
+            assert b.hip_stream_read(0, p, nb)
+        with hrt.Graph(self.stream) as g3:
+            for p in bufs:
+                assert b.hip_stream_read(0, p, nb)
+        g3.launch()
+        hrt.device_sync()
+        a0, a1 = hrt.Event(), hrt.Event()
+        a0.record(self.stream)
+        g3.launch()
+        a1.record(self.stream)
+        read_floor_us = a0.elapsed_ms(a1) / copies * 1e3
         value = K * step_bytes / wall / 1e9
         self.dense_result = dict(value=value, wall=wall, gpu_ms=gpu_ms, K=K, W=W, by_batch=by_batch, copies=copies,
+                                 read_floor_us=read_floor_us, read_floor_bytes=nb,
                                  kern_gbs=kern_gbs, kern_avg_us=kern_ms / kern_n * 1e3,
                                  kern_avg_bytes=kern_bytes / kern_n, pair=pair)
         for t in ups + downs:
@@ -695,7 +714,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(r["kern_gbs"], 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["kern_gbs"] / PEAK_GBS, 3), "traffic": measured_traffic(),
                      "kernel": "coli_gemv_dma (B1, B4) + coli_gemv_tiles (B8, B16); up launches emit h as the down GEMV fragments", "avg_launch_us": round(r["kern_avg_us"], 2),
-                     "avg_launch_bytes": int(r["kern_avg_bytes"])},
+                     "avg_launch_bytes": int(r["kern_avg_bytes"]),
+                     # a plain streaming read of the same bytes, one launch each
+                     "read_floor_us": round(r["read_floor_us"], 2),
+                     "read_floor_frac": round(r["read_floor_bytes"] / r["read_floor_us"] / 1e3 / PEAK_GBS, 3)},
         "gemv_by_batch": r["by_batch"],
     }
     if not args.skip_moe:

@@ -108,6 +108,7 @@ _SIGS = {
     "coli_hip_stream": ([_i], _vp),
     "coli_hip_tensor_upload_from_device": ([_tpp, _vp, _f, _u8, _i, _i, _i, _i, _i], _i),
     "coli_hip_fill_random_u8": ([_i, _vp, _sz, C.c_ulonglong], _i),
+    "coli_hip_stream_read": ([_i, _vp, _sz], _i),
     "coli_hip_gemm_prep_dev": ([_tp, _vp, _i], _i),
     "coli_hip_pipe_gemm_noalloc": ([_tp, _vp, _vp, _i], _i),
     "coli_hip_gemm_run_dev": ([_tp, _vp, _i], _i),

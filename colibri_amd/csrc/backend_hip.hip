@@ -525,6 +525,12 @@ extern "C" int coli_hip_fill_random_u8(int device, void *dev, size_t n, unsigned
            hip_check(hipStreamSynchronize(ctx->stream), "random fill sync");
 }
 
+extern "C" int coli_hip_stream_read(int device, const void *dev, size_t bytes) {
+    DevCtx *ctx = ctx_of(device);
+    if (!dev || !bind_ctx(ctx)) return 0;
+    return hip_check(coli_launch_stream_read(dev, bytes, ctx->stream), "stream read");
+}
+
 extern "C" void *coli_hip_stream(int device) {
     DevCtx *ctx = ctx_of(device);
     return ctx ? (void *)ctx->stream : nullptr;

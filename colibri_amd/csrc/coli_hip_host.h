@@ -142,6 +142,7 @@ hipError_t coli_launch_router_select(const float *part, int nch, const float *bi
                                      int *keff, hipStream_t st);
 hipError_t coli_launch_zero_i32(int *p, int n, hipStream_t st);
 hipError_t coli_launch_fill_random(void *dev, size_t n, unsigned long long seed, hipStream_t st);
+hipError_t coli_launch_stream_read(const void *dev, size_t bytes, hipStream_t st);
 hipError_t coli_launch_silu_mul(float *gate, const float *up, size_t n, hipStream_t st);
 hipError_t coli_launch_silu_mul_to(float *h, const float *gate, const float *up, size_t n, hipStream_t st);
 hipError_t coli_launch_copy_f32(float *dst, const float *src, size_t n, hipStream_t st);

@@ -310,3 +310,30 @@ extern "C" hipError_t coli_launch_fill_random(void *dev, size_t n, unsigned long
     hipLaunchKernelGGL(coli_fill_random, dim3(4096), dim3(256), 0, st, (uint8_t *)dev, n, seed);
     return hipGetLastError();
 }
+
+// Plain streaming read of n16 16-byte words (benchmark reference: what one
+// launch of a given size can read, with no arithmetic and no dependency):
+// consecutive lanes read consecutive words, four independent loads per
+// thread in flight; the values only feed an opaque use, so nothing is written.
+__global__ __launch_bounds__(256) void coli_stream_read(const uint8_t *__restrict__ p, size_t n16) {
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nt = (size_t)gridDim.x * blockDim.x;
+    u32x4 acc = (u32x4){0u, 0u, 0u, 0u};
+    for (size_t i = tid; i < n16; i += 4 * nt) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const size_t w = i + u * nt;
+            v[u] = w < n16 ? __builtin_nontemporal_load(GPTR(u32x4, p) + w) : (u32x4){0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u];
+    }
+    asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]));
+}
+
+extern "C" hipError_t coli_launch_stream_read(const void *dev, size_t bytes, hipStream_t st) {
+    if (((uintptr_t)dev & 15) != 0 || bytes % 16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(coli_stream_read, dim3(2048), dim3(256), 0, st, (const uint8_t *)dev, bytes / 16);
+    return hipGetLastError();
+}

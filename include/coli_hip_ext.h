@@ -151,6 +151,10 @@ int coli_hip_gemm_run_dev_emit(ColiCudaTensor *tensor, float *y_dev, int S, cons
 /* Fill n bytes of device memory with uniform pseudo-random bytes (seeded,
  * deterministic): synthetic weights for benchmarks without a host round trip. */
 int coli_hip_fill_random_u8(int device, void *dev, size_t n, unsigned long long seed);
+/* Queue a plain streaming read of `bytes` (a multiple of 16, 16-byte aligned)
+ * of device memory on the device's stream: no arithmetic, nothing written.
+ * The benchmark's reference for what one launch of a given size can read. */
+int coli_hip_stream_read(int device, const void *dev, size_t bytes);
 /* The hipStream_t every asynchronous entry point of `device` runs on. */
 void *coli_hip_stream(int device);
 /* Bytes the tensor streams per full GEMV (weights + scales, tiled storage). */
