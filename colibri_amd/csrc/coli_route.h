@@ -238,13 +238,14 @@ __device__ __forceinline__ void router_partial_block(const float *__restrict__ x
 // ATOMIC: idx / wout / keff are written as agent-scope atomics (read back by
 // another workgroup of the same launch); LD_ATOMIC: the partials are read as
 // agent-scope atomics (written by other workgroups of the same launch). sidx / skeff (optional): copies of the
-// row's slots and keff for a reader in the same workgroup.
+// row's slots and keff for a reader in the same workgroup. gwrite false: idx / wout / keff are not written
+// (workgroups that select only for themselves).
 template <int JM, bool ATOMIC, bool LD_ATOMIC = ATOMIC>
 __device__ __forceinline__ void select_row(const float *__restrict__ part, int nch, const float *__restrict__ bias,
                                            int S, int E, int K, int mode, float topp, int norm_topk,
                                            float routed_scale, int *__restrict__ idx, float *__restrict__ wout,
                                            int *__restrict__ keff, float *p, int s, int lane, int *sidx,
-                                           int *skeff) {
+                                           int *skeff, bool gwrite = true) {
     auto ld = [](const float *q) {
         if constexpr (LD_ATOMIC) return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else return *q;
@@ -465,7 +466,7 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
         }
         if (routed_scale != 1.0f && slot < ke) my_w *= routed_scale;
     }
-    if (act) {
+    if (act && gwrite) {
         if constexpr (ATOMIC) {   // read back by another workgroup of the same launch
             __hip_atomic_store(idx + (size_t)s * K + slot, my_e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(wout + (size_t)s * K + slot, slot < ke ? my_w : 0.0f, __ATOMIC_RELAXED,
@@ -474,11 +475,13 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
             idx[(size_t)s * K + slot] = my_e;
             wout[(size_t)s * K + slot] = slot < ke ? my_w : 0.0f;
         }
-        if (sidx) sidx[s * K + slot] = my_e;
     }
+    if (act && sidx) sidx[s * K + slot] = my_e;
     if (lane == 0) {
-        if constexpr (ATOMIC) __hip_atomic_store(keff + s, ke, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else keff[s] = ke;
+        if (gwrite) {
+            if constexpr (ATOMIC) __hip_atomic_store(keff + s, ke, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else keff[s] = ke;
+        }
         if (skeff) skeff[s] = ke;
     }
 }

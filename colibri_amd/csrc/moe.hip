@@ -690,33 +690,31 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1m(co
 // coli_moe_down_combine1, then the waves' sums meet in LDS in fixed wave order
 // and wave 0 applies SwiGLU and writes the tile's 16 values of h.
 // ---------------------------------------------------------------------------
-template <int KIND, int W, int NQW>
-__global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restrict__ pdual,
-                                                         const int *__restrict__ state, const float *__restrict__ x,
-                                                         int D, int nrt, float *__restrict__ h, int I,
-                                                         float swiglu_limit) {
-    constexpr int NQ = W * NQW;   // the row's 128-column quads (D = NQ x 128)
-    __shared__ __attribute__((aligned(16))) float xs[NQ * 128];
-    __shared__ float red[W][2][16];
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
-    // the live count and the descriptor (in the array: p < the launch's
-    // problem count) in one round trip
-    const int np = state[0];
-    const ColiProb pd = pdual[p];
-    if (p >= np) return;
-    const ColiProb pr = uniform_prob(pd);
-    const int ks = lane >> 4, r16 = lane & 15;
-    const size_t t0 = (size_t)rt * NQ;
-    // x (issued first; each wave moves its NQW quads' 512 floats x ... into
-    // LDS through registers) and every weight quad of this wave's share
-    floatx4 xv[NQW / 2 + 1];
-    constexpr int XF4 = NQ * 32;   // float4s in the row
+// The token's row of x: each wave loads its share (quads w, w + W, ...) into
+// registers first, before anything else is requested.
+template <int W, int NQW>
+__device__ __forceinline__ void dual1_load_x(const float *__restrict__ x, floatx4 (&xv)[NQW / 2 + 1], int wave,
+                                             int lane) {
+    constexpr int XF4 = W * NQW * 32;   // float4s in the row
 #pragma unroll
     for (int k = 0; k < NQW / 2 + 1; k++) {
         const int i = (wave + W * k) * 64 + lane;
         xv[k] = i < XF4 ? *GPTR(floatx4, x + (size_t)i * 4) : (floatx4){0.f, 0.f, 0.f, 0.f};
     }
+}
+
+// Gate/up of row tile rt of problem pr for the row whose share each wave
+// holds in xv: every weight quad of the wave's share requested at once, x
+// moved into LDS (a bare barrier: the weight loads in flight are not
+// drained), f32 dots, the waves' sums in fixed order, SwiGLU by wave 0.
+template <int KIND, int W, int NQW>
+__device__ __forceinline__ void dual1_tile(const ColiProb &pr, int rt, const floatx4 (&xv)[NQW / 2 + 1],
+                                           float *__restrict__ xs, float (&red)[W][2][16], float *__restrict__ h,
+                                           int I, float swiglu_limit, int wave, int lane) {
+    constexpr int NQ = W * NQW;   // the row's 128-column quads (D = NQ x 128)
+    constexpr int XF4 = NQ * 32;
+    const int ks = lane >> 4, r16 = lane & 15;
+    const size_t t0 = (size_t)rt * NQ;
     u32x4 wg[NQW], wu[NQW];
     ScaleRegs<KIND> sg[NQW], su[NQW];
 #pragma unroll
@@ -732,8 +730,6 @@ __global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restr
         const int i = (wave + W * k) * 64 + lane;
         if (i < XF4) *(floatx4 *)(xs + (size_t)i * 4) = xv[k];
     }
-    // every wave's share of x is in LDS (a bare barrier: the weight loads in
-    // flight are not drained)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -768,6 +764,78 @@ __global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restr
         const int o = rt * 16 + lane;
         if (o < I) h[(size_t)pr.out_row0 * I + o] = swiglu_out(g, u, swiglu_limit);
     }
+}
+
+template <int KIND, int W, int NQW>
+__global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restrict__ pdual,
+                                                         const int *__restrict__ state, const float *__restrict__ x,
+                                                         int D, int nrt, float *__restrict__ h, int I,
+                                                         float swiglu_limit) {
+    __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
+    __shared__ float red[W][2][16];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
+    // the live count and the descriptor (in the array: p < the launch's
+    // problem count) in one round trip
+    const int np = state[0];
+    const ColiProb pd = pdual[p];
+    if (p >= np) return;
+    const ColiProb pr = uniform_prob(pd);
+    floatx4 xv[NQW / 2 + 1];
+    dual1_load_x<W, NQW>(x, xv, wave, lane);
+    dual1_tile<KIND, W, NQW>(pr, rt, xv, xs, red, h, I, swiglu_limit, wave, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Decode (one token), routing and gate/up in one launch after the router
+// partials (coli_router_partial): every workgroup of the gate/up grid selects
+// the token's experts itself (one wave, select_row on the partials: the same
+// code, inputs and order in every workgroup, so every workgroup finds the
+// same experts) and takes its problem's descriptor from the templates staged
+// in LDS meanwhile; problem p < keff is the expert of slot p (the union order
+// of one row), p == keff the shared expert. Workgroup 0 also writes the
+// selection and builds the union's descriptors and lists, as the separate
+// selection + union launch would, for the down projection + combine that
+// follows. No workgroup waits for another. Results are bitwise those of the
+// separate launches.
+// ---------------------------------------------------------------------------
+template <int KIND, int W, int NQW>
+__global__ __launch_bounds__(64 * W) void coli_moe_route_dual1(
+    const float *__restrict__ part, int nch, const float *__restrict__ bias, int E, int K, int mode, float topp,
+    int norm_topk, float routed_scale, int *__restrict__ idx, float *__restrict__ wsel, int *__restrict__ keff,
+    int has_shared, const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual, ColiProb *__restrict__ pdown,
+    int *__restrict__ uniq, int *__restrict__ xrows, int *__restrict__ slotrow, int *__restrict__ mt,
+    int *__restrict__ state, const float *__restrict__ x, int nrt, float *__restrict__ h, int I, float swiglu_limit) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
+    __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
+    __shared__ float red[W][2][16];
+    __shared__ int sidx[64], skeff[1];
+    // dynamic LDS: the selection's E floats, then the 2 (E + 1) descriptor templates
+    float *psel = (float *)dsm;
+    ColiProb *stab = (ColiProb *)(dsm + (((size_t)E * sizeof(float) + 15) & ~(size_t)15));
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
+    floatx4 xv[NQW / 2 + 1];
+    dual1_load_x<W, NQW>(x, xv, wave, lane);
+    for (int i = threadIdx.x; i < 2 * (E + 1); i += 64 * W) stab[i] = tab[i];
+    const bool first = blockIdx.x == 0;
+    if (wave == 0)
+        select_row<1, false, false>(part, nch, bias, 1, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
+                                    psel, 0, lane, sidx, skeff, first);
+    __syncthreads();
+    if (first && wave == 0)
+        moe_union_wave(sidx, skeff, 1, K, E, has_shared, stab, pdual, pdown, uniq, xrows, slotrow, mt, state, lane);
+    const int ke = skeff[0];
+    int e;
+    if (p < ke) e = sidx[p];
+    else if (p == ke && has_shared) e = E;
+    else return;
+    if (e < 0 || e >= E + 1) return;
+    ColiProb pr = uniform_prob(stab[2 * e]);
+    pr.nrows = 1;
+    pr.xrow_off = p;
+    pr.out_row0 = p;
+    dual1_tile<KIND, W, NQW>(pr, rt, xv, xs, red, h, I, swiglu_limit, wave, lane);
 }
 
 // out[t, d] = sum_{kk < keff[t]} w[t, kk] * y[slotrow[t, kk], d]  (+ y[shared row of t])
@@ -987,6 +1055,40 @@ static bool launch_dual1(ColiHipMoe *m, hipStream_t st, const float *x, int nrt,
     return false;
 }
 
+// COLI_HIP_ROUTE_DUAL1=0: at one token, the selection + union keep their own
+// launch before the gate/up (instead of running inside it).
+static bool route_dual1_enabled() {
+    const char *e = std::getenv("COLI_HIP_ROUTE_DUAL1");
+    return !(e && e[0] == '0');
+}
+
+// One token's selection, union and gate/up + SwiGLU in one launch after the
+// router partials (nch chunks in m->logits), for at most 64 experts (one per
+// lane of the selecting wave); false: not built for the shape. With more
+// experts every workgroup's selection costs more than the separate launch
+// (DSV3, 256 experts: layer 60.6-62.9 -> 65.1-65.8 us; OLMoE, 64: 22.0 ->
+// 18.9 us).
+static bool launch_route_dual1(ColiHipMoe *m, hipStream_t st, int nch, const float *x, int nrt, int nq, int P) {
+    const ColiHipMoeConfig &c = m->cfg;
+    if (c.K > 64 || c.E > 64 || !((c.D == 2048 && nq == 16) || (c.D == 7168 && nq == 56))) return false;
+    const size_t shm = (((size_t)c.E * sizeof(float) + 15) & ~(size_t)15) + (size_t)2 * (c.E + 1) * sizeof(ColiProb);
+    const dim3 grid((unsigned)(P * nrt));
+#define COLI_RD1(KD, W, NQW)                                                                                   \
+    hipLaunchKernelGGL((coli_moe_route_dual1<KD, W, NQW>), grid, dim3(64 * W), shm, st, m->logits, nch, m->rb, c.E, \
+                       c.K, c.route_mode, c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff,          \
+                       c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state, x, \
+                       nrt, m->h, c.I, c.swiglu_limit)
+#define COLI_RD1_KIND(W, NQW)                                      \
+    if (m->kind == COLI_KIND_I4_H) COLI_RD1(COLI_KIND_I4_H, W, NQW);      \
+    else if (m->kind == COLI_KIND_I4_F) COLI_RD1(COLI_KIND_I4_F, W, NQW); \
+    else COLI_RD1(COLI_KIND_FP4, W, NQW);                                 \
+    return true
+    if (c.D == 2048) { COLI_RD1_KIND(4, 4); }
+    COLI_RD1_KIND(8, 7);
+#undef COLI_RD1_KIND
+#undef COLI_RD1
+}
+
 // COLI_HIP_DOWNCOMBINE=0: at one token, the down projection and the combine
 // run as separate launches (the GEMV of any batch size, then the combine).
 static bool down_combine_enabled() {
@@ -1030,11 +1132,22 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     const bool gemm = S > COLI_GEMM_MIN_ROWS, mx = gemm && m->kind == COLI_KIND_FP4 && mx_gemm_enabled();
     // 1. activation fragments, 2-3. router
     if (!(mx ? make_frags8(ctx, fx, x_dev, c.D, S, c.D) : make_frags(ctx, fx, x_dev, c.D, S, c.D, int4))) return 0;
-    // One launch when few workgroups arrive: every arrival is an atomic on
-    // one counter, and hundreds of them serialize (measured: 896 arrivals
-    // cost more than the two launches they save).
-    if (S <= 16 && (long)((c.E + 3) / 4) * coli_router_chunks(c.D) <= 128 && !fused_route_disabled()) {
-        // 2-4. router, selection and union in one launch
+    const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
+    // One token, up to 64 experts: the router partials, then the selection and
+    // the union inside the gate/up launch (every workgroup selects for itself).
+    bool gateup_done = false;
+    if (S == 1 && !gemm && dual1_enabled() && route_dual1_enabled() && !fused_route_disabled() &&
+        c.K <= 64 && c.E <= 64 && ((c.D == 2048 && nq_d == 16) || (c.D == 7168 && nq_d == 56))) {
+        const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
+        if (!nch || !launch_route_dual1(m, st, nch, x_dev, nrt_i, nq_d, P) ||
+            !hip_check(hipGetLastError(), "moe routing + gate/up"))
+            return 0;
+        gateup_done = true;
+    } else if (S <= 16 && (long)((c.E + 3) / 4) * coli_router_chunks(c.D) <= 128 && !fused_route_disabled()) {
+        // 2-4. router, selection and union in one launch, when few workgroups
+        // arrive: every arrival is an atomic on one counter, and hundreds of
+        // them serialize (measured: 896 arrivals cost more than the two
+        // launches they save)
         if (!launch_route(m, x_dev, S, st)) return 0;
     } else if (S <= 64 && !fused_route_disabled()) {
         // 2. router partials, 3-4. selection and union in one launch
@@ -1057,8 +1170,8 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     // re-checked per call, since tensor_update may change the scales)
     bool fold = m->kind == COLI_KIND_FP4;
     for (size_t i = 0; fold && i < m->mats.size(); i++) fold = m->mats[i]->e8_fold != 0;
-    const int nrt_i = (c.I + 15) / 16, nrt_d = (c.D + 15) / 16;
-    if (gemm) {
+    if (gateup_done) {
+    } else if (gemm) {
         if (!run_gemm(ctx, m->kind, true, m->pdual, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_i, nq_d,
                       c.I, fx, m->xrows, m->h, c.I, c.swiglu_limit, fold))
             return 0;

@@ -128,6 +128,60 @@ def test_decode_down_combine_paths(session, monkeypatch, shape):
     assert max(e1, e2, e3, e4) <= TOL
 
 
+# One token, at most 64 experts: the selection and the union run inside the
+# gate/up launch (every workgroup selects for itself, workgroup 0 writes the
+# union) against their own launch before it (COLI_HIP_ROUTE_DUAL1=0):
+# outputs, indices, weights and keff bitwise equal, and against the oracle.
+# Softmax (OLMoE); sigmoid-normalized with the shared expert at the DSV3
+# hidden size (the 8-wave kernel) in MXFP4; sigmoid + bias with a TOPP cut
+# that keeps fewer than K experts (the shared expert's problem moves up).
+@pytest.mark.parametrize("shape", ["olmoe", "e64_d7168_shared", "e64_topp"])
+def test_one_token_routing_inside_gateup_bitwise(session, monkeypatch, shape):
+    rng = np.random.default_rng(4700 + len(shape))
+    if shape == "olmoe":
+        D, I, E, K, fmt, mode, shared = 2048, 1024, 64, 8, 4, 0, False
+    elif shape == "e64_d7168_shared":
+        D, I, E, K, fmt, mode, shared = 7168, 2048, 64, 8, 7, 2, True
+    else:
+        D, I, E, K, fmt, mode, shared = 2048, 1024, 64, 8, 4, 1, True
+    layer = Layer(rng, fmt, D, I, E, shared=shared, distinct=6)
+    x, W, b = make_router_inputs(rng, 1, D, E, K, mode, bias=(mode != 0))
+    hs = layer.upload(session)
+    routed, sh = hs[:E], (hs[E] if shared else (None, None, None))
+    g, _ga = tensor_array([h[0] for h in routed])
+    u, _ua = tensor_array([h[1] for h in routed])
+    d, _da = tensor_array([h[2] for h in routed])
+    topp = 0.0
+    if shape == "e64_topp":   # a cut the oracle says keeps fewer than K experts
+        for cand in (0.6, 0.5, 0.4, 0.3, 0.2):
+            if cref.route(cref.matmul_f32(x, W), K, mode, bias=b, norm_topk=1, topp=cand)[2][0] < K:
+                topp = cand
+                break
+        assert topp > 0.0
+    cfg = ColiHipMoeConfig(D, I, E, K, mode, 1 if mode == 1 else 0, topp, 1.0, 1 if shared else 0, 0.0)
+    m = C.c_void_p()
+    assert session.b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(np.ascontiguousarray(W)),
+                                    f32p(np.ascontiguousarray(b)) if b is not None else None, g, u, d,
+                                    sh[0], sh[1], sh[2])
+    try:
+        res = []
+        for env in ("1", "0", "1"):
+            monkeypatch.setenv("COLI_HIP_ROUTE_DUAL1", env)
+            res.append(forward(session, m, x, K))
+    finally:
+        session.b.hip_moe_free(m)
+        free_handles(session, hs)
+    for a, c in ((res[0], res[1]), (res[0], res[2])):
+        for ta, tc in zip(a, c):
+            assert np.array_equal(ta.view(np.uint32) if ta.dtype == np.float32 else ta,
+                                  tc.view(np.uint32) if tc.dtype == np.float32 else tc)
+    out, idx, w, keff = res[0]
+    ri, rw, rk = cref.route(cref.matmul_f32(x, W), K, mode, bias=b, norm_topk=1 if mode == 1 else 0, topp=topp)
+    assert np.array_equal(keff, rk) and np.array_equal(idx[:, :rk[0]], ri[:, :rk[0]])
+    _, _, _, ref, mag = moe_reference(layer, x, W, b, K, mode, norm_topk=1 if mode == 1 else 0, topp=topp)
+    assert rel_err(out, ref, mag).max() <= TOL
+
+
 # one verification step (16-node draft tree + 5-token linear
 # draft = 21 rows) on the configs[2] layer, MXFP4 and int4
 @pytest.mark.parametrize("fmt", [7, 4])
