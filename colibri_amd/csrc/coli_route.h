@@ -234,6 +234,89 @@ __device__ __forceinline__ void router_partial_block(const float *__restrict__ x
     }
 }
 
+// The end of one row's selection, once lane kk < want holds the expert of
+// rank kk (my_e) and its weight source (my_w, = p[my_e]): the slots past
+// want (fewer valid scores than K) take experts 0, 1, ...; the mode's
+// normalization, TOPP cut and scale; then the row's slots, weights and keff
+// are written (see select_row).
+template <bool ATOMIC>
+__device__ __forceinline__ void select_finish(int my_e, float my_w, int want, int E, int K, int mode, float topp,
+                                              int norm_topk, float routed_scale, const float *p,
+                                              int *__restrict__ idx, float *__restrict__ wout,
+                                              int *__restrict__ keff, int s, int lane, int *sidx, int *skeff,
+                                              bool gwrite) {
+    const bool act = lane < K;
+    if (act && lane >= want) {   // fewer valid scores than K: experts 0, 1, ... fill the rest
+        my_e = lane < E ? lane : 0;
+        my_w = p[my_e];
+    }
+    if (!act) my_w = 0.0f;
+    auto wsum = [](float v) { return wave_sum(v); };
+    // rank of this slot when sorted by weight, descending and stable (ties
+    // keep slot order), and the inclusive cumulative weight in that order
+    auto sort_rank = [&](int &rank, float &cum) {
+        rank = 0;
+        cum = 0.0f;
+        for (int j = 0; j < K; j++) {
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
+            const bool before = wj > my_w || (wj == my_w && j < lane);
+            rank += before ? 1 : 0;
+            cum += (before || j == lane) ? wj : 0.0f;
+        }
+    };
+    int slot = lane, ke = K;
+    const bool cut = topp > 0.0f && topp < 1.0f;
+    if (mode == 0) {
+        if (norm_topk) my_w /= wsum(my_w);
+    } else if (mode == 1) {
+        if (cut) {
+            float cum;
+            sort_rank(slot, cum);
+            const float tot = 1e-20f + wsum(my_w);
+            const int first = wave_min_i(act && cum >= topp * tot ? slot : K - 1);
+            ke = first + 1;
+        }
+        if (norm_topk) my_w /= wsum(act && slot < ke ? my_w : 0.0f) + 1e-20f;
+        if (slot < ke) my_w *= routed_scale;
+    } else if (mode == 3) {
+        // score / sum of the selected scores * route scale; a non-positive sum
+        // (an error in coli_v4_route) selects nothing
+        const float total = wsum(my_w);
+        if (!(total > 0.0f)) ke = 0;
+        else my_w = my_w / total * routed_scale;
+    } else {
+        my_w /= wsum(my_w) + 1e-20f;
+        if (cut) {
+            float cum;
+            sort_rank(slot, cum);
+            const int keep = wave_min_i(act && cum >= topp ? slot + 1 : K);
+            if (keep < K) {
+                my_w /= wsum(act && slot < keep ? my_w : 0.0f) + 1e-20f;
+                ke = keep;
+            }
+        }
+        if (routed_scale != 1.0f && slot < ke) my_w *= routed_scale;
+    }
+    if (act && gwrite) {
+        if constexpr (ATOMIC) {   // read back by another workgroup of the same launch
+            __hip_atomic_store(idx + (size_t)s * K + slot, my_e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(wout + (size_t)s * K + slot, slot < ke ? my_w : 0.0f, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            idx[(size_t)s * K + slot] = my_e;
+            wout[(size_t)s * K + slot] = slot < ke ? my_w : 0.0f;
+        }
+    }
+    if (act && sidx) sidx[s * K + slot] = my_e;
+    if (lane == 0) {
+        if (gwrite) {
+            if constexpr (ATOMIC) __hip_atomic_store(keff + s, ke, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else keff[s] = ke;
+        }
+        if (skeff) skeff[s] = ke;
+    }
+}
+
 // Selection of token row s by one wave; p: [E] floats of LDS for this wave.
 // ATOMIC: idx / wout / keff are written as agent-scope atomics (read back by
 // another workgroup of the same launch); LD_ATOMIC: the partials are read as
@@ -414,75 +497,103 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // p[] written by all lanes
-    const bool act = lane < K;
-    if (act && lane >= want) {   // fewer valid scores than K: experts 0, 1, ... fill the rest
-        my_e = lane < E ? lane : 0;
-        my_w = p[my_e];
-    }
-    if (!act) my_w = 0.0f;
-    auto wsum = [](float v) { return wave_sum(v); };
-    // rank of this slot when sorted by weight, descending and stable (ties
-    // keep slot order), and the inclusive cumulative weight in that order
-    auto sort_rank = [&](int &rank, float &cum) {
-        rank = 0;
-        cum = 0.0f;
-        for (int j = 0; j < K; j++) {
-            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), j));
-            const bool before = wj > my_w || (wj == my_w && j < lane);
-            rank += before ? 1 : 0;
-            cum += (before || j == lane) ? wj : 0.0f;
-        }
-    };
-    int slot = lane, ke = K;
-    const bool cut = topp > 0.0f && topp < 1.0f;
-    if (mode == 0) {
-        if (norm_topk) my_w /= wsum(my_w);
-    } else if (mode == 1) {
-        if (cut) {
-            float cum;
-            sort_rank(slot, cum);
-            const float tot = 1e-20f + wsum(my_w);
-            const int first = wave_min_i(act && cum >= topp * tot ? slot : K - 1);
-            ke = first + 1;
-        }
-        if (norm_topk) my_w /= wsum(act && slot < ke ? my_w : 0.0f) + 1e-20f;
-        if (slot < ke) my_w *= routed_scale;
-    } else if (mode == 3) {
-        // score / sum of the selected scores * route scale; a non-positive sum
-        // (an error in coli_v4_route) selects nothing
-        const float total = wsum(my_w);
-        if (!(total > 0.0f)) ke = 0;
-        else my_w = my_w / total * routed_scale;
-    } else {
-        my_w /= wsum(my_w) + 1e-20f;
-        if (cut) {
-            float cum;
-            sort_rank(slot, cum);
-            const int keep = wave_min_i(act && cum >= topp ? slot + 1 : K);
-            if (keep < K) {
-                my_w /= wsum(act && slot < keep ? my_w : 0.0f) + 1e-20f;
-                ke = keep;
+    select_finish<ATOMIC>(my_e, my_w, want, E, K, mode, topp, norm_topk, routed_scale, p, idx, wout, keff, s, lane,
+                          sidx, skeff, gwrite);
+}
+
+// Selection of one token row (S = 1) by the first NW waves of a workgroup,
+// for the sigmoid-family modes 1-3 and E <= 64 NW: wave w scores experts
+// 64 w + lane (chunk partials summed in chunk order, as select_row) and ranks
+// them among its 64 by comparison; each wave's top K meet in LDS, and wave 0
+// ranks those to the row's top K. The order is select_row's (score key
+// descending, then expert index ascending), and so are the results: an expert
+// among the row's top K is among its own wave's top K. Every wave of the
+// workgroup calls it (one barrier); wave 0 returns with the row's slots and
+// keff in sidx / skeff and, with gwrite, idx / wout / keff written (ATOMIC:
+// as agent-scope atomics).
+// LDS: p [E] floats (scores), stage [NW][64] and cand [NW][64] keys, nval
+// [NW], selb [64] keys.
+template <int NW, bool ATOMIC>
+__device__ __forceinline__ void select_row_waves(const float *__restrict__ part, int nch,
+                                                 const float *__restrict__ bias, int E, int K, int mode, float topp,
+                                                 int norm_topk, float routed_scale, int *__restrict__ idx,
+                                                 float *__restrict__ wout, int *__restrict__ keff, float *p,
+                                                 unsigned long long (*stage)[64], unsigned long long (*cand)[64],
+                                                 int *nval, unsigned long long *selb, int *sidx, int *skeff,
+                                                 bool gwrite, int wave, int lane) {
+    if (wave < NW) {
+        constexpr int CH = COLI_SEL_MAXCH;
+        const int e = 64 * wave + lane;
+        const bool live = e < E;
+        const int ee = live ? e : E - 1;
+        float t[CH];
+#pragma unroll
+        for (int ch = 0; ch < CH; ch++) t[ch] = part[(size_t)min(ch, nch - 1) * E + ee];
+        const float bs = bias ? bias[ee] : 0.0f;
+        float z = t[0];
+#pragma unroll
+        for (int ch = 1; ch < CH; ch++) z += ch < nch ? t[ch] : 0.0f;
+        for (int ch = CH; ch < nch; ch++) z += part[(size_t)ch * E + ee];
+        const float v = mode == 3 ? sqrtf(fmaxf(z, 0.0f) + log1pf(expf(-fabsf(z)))) : 1.0f / (1.0f + expf(-z));
+        if (live) p[e] = v;
+        unsigned k = 0;
+        if (live) {
+            float c = v + bs;
+            if (valid_score(c)) {
+                if (c == 0.0f) c = 0.0f;
+                const unsigned b = __float_as_uint(c);
+                k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
             }
         }
-        if (routed_scale != 1.0f && slot < ke) my_w *= routed_scale;
-    }
-    if (act && gwrite) {
-        if constexpr (ATOMIC) {   // read back by another workgroup of the same launch
-            __hip_atomic_store(idx + (size_t)s * K + slot, my_e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(wout + (size_t)s * K + slot, slot < ke ? my_w : 0.0f, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            idx[(size_t)s * K + slot] = my_e;
-            wout[(size_t)s * K + slot] = slot < ke ? my_w : 0.0f;
+        const int nv = wave_sum_i(k != 0);
+        const unsigned long long c = k ? ((unsigned long long)k << 32) | (0xFFFFFFFFu - (unsigned)e) : 0ull;
+        stage[wave][lane] = c;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        unsigned long long vv[64];
+#pragma unroll
+        for (int i = 0; i < 64; i += 2) {
+            const ulonglong2 t2 = *(const ulonglong2 *)(stage[wave] + i);
+            vv[i] = t2.x;
+            vv[i + 1] = t2.y;
         }
+        int r = 0;
+#pragma unroll
+        for (int i = 0; i < 64; i++) r += vv[i] > c;
+        if (c != 0ull && r < K) cand[wave][r] = c;
+        if (lane == 0) nval[wave] = nv;
     }
-    if (act && sidx) sidx[s * K + slot] = my_e;
-    if (lane == 0) {
-        if (gwrite) {
-            if constexpr (ATOMIC) __hip_atomic_store(keff + s, ke, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else keff[s] = ke;
-        }
-        if (skeff) skeff[s] = ke;
+    __syncthreads();
+    if (wave != 0) return;
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) total += nval[w];
+    const int want = total < K ? total : K;
+    // candidate lane l: rank l % K of wave l / K (NW K <= 64)
+    const int w = lane / K, r0 = lane - w * K;
+    const unsigned long long c = (w < NW && r0 < min(K, nval[w < NW ? w : 0])) ? cand[w][r0] : 0ull;
+    stage[0][lane] = c;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    unsigned long long vv[64];
+#pragma unroll
+    for (int i = 0; i < 64; i += 2) {
+        const ulonglong2 t2 = *(const ulonglong2 *)(stage[0] + i);
+        vv[i] = t2.x;
+        vv[i + 1] = t2.y;
     }
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < 64; i++) r += vv[i] > c;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (c != 0ull && r < K) selb[r] = c;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int my_e = 0;
+    float my_w = 0.0f;
+    if (lane < want) {
+        my_e = (int)(0xFFFFFFFFu - (unsigned)(selb[lane] & 0xFFFFFFFFull));
+        my_w = p[my_e];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    select_finish<ATOMIC>(my_e, my_w, want, E, K, mode, topp, norm_topk, routed_scale, p, idx, wout, keff, 0, lane,
+                          sidx, skeff, gwrite);
 }
 

@@ -374,8 +374,11 @@ def test_moe_layer_deepseek_v4(session, fmt, S, shared, limit):
 # Decode routing in one launch (router partials, selection and union; the
 # last workgroup to arrive selects) against the three separate launches:
 # bitwise equal outputs, slots and weights, over several calls in a row (the
-# arrival counter resets itself) and several column chunks.
-@pytest.mark.parametrize("mode,S,E", [(0, 1, 64), (1, 4, 32), (2, 7, 256), (3, 16, 128), (2, 16, 256)])
+# arrival counter resets itself) and several column chunks. At one row of
+# more than 64 experts the selection + union launch selects with four waves
+# (64 experts each, merged by wave 0), the separate selection with one.
+@pytest.mark.parametrize("mode,S,E", [(0, 1, 64), (1, 4, 32), (2, 7, 256), (3, 16, 128), (2, 16, 256), (1, 1, 256),
+                                    (2, 1, 256), (3, 1, 200)])
 def test_moe_fused_routing_bitwise(session, monkeypatch, mode, S, E):
     rng = np.random.default_rng(500 + mode * 7 + S + E)
     D, I, K = 1536, 256, 8 if E >= 64 else 4
