@@ -501,7 +501,7 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
                           sidx, skeff, gwrite);
 }
 
-// Selection of one token row (S = 1) by the first NW waves of a workgroup,
+// Selection of token row s (of S) by the first NW waves of a workgroup,
 // for the sigmoid-family modes 1-3 and E <= 64 NW: wave w scores experts
 // 64 w + lane (chunk partials summed in chunk order, as select_row) and ranks
 // them among its 64 by comparison; each wave's top K meet in LDS, and wave 0
@@ -515,7 +515,8 @@ __device__ __forceinline__ void select_row(const float *__restrict__ part, int n
 // [NW], selb [64] keys.
 template <int NW, bool ATOMIC>
 __device__ __forceinline__ void select_row_waves(const float *__restrict__ part, int nch,
-                                                 const float *__restrict__ bias, int E, int K, int mode, float topp,
+                                                 const float *__restrict__ bias, int S, int s, int E, int K, int mode,
+                                                 float topp,
                                                  int norm_topk, float routed_scale, int *__restrict__ idx,
                                                  float *__restrict__ wout, int *__restrict__ keff, float *p,
                                                  unsigned long long (*stage)[64], unsigned long long (*cand)[64],
@@ -526,14 +527,16 @@ __device__ __forceinline__ void select_row_waves(const float *__restrict__ part,
         const int e = 64 * wave + lane;
         const bool live = e < E;
         const int ee = live ? e : E - 1;
+        const size_t chstride = (size_t)S * E;
+        const float *z0 = part + (size_t)s * E + ee;
         float t[CH];
 #pragma unroll
-        for (int ch = 0; ch < CH; ch++) t[ch] = part[(size_t)min(ch, nch - 1) * E + ee];
+        for (int ch = 0; ch < CH; ch++) t[ch] = z0[(size_t)min(ch, nch - 1) * chstride];
         const float bs = bias ? bias[ee] : 0.0f;
         float z = t[0];
 #pragma unroll
         for (int ch = 1; ch < CH; ch++) z += ch < nch ? t[ch] : 0.0f;
-        for (int ch = CH; ch < nch; ch++) z += part[(size_t)ch * E + ee];
+        for (int ch = CH; ch < nch; ch++) z += z0[(size_t)ch * chstride];
         const float v = mode == 3 ? sqrtf(fmaxf(z, 0.0f) + log1pf(expf(-fabsf(z)))) : 1.0f / (1.0f + expf(-z));
         if (live) p[e] = v;
         unsigned k = 0;
@@ -593,7 +596,7 @@ __device__ __forceinline__ void select_row_waves(const float *__restrict__ part,
         my_w = p[my_e];
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    select_finish<ATOMIC>(my_e, my_w, want, E, K, mode, topp, norm_topk, routed_scale, p, idx, wout, keff, 0, lane,
+    select_finish<ATOMIC>(my_e, my_w, want, E, K, mode, topp, norm_topk, routed_scale, p, idx, wout, keff, s, lane,
                           sidx, skeff, gwrite);
 }
 

@@ -328,14 +328,14 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
     if (small)
         for (int i = threadIdx.x; i < 2 * (E + 1); i += blockDim.x) stab[i] = tab[i];
     if constexpr (MW) {
-        // one row (S = 1) of 65-256 experts, sigmoid-family router, K <= 16:
-        // the four waves score and rank 64 experts each and wave 0 merges
-        // their top K (same order and results as one wave's K rounds over
-        // all of them)
+        // one row per workgroup (65-256 experts, sigmoid-family router, K <=
+        // 16): the four waves score and rank 64 experts each and wave 0
+        // merges their top K (same order and results as one wave's K rounds
+        // over all of them)
         __shared__ __attribute__((aligned(16))) unsigned long long stage[4][64], cand[4][64], selb[64];
         __shared__ int nval[4];
-        select_row_waves<4, true>(part, nch, bias, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
-                                  (float *)work, stage, cand, nval, selb, sidx, skeff, true, wave, lane);
+        select_row_waves<4, true>(part, nch, bias, S, blockIdx.x, E, K, mode, topp, norm_topk, routed_scale, idx,
+                                  wsel, keff, (float *)work, stage, cand, nval, selb, sidx, skeff, true, wave, lane);
     } else {
         select_row<JM, true, false>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
                                     (float *)work + (size_t)wave * E, blockIdx.x * 4 + wave, lane, sidx, skeff);
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
         __syncthreads();
         if (!s_last) return;
         // the other workgroups' rows (this one's are in LDS already)
-        const int own0 = blockIdx.x * 4, own1 = min(S, own0 + 4);
+        const int own0 = MW ? blockIdx.x : blockIdx.x * 4, own1 = MW ? own0 + 1 : min(S, own0 + 4);
         for (int i = threadIdx.x; i < S * K; i += blockDim.x)
             if (i / K < own0 || i / K >= own1)
                 sidx[i] = __hip_atomic_load(idx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1027,9 +1027,11 @@ static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
     hipLaunchKernelGGL((coli_moe_select_union<JM>), grid, block, shm, st, m->logits, nch, m->rb, S, c.E, c.K,     \
                        c.route_mode, c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, m->route_cnt, \
                        c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state)
-    if (S == 1 && c.route_mode != 0 && c.E > 64 && c.E <= 256 && c.K <= 16) {
-        // one row: selected by four waves (S = 1 selection 8.0 -> 6.6 us at DSV3's 256 experts)
-        hipLaunchKernelGGL((coli_moe_select_union<4, true>), grid, block, shm, st, m->logits, nch, m->rb, S, c.E, c.K,
+    if (c.route_mode != 0 && c.E > 64 && c.E <= 256 && c.K <= 16) {
+        // one row per workgroup, selected by its four waves (DSV3's 256
+        // experts: S = 1 selection 8.0 -> 6.5 us)
+        hipLaunchKernelGGL((coli_moe_select_union<4, true>), dim3((unsigned)S), block, shm, st, m->logits, nch, m->rb, S,
+                           c.E, c.K,
                            c.route_mode, c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, m->route_cnt,
                            c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state);
         return hip_check(hipGetLastError(), "moe selection + union");
