@@ -374,12 +374,14 @@ def test_moe_layer_deepseek_v4(session, fmt, S, shared, limit):
 # Decode routing in one launch (router partials, selection and union; the
 # last workgroup to arrive selects) against the three separate launches:
 # bitwise equal outputs, slots and weights, over several calls in a row (the
-# arrival counter resets itself) and several column chunks. At one row of
-# more than 64 experts the selection + union launch selects with four waves
-# (64 experts each, merged by wave 0), the separate selection with one.
-@pytest.mark.parametrize("mode,S,E", [(0, 1, 64), (1, 4, 32), (2, 7, 256), (3, 16, 128), (2, 16, 256), (1, 1, 256),
-                                    (2, 1, 256), (3, 1, 200)])
-def test_moe_fused_routing_bitwise(session, monkeypatch, mode, S, E):
+# arrival counter resets itself) and several column chunks. Above 64 experts
+# the selection + union launch selects each row with four waves (64 experts
+# each, merged by wave 0), the separate selection with one; the TOPP cases
+# cut rows below K slots (checked).
+@pytest.mark.parametrize("mode,S,E,topp", [(0, 1, 64, 0.0), (1, 4, 32, 0.0), (2, 7, 256, 0.0), (3, 16, 128, 0.0),
+                                         (2, 16, 256, 0.0), (1, 1, 256, 0.0), (2, 1, 256, 0.0), (3, 1, 200, 0.0),
+                                         (1, 3, 256, 0.5), (2, 5, 200, 0.6)])
+def test_moe_fused_routing_bitwise(session, monkeypatch, mode, S, E, topp):
     rng = np.random.default_rng(500 + mode * 7 + S + E)
     D, I, K = 1536, 256, 8 if E >= 64 else 4
     layer = Layer(rng, 4, D, I, E, shared=mode == 2)
@@ -388,7 +390,7 @@ def test_moe_fused_routing_bitwise(session, monkeypatch, mode, S, E):
         monkeypatch.setenv("COLI_HIP_FUSED_ROUTE", fused)
         m, hs = make_moe(session, layer, *make_router_inputs(np.random.default_rng(7), S, D, E, K, mode,
                                                              bias=(mode != 0))[1:], K, mode,
-                         norm_topk=1 if mode == 1 else 0, routed_scale=2.5 if mode == 1 else 1.0)
+                         norm_topk=1 if mode == 1 else 0, topp=topp, routed_scale=2.5 if mode == 1 else 1.0)
         got = []
         try:
             for call in range(3):
@@ -408,3 +410,5 @@ def test_moe_fused_routing_bitwise(session, monkeypatch, mode, S, E):
     for a, b in zip(runs["1"], runs["0"]):
         for u, v in zip(a, b):
             assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+    if topp > 0.0:
+        assert any((got[3] < K).any() for got in runs["1"])
