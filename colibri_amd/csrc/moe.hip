@@ -439,9 +439,9 @@ __global__ __launch_bounds__(256) void coli_moe_route(const float *__restrict__ 
 // ---------------------------------------------------------------------------
 
 template <int KIND>
-__device__ __forceinline__ float dc_group(uint32_t wd, const ScaleRegs<KIND> &sc, int j, const float *xp) {
+__device__ __forceinline__ float dc_group(uint32_t wd, const ScaleRegs<KIND> &sc, int j, const floatx4 &a,
+                                          const floatx4 &b) {
     float x[8];
-    const floatx4 a = *(const floatx4 *)xp, b = *(const floatx4 *)(xp + 4);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         x[i] = a[i];
@@ -471,18 +471,52 @@ __device__ __forceinline__ float dc_group(uint32_t wd, const ScaleRegs<KIND> &sc
     }
 }
 
-// NQ: the tile's 128-column quads (the expert's intermediate size is
-// exactly NQ x 128), all held in registers. At most COLI_DC_WAVES problems (routed + shared).
+template <int KIND>
+__device__ __forceinline__ float dc_group(uint32_t wd, const ScaleRegs<KIND> &sc, int j, const float *xp) {
+    return dc_group<KIND>(wd, sc, j, *(const floatx4 *)xp, *(const floatx4 *)(xp + 4));
+}
+
+// One-token down projection of every problem + the combine, one workgroup
+// per 16-row tile of the output: wave p holds problem p's whole tile (NQ
+// 128-column quads: the expert's intermediate size is exactly NQ x 128, all
+// in registers, all requested at once) and reduces it against its row of h;
+// wave 0 then adds the problems' rows in slot order (c/colibri.c:4781-4782),
+// the shared expert last. At most COLI_DC_WAVES problems (routed + shared).
+// The row of h stays in registers: lane (ks, r) loads h[32 (4q + r/4) + 8 ks +
+// 2 (r%4) + {0, 1}] of each quad q (the 32 activations its 16-lane row ks
+// needs, two a lane), and every product takes its activation from lane
+// 4j + i/2 of the row by a DPP row broadcast, with no LDS traffic (staging the
+// row in LDS, 64 B read per lane and group, was slower: DSV3 B1 layer 60.1 ->
+// 57.5 us, the 21 per-token passes 1236 -> 1172 us).
 #define COLI_DC_WAVES 10
+template <int ROWLANE>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + ROWLANE, 0xF, 0xF,
+                                                              true));
+}
+template <int KIND, int J>
+__device__ __forceinline__ float dc_group_dpp(uint32_t wd, const ScaleRegs<KIND> &sc, const float (&xr)[2]) {
+    float x[8];
+    x[0] = row_bcast<4 * J + 0>(xr[0]);
+    x[1] = row_bcast<4 * J + 0>(xr[1]);
+    x[2] = row_bcast<4 * J + 1>(xr[0]);
+    x[3] = row_bcast<4 * J + 1>(xr[1]);
+    x[4] = row_bcast<4 * J + 2>(xr[0]);
+    x[5] = row_bcast<4 * J + 2>(xr[1]);
+    x[6] = row_bcast<4 * J + 3>(xr[0]);
+    x[7] = row_bcast<4 * J + 3>(xr[1]);
+    return dc_group<KIND>(wd, sc, J, (floatx4){x[0], x[1], x[2], x[3]}, (floatx4){x[4], x[5], x[6], x[7]});
+}
+
 template <int KIND, int NQ>
 __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(const ColiProb *__restrict__ pdown,
-                                                               const int *__restrict__ state,
-                                                               const float *__restrict__ h, int D,
-                                                               const float *__restrict__ w, const int *__restrict__ keff,
-                                                               const int *__restrict__ slotrow, int K, int has_shared,
-                                                               float *__restrict__ out) {
+                                                                const int *__restrict__ state,
+                                                                const float *__restrict__ h, int D,
+                                                                const float *__restrict__ w,
+                                                                const int *__restrict__ keff,
+                                                                const int *__restrict__ slotrow, int K,
+                                                                int has_shared, float *__restrict__ out) {
     __shared__ float ys[COLI_DC_WAVES][16];   // [problem][tile row]
-    extern __shared__ __attribute__((aligned(16))) float hsm[];   // [wave][NQ * 128]: the wave's row of h
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rb = blockIdx.x;
     // the live count, this wave's descriptor (the array holds one per wave
@@ -503,18 +537,20 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
     }
     if (wave < P) {
         const ColiProb pr = uniform_prob(pd);
-        const float *hr = h + (size_t)pr.xrow_off * (NQ * 128);
-        float *hs = hsm + wave * (NQ * 128);
+        const int ks = lane >> 4, r16 = lane & 15;
+        const float *hr = h + (size_t)pr.xrow_off * (NQ * 128) + 8 * ks + 2 * (r16 & 3) + 32 * (r16 >> 2);
         const size_t t0 = (size_t)rb * NQ;
         const uint8_t *wt = pr.w0 + t0 * COLI_TILE_BYTES;
-        const int ks = lane >> 4, r16 = lane & 15;
-        // the row of h (issued first, through registers into LDS: an LDS DMA
-        // would make the compiler drain every load before the first LDS
-        // read) and every weight quad of the tile: all in flight at once;
-        // the LDS writes wait for h only, and each quad for its own weights
-        floatx4 hv[NQ / 2];
+        // h first, then every weight quad of the tile: all in flight at once.
+        // (Two scalar loads, which the compiler pairs: the elements of one
+        // vector load broadcast by DPP were folded into one broadcast by this
+        // toolchain, a wrong result.)
+        float xq[NQ][2];
 #pragma unroll
-        for (int k = 0; k < NQ / 2; k++) hv[k] = *GPTR(floatx4, hr + (k * 64 + lane) * 4);
+        for (int q = 0; q < NQ; q++) {
+            xq[q][0] = hr[q * 128];
+            xq[q][1] = hr[q * 128 + 1];
+        }
         u32x4 wq[NQ];
         ScaleRegs<KIND> sq[NQ];
 #pragma unroll
@@ -522,18 +558,13 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
             wq[q] = __builtin_nontemporal_load(GPTR(u32x4, wt + (size_t)q * COLI_TILE_BYTES) + lane);
             sq[q].load(pr.s0, t0 + q, r16);
         }
-#pragma unroll
-        for (int k = 0; k < NQ / 2; k++) *(floatx4 *)(hs + (k * 64 + lane) * 4) = hv[k];
         float acc = 0.0f;
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
-            // one quad's activations at a time (not every quad's hoisted)
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int col = 32 * (4 * q + j) + 8 * ks;
-                acc += dc_group<KIND>(wq[q][j], sq[q], j, hs + col);
-            }
+            acc += dc_group_dpp<KIND, 0>(wq[q][0], sq[q], xq[q]);
+            acc += dc_group_dpp<KIND, 1>(wq[q][1], sq[q], xq[q]);
+            acc += dc_group_dpp<KIND, 2>(wq[q][2], sq[q], xq[q]);
+            acc += dc_group_dpp<KIND, 3>(wq[q][3], sq[q], xq[q]);
         }
         acc += __shfl_xor(acc, 16);
         acc += __shfl_xor(acc, 32);
@@ -1227,8 +1258,7 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     if (!gemm && S == 1 && pmax <= COLI_DC_WAVES && (c.I == 1024 || c.I == 2048) && down_combine_enabled()) {
         const dim3 grid((unsigned)nrt_d), block(64 * pmax);
 #define COLI_DC_LAUNCH(KD, NQ)                                                                                  \
-    hipLaunchKernelGGL((coli_moe_down_combine1<KD, NQ>), grid, block, (size_t)pmax * c.I * 4, st, m->pdown,  \
-                       m->state, m->h, c.D,                                                                \
+    hipLaunchKernelGGL((coli_moe_down_combine1<KD, NQ>), grid, block, 0, st, m->pdown, m->state, m->h, c.D,     \
                        m->wsel, m->keff, m->slotrow, c.K, c.has_shared, out_dev)
 #define COLI_DC_KIND(KD)                \
     if (nq_i == 8) COLI_DC_LAUNCH(KD, 8); \
