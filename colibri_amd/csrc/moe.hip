@@ -218,7 +218,8 @@ __device__ __forceinline__ void moe_union_wave(const int *idx, const int *keff, 
                                                const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual,
                                                ColiProb *__restrict__ pdown, int *__restrict__ uniq,
                                                int *__restrict__ xrows, int *__restrict__ slotrow,
-                                               int *__restrict__ mt, int *__restrict__ state, int lane) {
+                                               int *__restrict__ mt, int *__restrict__ state, int lane,
+                                               int shared_row = -1) {
     const int n = S * K;
     const int t = lane / K, kk = lane - t * K;
     int e = -1;
@@ -276,6 +277,8 @@ __device__ __forceinline__ void moe_union_wave(const int *idx, const int *keff, 
             sd.nrows = sdn.nrows = S;
             sd.xrow_off = sdn.xrow_off = rows_routed;
             sd.out_row0 = sdn.out_row0 = rows_routed;
+            // (its h row written elsewhere, at a row the selection does not move)
+            if (shared_row >= 0) sdn.xrow_off = shared_row;
             pdual[nu] = sd;
             pdown[nu] = sdn;
             mt[nu] = nu << 16;
@@ -812,20 +815,65 @@ template <int KIND, int W, int NQW>
 __global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restrict__ pdual,
                                                          const int *__restrict__ state, const float *__restrict__ x,
                                                          int D, int nrt, float *__restrict__ h, int I,
-                                                         float swiglu_limit) {
+                                                         float swiglu_limit, int routed_only) {
     __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
     __shared__ float red[W][2][16];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
     // the live count and the descriptor (in the array: p < the launch's
-    // problem count) in one round trip
-    const int np = state[0];
+    // problem count) in one round trip; routed_only: the shared expert's
+    // gate/up ran in the selection launch
+    const int np = state[routed_only ? 2 : 0];
     const ColiProb pd = pdual[p];
     if (p >= np) return;
     const ColiProb pr = uniform_prob(pd);
     floatx4 xv[NQW / 2 + 1];
     dual1_load_x<W, NQW>(x, xv, wave, lane);
     dual1_tile<KIND, W, NQW>(pr, rt, xv, xs, red, h, I, swiglu_limit, wave, lane);
+}
+
+// ---------------------------------------------------------------------------
+// One token, 65-256 experts with a shared expert: the selection + union of
+// coli_moe_select_union (workgroup 0, its first four waves) and the shared
+// expert's gate/up + SwiGLU (workgroups 1..nrt, one 16-row tile each, the code
+// and decomposition of coli_moe_dual1) in one launch: the shared expert needs
+// no selection, so its weights stream while one workgroup selects. Its row of
+// h goes to row K (the routed experts take rows 0..keff-1); the union points
+// the down projection there, and the gate/up launch that follows runs the
+// routed problems only.
+// ---------------------------------------------------------------------------
+template <int KIND, int W, int NQW>
+__global__ __launch_bounds__(64 * W) void coli_moe_select_union_sh(
+    const float *__restrict__ part, int nch, const float *__restrict__ bias, int E, int K, int mode, float topp,
+    int norm_topk, float routed_scale, int *__restrict__ idx, float *__restrict__ wsel, int *__restrict__ keff,
+    const ColiProb *__restrict__ tab, ColiProb *__restrict__ pdual, ColiProb *__restrict__ pdown,
+    int *__restrict__ uniq, int *__restrict__ xrows, int *__restrict__ slotrow, int *__restrict__ mt,
+    int *__restrict__ state, const float *__restrict__ x, float *__restrict__ h, int I, float swiglu_limit) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (blockIdx.x > 0) {
+        __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
+        __shared__ float red[W][2][16];
+        floatx4 xv[NQW / 2 + 1];
+        dual1_load_x<W, NQW>(x, xv, wave, lane);
+        ColiProb pr = uniform_prob(tab[2 * E]);
+        pr.nrows = 1;
+        pr.xrow_off = 0;
+        pr.out_row0 = K;
+        dual1_tile<KIND, W, NQW>(pr, (int)blockIdx.x - 1, xv, xs, red, h, I, swiglu_limit, wave, lane);
+        return;
+    }
+    extern __shared__ int sm[];
+    // LDS: slots [K] | keff [1] | selection weights, then the descriptor templates
+    int *sidx = sm, *skeff = sm + K, *work = skeff + 1;
+    ColiProb *stab = (ColiProb *)(((uintptr_t)(work + moe_work_ints(E)) + 15) & ~(uintptr_t)15);
+    for (int i = threadIdx.x; i < 2 * (E + 1); i += blockDim.x) stab[i] = tab[i];
+    __shared__ __attribute__((aligned(16))) unsigned long long stage[4][64], cand[4][64], selb[64];
+    __shared__ int nval[4];
+    select_row_waves<4, true>(part, nch, bias, 1, 0, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
+                              (float *)work, stage, cand, nval, selb, sidx, skeff, true, wave, lane);
+    __syncthreads();
+    if (wave == 0)
+        moe_union_wave(sidx, skeff, 1, K, E, 1, stab, pdual, pdown, uniq, xrows, slotrow, mt, state, lane, K);
 }
 
 // ---------------------------------------------------------------------------
@@ -1088,12 +1136,13 @@ static bool dual1_enabled() {
 
 // One token's gate/up + SwiGLU for the hidden sizes it is built for (2048:
 // 4 waves x 4 quads, 7168: 8 waves x 7 quads); false: not launched.
-static bool launch_dual1(ColiHipMoe *m, hipStream_t st, const float *x, int nrt, int nq, int P) {
+static bool launch_dual1(ColiHipMoe *m, hipStream_t st, const float *x, int nrt, int nq, int P,
+                         bool routed_only = false) {
     const ColiHipMoeConfig &c = m->cfg;
-    const dim3 grid((unsigned)(P * nrt));
+    const dim3 grid((unsigned)((routed_only ? P - 1 : P) * nrt));
 #define COLI_D1(KD, W, NQW)                                                                                   \
     hipLaunchKernelGGL((coli_moe_dual1<KD, W, NQW>), grid, dim3(64 * W), 0, st, m->pdual, m->state, x, c.D, nrt, \
-                       m->h, c.I, c.swiglu_limit)
+                       m->h, c.I, c.swiglu_limit, routed_only ? 1 : 0)
 #define COLI_D1_KIND(W, NQW)                                                  \
     if (m->kind == COLI_KIND_I4_H) COLI_D1(COLI_KIND_I4_H, W, NQW);          \
     else if (m->kind == COLI_KIND_I4_F) COLI_D1(COLI_KIND_I4_F, W, NQW);     \
@@ -1104,6 +1153,40 @@ static bool launch_dual1(ColiHipMoe *m, hipStream_t st, const float *x, int nrt,
 #undef COLI_D1_KIND
 #undef COLI_D1
     return false;
+}
+
+// COLI_HIP_SHARED_OVERLAP=0: the shared expert's gate/up stays in the gate/up
+// launch instead of running beside the selection.
+static bool shared_overlap_enabled() {
+    const char *e = std::getenv("COLI_HIP_SHARED_OVERLAP");
+    return !(e && e[0] == '0');
+}
+
+// The selection + union with the shared expert's gate/up beside it (one
+// token, four-wave selection of 65-256 experts, the hidden sizes the one-token
+// gate/up is built for); false: not built for the shape.
+static bool launch_select_union_sh(ColiHipMoe *m, hipStream_t st, int nch, const float *x, int nrt, int nq) {
+    const ColiHipMoeConfig &c = m->cfg;
+    if (!c.has_shared || c.route_mode == 0 || c.E <= 64 || c.E > 256 || c.K > 16 ||
+        !((c.D == 2048 && nq == 16) || (c.D == 7168 && nq == 56)))
+        return false;
+    const size_t shm = (size_t)(c.K + 1) * sizeof(int) + (size_t)moe_work_ints(c.E) * sizeof(int) + 16 +
+                       (size_t)2 * (c.E + 1) * sizeof(ColiProb);
+    const dim3 grid((unsigned)(1 + nrt));
+#define COLI_SUS(KD, W, NQW)                                                                                    \
+    hipLaunchKernelGGL((coli_moe_select_union_sh<KD, W, NQW>), grid, dim3(64 * W), shm, st, m->logits, nch, m->rb, \
+                       c.E, c.K, c.route_mode, c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff,      \
+                       m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state, x, m->h, c.I,   \
+                       c.swiglu_limit)
+#define COLI_SUS_KIND(W, NQW)                                                 \
+    if (m->kind == COLI_KIND_I4_H) COLI_SUS(COLI_KIND_I4_H, W, NQW);          \
+    else if (m->kind == COLI_KIND_I4_F) COLI_SUS(COLI_KIND_I4_F, W, NQW);     \
+    else COLI_SUS(COLI_KIND_FP4, W, NQW);                                     \
+    return true
+    if (c.D == 2048) { COLI_SUS_KIND(4, 4); }
+    COLI_SUS_KIND(8, 7);
+#undef COLI_SUS_KIND
+#undef COLI_SUS
 }
 
 // COLI_HIP_ROUTE_DUAL1=0: at one token, the selection + union keep their own
@@ -1187,6 +1270,15 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
     // One token, up to 64 experts: the router partials, then the selection and
     // the union inside the gate/up launch (every workgroup selects for itself).
     bool gateup_done = false;
+    // One token, 65-256 experts and a shared expert, the one-token gate/up and
+    // down + combine: the shared expert's gate/up runs in the selection launch
+    // (the down + combine reads its h from row K).
+    const int pmax1 = c.K + (c.has_shared ? 1 : 0);
+    const bool shared_overlap = S == 1 && !gemm && c.has_shared && shared_overlap_enabled() && dual1_enabled() &&
+                                c.route_mode != 0 && c.E > 64 && c.E <= 256 && c.K <= 16 &&
+                                ((c.D == 2048 && nq_d == 16) || (c.D == 7168 && nq_d == 56)) &&
+                                pmax1 <= COLI_DC_WAVES && (c.I == 1024 || c.I == 2048) && down_combine_enabled() && !fused_route_disabled() &&
+                                !(S <= 16 && (long)((c.E + 3) / 4) * coli_router_chunks(c.D) <= 128);
     if (S == 1 && !gemm && dual1_enabled() && route_dual1_enabled() && !fused_route_disabled() &&
         c.K <= 64 && c.E <= 64 && ((c.D == 2048 && nq_d == 16) || (c.D == 7168 && nq_d == 56))) {
         const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
@@ -1200,6 +1292,13 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
         // them serialize (measured: 896 arrivals cost more than the two
         // launches they save)
         if (!launch_route(m, x_dev, S, st)) return 0;
+    } else if (S == 1 && !gemm && shared_overlap && !fused_route_disabled()) {
+        // 2. router partials, 3-4. selection and union with the shared
+        // expert's gate/up beside them
+        const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
+        if (!nch || !launch_select_union_sh(m, st, nch, x_dev, nrt_i, nq_d) ||
+            !hip_check(hipGetLastError(), "moe selection + union + shared gate/up"))
+            return 0;
     } else if (S <= 64 && !fused_route_disabled()) {
         // 2. router partials, 3-4. selection and union in one launch
         const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
@@ -1226,7 +1325,7 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
         if (!run_gemm(ctx, m->kind, true, m->pdual, P, m->state, m->mt, m->state + 3, moe_tiles(c, S), nrt_i, nq_d,
                       c.I, fx, m->xrows, m->h, c.I, c.swiglu_limit, fold))
             return 0;
-    } else if (S == 1 && dual1_enabled() && launch_dual1(m, st, x_dev, nrt_i, nq_d, P)) {
+    } else if (S == 1 && dual1_enabled() && launch_dual1(m, st, x_dev, nrt_i, nq_d, P, shared_overlap)) {
         if (!hip_check(hipGetLastError(), "moe gate/up")) return 0;
     } else if (!run_gemv(ctx, m->kind, true, m->pdual, P, m->state, nrt_i, nq_d, c.I, S, fx, m->xrows, m->h, c.I,
                          nullptr, c.swiglu_limit, nullptr, nullptr, fold)) {

@@ -182,6 +182,58 @@ def test_one_token_routing_inside_gateup_bitwise(session, monkeypatch, shape):
     assert rel_err(out, ref, mag).max() <= TOL
 
 
+# One token, 65-256 experts and a shared expert: the shared expert's gate/up
+# runs in the selection launch (its h at row K) against the gate/up launch
+# (COLI_HIP_SHARED_OVERLAP=0): outputs, indices, weights and keff bitwise
+# equal, and against the oracle. DSV3's shape in MXFP4 (the f32 down +
+# combine); int4 at D 2048 with the matrix-core down + combine (I 1024) and a
+# TOPP cut below K; the sqrt-softplus router with K = 6 of 200 experts.
+@pytest.mark.parametrize("shape", ["dsv3", "e256_topp_i1024", "e200_mode3"])
+def test_one_token_shared_beside_selection_bitwise(session, monkeypatch, shape):
+    rng = np.random.default_rng(4900 + len(shape))
+    if shape == "dsv3":
+        D, I, E, K, fmt, mode = 7168, 2048, 256, 8, 7, 2
+    elif shape == "e256_topp_i1024":
+        D, I, E, K, fmt, mode = 2048, 1024, 256, 8, 4, 1
+    else:
+        D, I, E, K, fmt, mode = 2048, 2048, 200, 6, 4, 3
+    layer = Layer(rng, fmt, D, I, E, shared=True, distinct=6)
+    x, W, b = make_router_inputs(rng, 1, D, E, K, mode, bias=True)
+    hs = layer.upload(session)
+    routed, sh = hs[:E], hs[E]
+    g, _ga = tensor_array([h[0] for h in routed])
+    u, _ua = tensor_array([h[1] for h in routed])
+    d, _da = tensor_array([h[2] for h in routed])
+    topp, norm = 0.0, 1 if mode == 1 else 0
+    if shape == "e256_topp_i1024":   # a cut the oracle says keeps fewer than K experts
+        for cand in (0.6, 0.5, 0.4, 0.3, 0.2):
+            if cref.route(cref.matmul_f32(x, W), K, mode, bias=b, norm_topk=norm, topp=cand)[2][0] < K:
+                topp = cand
+                break
+        assert topp > 0.0
+    cfg = ColiHipMoeConfig(D, I, E, K, mode, norm, topp, 1.0, 1, 0.0)
+    m = C.c_void_p()
+    assert session.b.hip_moe_create(C.byref(m), 0, C.byref(cfg), f32p(np.ascontiguousarray(W)),
+                                    f32p(np.ascontiguousarray(b)), g, u, d, sh[0], sh[1], sh[2])
+    try:
+        res = []
+        for env in ("1", "0", "1"):
+            monkeypatch.setenv("COLI_HIP_SHARED_OVERLAP", env)
+            res.append(forward(session, m, x, K))
+    finally:
+        session.b.hip_moe_free(m)
+        free_handles(session, hs)
+    for a, c in ((res[0], res[1]), (res[0], res[2])):
+        for ta, tc in zip(a, c):
+            assert np.array_equal(ta.view(np.uint32) if ta.dtype == np.float32 else ta,
+                                  tc.view(np.uint32) if tc.dtype == np.float32 else tc)
+    out, idx, w, keff = res[0]
+    ri, rw, rk = cref.route(cref.matmul_f32(x, W), K, mode, bias=b, norm_topk=norm, topp=topp)
+    assert np.array_equal(keff, rk) and np.array_equal(idx[:, :rk[0]], ri[:, :rk[0]])
+    _, _, _, ref, mag = moe_reference(layer, x, W, b, K, mode, norm_topk=norm, topp=topp)
+    assert rel_err(out, ref, mag).max() <= TOL
+
+
 # one verification step (16-node draft tree + 5-token linear
 # draft = 21 rows) on the configs[2] layer, MXFP4 and int4
 @pytest.mark.parametrize("fmt", [7, 4])
