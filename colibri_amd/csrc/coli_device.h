@@ -268,3 +268,96 @@ __device__ __forceinline__ void dma_wait_tail(int pend) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// ---------------------------------------------------------------------------
+// Activation-fragment build (the format and its reasons are described with
+// coli_prep_frag in gemv.hip), shared by that kernel and launches that run
+// the build beside other work.
+// ---------------------------------------------------------------------------
+#define COLI_PREP_SLOTS 8
+// Block `blk` of the build (every thread of a 256-thread block calls it).
+__device__ __forceinline__ void prep_frag_block(const ColiPrepArgs &a, int blk) {
+    const float *__restrict__ x = a.x;
+    const int *__restrict__ src_row = a.src_row, *__restrict__ nrows_dev = a.nrows_dev;
+    _Float16 *__restrict__ hi = a.hi, *__restrict__ lo = a.lo;
+    int *__restrict__ exp2out = a.exp2out, *__restrict__ haslo = a.haslo;
+    const float *__restrict__ zero = a.zero;
+    const int ldx = a.ldx, K = a.K, ngp = a.ngp, int4_order = a.int4_order, gen = a.gen, vec = a.vec,
+              nchunk = a.nchunk;
+    const int r = blk / nchunk, chunk = blk - r * nchunk;
+    if (nrows_dev && r >= *nrows_dev) return;
+    const int srow = src_row ? src_row[r] : r;
+    if (srow < 0) return;
+    const float *xr = x + (size_t)srow * ldx;
+    const int nslot = ngp * 4;
+    auto load_slot = [&](int slot, float (&v)[8]) {
+        const int k0 = slot * 8;
+        if (vec) {   // aligned rows, K % 8 == 0: slots past K read zeros
+            const float *p = slot < nslot && k0 < K ? xr + k0 : zero;
+            const floatx4 a = *GPTR(floatx4, p), b = *GPTR(floatx4, p + 4);
+#pragma unroll
+            for (int t = 0; t < 4; t++) { v[t] = a[t]; v[t + 4] = b[t]; }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; t++) v[t] = slot < nslot && k0 + t < K ? xr[k0 + t] : 0.0f;
+        }
+    };
+    float v[COLI_PREP_SLOTS][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < COLI_PREP_SLOTS; i++) load_slot(threadIdx.x + 256 * i, v[i]);
+#pragma unroll
+    for (int i = 0; i < COLI_PREP_SLOTS; i++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) m = fmaxf(m, fabsf(v[i][t]));
+    for (int slot = threadIdx.x + 256 * COLI_PREP_SLOTS; slot < nslot; slot += 256) {
+        float u[8];
+        load_slot(slot, u);
+#pragma unroll
+        for (int t = 0; t < 8; t++) m = fmaxf(m, fabsf(u[t]));
+    }
+#pragma unroll
+    for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __shared__ float wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int E = 0;
+    if (m > 0.0f && isfinite(m)) {
+        frexpf(m, &E);
+        E -= 15;
+    }
+    if (threadIdx.x == 0 && chunk == 0) exp2out[r] = E;
+    bool any = false;
+    auto convert = [&](int slot, const float (&u)[8]) {
+        if (slot >= nslot) return;
+        _Float16 h[8], l[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            int off = int4_order ? ((t < 4) ? 2 * t : 2 * (t - 4) + 1) : t;
+            float y = ldexpf(u[off], -E);
+            if (int4_order && (off & 1)) y *= 0.0625f;
+            h[t] = (_Float16)y;
+            l[t] = (_Float16)(y - (float)h[t]);
+            any |= (l[t] != (_Float16)0.0f);
+        }
+        const size_t base = (size_t)r * ngp * 32 + (size_t)slot * 8;
+        *(half8v *)(hi + base) = (half8v){h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
+        *(half8v *)(lo + base) = (half8v){l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
+    };
+#pragma unroll
+    for (int i = 0; i < COLI_PREP_SLOTS; i++)
+        if (i % nchunk == chunk) convert(threadIdx.x + 256 * i, v[i]);
+    for (int i = COLI_PREP_SLOTS; 256 * i < nslot; i++) {
+        if (i % nchunk != chunk) continue;
+        const int slot = threadIdx.x + 256 * i;
+        float u[8];
+        load_slot(slot, u);
+        convert(slot, u);
+    }
+    // every block with a lo part raises the flag; once one has, the others
+    // see it and skip their atomic (thousands of blocks on one address
+    // serialize: 4096 rows took 53 us instead of 6)
+    if (__syncthreads_or(any) && threadIdx.x == 0 &&
+        __hip_atomic_load(haslo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen)
+        atomicMax(haslo, gen);
+}

@@ -115,7 +115,8 @@ hipError_t coli_launch_gemv_dma(int kind, const ColiGemvArgs *a, int R, int dual
                                 hipStream_t st);
 hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row, const int *nrows_dev,
                                  int nrows, int K, int ngp, int int4_order, _Float16 *hi, _Float16 *lo,
-                                 int *exp2out, int *haslo, int gen, const void *zero, hipStream_t st);
+                                 int *exp2out, int *haslo, int gen, const void *zero, hipStream_t st,
+                                 ColiPrepArgs *args_only = nullptr);
 hipError_t coli_launch_gemm(int kind, int dual, const ColiGemmArgs *a, hipStream_t st);
 hipError_t coli_launch_gemm_mx(int dual, const ColiGemmMxArgs *a, hipStream_t st);
 hipError_t coli_launch_prep_fp8(const float *x, int ldx, const int *src_row, const int *nrows_dev, int nrows, int K,
@@ -170,6 +171,10 @@ GemvLaunchPlan plan_gemv(const DevCtx *ctx, int nprob, int n_bt, int nrt, int nq
 int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, int int4_order,
                const int *src_rows = nullptr, const int *nrows_dev = nullptr);
 int flush_frags(DevCtx *ctx, int set);
+// the pending build of `set` made ready (buffers, generation) but returned as
+// launch arguments for a launch that runs it beside other work (nblocks 0:
+// nothing pending)
+int flush_frags_args(DevCtx *ctx, int set, ColiPrepArgs *a);
 int frag_set_of(int kind, bool hidden);
 // Activation pieces of the MXFP4 grouped GEMM (e4m3 + e8m0 per 32 columns)
 // of the same rows, into fragment set `set`.

@@ -60,6 +60,20 @@ struct ColiProb {
     int pad;
 };
 
+// One activation-fragment build (coli_prep_frag): nblocks 256-thread blocks,
+// nchunk per row.
+struct ColiPrepArgs {
+    const float *x;
+    const int *src_row;
+    const int *nrows_dev;
+    _Float16 *hi;
+    _Float16 *lo;
+    int *exp2out;
+    int *haslo;
+    const float *zero;
+    int ldx, K, ngp, int4_order, gen, vec, nchunk, nblocks;
+};
+
 struct ColiGemvArgs {
     const ColiProb *prob;     // device descriptors; null: the single problem prob0
     ColiProb prob0;

@@ -177,7 +177,10 @@ int make_frags(DevCtx *ctx, int set, const float *x, int ld, int nrows, int K, i
 
 // Build the pending fragments of f. ws == null: grow-only context buffers;
 // else the caller's fixed buffers (capacity checked, nothing allocated).
-static int flush_frags_into(DevCtx *ctx, FragSet &f, int *flag, const void *zero, const GemvScratch *ws) {
+// args_only: the build's launch arguments are returned instead of launched.
+static int flush_frags_into(DevCtx *ctx, FragSet &f, int *flag, const void *zero, const GemvScratch *ws,
+                            ColiPrepArgs *args_only = nullptr) {
+    if (args_only) args_only->nblocks = 0;
     if (!f.pending) return 1;
     f.pending = false;
     const float *x = f.px;
@@ -195,12 +198,16 @@ static int flush_frags_into(DevCtx *ctx, FragSet &f, int *flag, const void *zero
     if (f.gen == 1 && !hip_check(coli_launch_zero_i32(flag, 1, ctx->stream), "fragment flag")) return 0;
     return hip_check(coli_launch_prep_frag(x, ld, src_rows, nrows_dev, nrows, K, ngp, int4_order,
                                         (_Float16 *)f.hi.p, (_Float16 *)f.lo.p, (int *)f.exp.p, flag, f.gen,
-                                        zero, ctx->stream),
+                                        zero, ctx->stream, args_only),
                   "fragment prep");
 }
 
 int flush_frags(DevCtx *ctx, int set) {
     return flush_frags_into(ctx, ctx->frag[set], (int *)ctx->flags.p + set, ctx->zeros.p, nullptr);
+}
+
+int flush_frags_args(DevCtx *ctx, int set, ColiPrepArgs *a) {
+    return flush_frags_into(ctx, ctx->frag[set], (int *)ctx->flags.p + set, ctx->zeros.p, nullptr, a);
 }
 
 // Many-row MXFP4 problems run the exact fp16-MFMA grouped GEMM by default.

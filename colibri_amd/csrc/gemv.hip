@@ -133,92 +133,7 @@ __global__ void coli_repack_scales_e8(const uint8_t *__restrict__ src, int O, in
 // *haslo with an atomic max: the GEMV treats any flag >= its generation as
 // "lo present", so the flag never needs clearing and stays correct when a
 // captured graph replays an old generation.
-#define COLI_PREP_SLOTS 8
-__global__ __launch_bounds__(256) void coli_prep_frag(const float *__restrict__ x, int ldx,
-                                                      const int *__restrict__ src_row,
-                                                      const int *__restrict__ nrows_dev, int K, int ngp,
-                                                      int int4_order, _Float16 *__restrict__ hi,
-                                                      _Float16 *__restrict__ lo, int *__restrict__ exp2out,
-                                                      int *__restrict__ haslo, int gen, int vec, int nchunk,
-                                                      const float *__restrict__ zero) {
-    const int r = blockIdx.x / nchunk, chunk = blockIdx.x - r * nchunk;
-    if (nrows_dev && r >= *nrows_dev) return;
-    const int srow = src_row ? src_row[r] : r;
-    if (srow < 0) return;
-    const float *xr = x + (size_t)srow * ldx;
-    const int nslot = ngp * 4;
-    auto load_slot = [&](int slot, float (&v)[8]) {
-        const int k0 = slot * 8;
-        if (vec) {   // aligned rows, K % 8 == 0: slots past K read zeros
-            const float *p = slot < nslot && k0 < K ? xr + k0 : zero;
-            const floatx4 a = *GPTR(floatx4, p), b = *GPTR(floatx4, p + 4);
-#pragma unroll
-            for (int t = 0; t < 4; t++) { v[t] = a[t]; v[t + 4] = b[t]; }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 8; t++) v[t] = slot < nslot && k0 + t < K ? xr[k0 + t] : 0.0f;
-        }
-    };
-    float v[COLI_PREP_SLOTS][8];
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < COLI_PREP_SLOTS; i++) load_slot(threadIdx.x + 256 * i, v[i]);
-#pragma unroll
-    for (int i = 0; i < COLI_PREP_SLOTS; i++)
-#pragma unroll
-        for (int t = 0; t < 8; t++) m = fmaxf(m, fabsf(v[i][t]));
-    for (int slot = threadIdx.x + 256 * COLI_PREP_SLOTS; slot < nslot; slot += 256) {
-        float u[8];
-        load_slot(slot, u);
-#pragma unroll
-        for (int t = 0; t < 8; t++) m = fmaxf(m, fabsf(u[t]));
-    }
-#pragma unroll
-    for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    __shared__ float wmax[4];
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    int E = 0;
-    if (m > 0.0f && isfinite(m)) {
-        frexpf(m, &E);
-        E -= 15;
-    }
-    if (threadIdx.x == 0 && chunk == 0) exp2out[r] = E;
-    bool any = false;
-    auto convert = [&](int slot, const float (&u)[8]) {
-        if (slot >= nslot) return;
-        _Float16 h[8], l[8];
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            int off = int4_order ? ((t < 4) ? 2 * t : 2 * (t - 4) + 1) : t;
-            float y = ldexpf(u[off], -E);
-            if (int4_order && (off & 1)) y *= 0.0625f;
-            h[t] = (_Float16)y;
-            l[t] = (_Float16)(y - (float)h[t]);
-            any |= (l[t] != (_Float16)0.0f);
-        }
-        const size_t base = (size_t)r * ngp * 32 + (size_t)slot * 8;
-        *(half8v *)(hi + base) = (half8v){h[0], h[1], h[2], h[3], h[4], h[5], h[6], h[7]};
-        *(half8v *)(lo + base) = (half8v){l[0], l[1], l[2], l[3], l[4], l[5], l[6], l[7]};
-    };
-#pragma unroll
-    for (int i = 0; i < COLI_PREP_SLOTS; i++)
-        if (i % nchunk == chunk) convert(threadIdx.x + 256 * i, v[i]);
-    for (int i = COLI_PREP_SLOTS; 256 * i < nslot; i++) {
-        if (i % nchunk != chunk) continue;
-        const int slot = threadIdx.x + 256 * i;
-        float u[8];
-        load_slot(slot, u);
-        convert(slot, u);
-    }
-    // every block with a lo part raises the flag; once one has, the others
-    // see it and skip their atomic (thousands of blocks on one address
-    // serialize: 4096 rows took 53 us instead of 6)
-    if (__syncthreads_or(any) && threadIdx.x == 0 &&
-        __hip_atomic_load(haslo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gen)
-        atomicMax(haslo, gen);
-}
+__global__ __launch_bounds__(256) void coli_prep_frag(ColiPrepArgs a) { prep_frag_block(a, blockIdx.x); }
 
 // ---------------------------------------------------------------------------
 // GEMV problems
@@ -788,11 +703,14 @@ extern "C" hipError_t coli_launch_gemv(int kind, const ColiGemvArgs *a, int R, i
     }
 }
 
+// args_only: the launch's arguments are returned instead (the build then runs
+// inside another launch, prep_frag_block); nblocks 0 when there is nothing.
 extern "C" hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *src_row,
                                             const int *nrows_dev, int nrows, int K, int ngp,
                                             int int4_order, _Float16 *hi, _Float16 *lo,
                                             int *exp2out, int *haslo, int gen, const void *zero,
-                                            hipStream_t st) {
+                                            hipStream_t st, ColiPrepArgs *args_only) {
+    if (args_only) args_only->nblocks = 0;
     if (nrows <= 0) return hipSuccess;
     const int vec = ((uintptr_t)x % 16 == 0) && (ldx % 4 == 0) && (K % 8 == 0);
     // chunks per row: one per 256 slots (2048 columns), fewer when many rows
@@ -801,8 +719,28 @@ extern "C" hipError_t coli_launch_prep_frag(const float *x, int ldx, const int *
     const char *e = std::getenv("COLI_HIP_PREP_CHUNKS");
     if (e) nchunk = std::max(1, std::min(nchunk, std::atoi(e)));
     else if (nrows >= 64) nchunk = 1;
-    hipLaunchKernelGGL(coli_prep_frag, dim3((unsigned)(nrows * nchunk)), dim3(256), 0, st, x, ldx, src_row, nrows_dev,
-                       K, ngp, int4_order, hi, lo, exp2out, haslo, gen, vec, nchunk, (const float *)zero);
+    ColiPrepArgs a;
+    a.x = x;
+    a.src_row = src_row;
+    a.nrows_dev = nrows_dev;
+    a.hi = hi;
+    a.lo = lo;
+    a.exp2out = exp2out;
+    a.haslo = haslo;
+    a.zero = (const float *)zero;
+    a.ldx = ldx;
+    a.K = K;
+    a.ngp = ngp;
+    a.int4_order = int4_order;
+    a.gen = gen;
+    a.vec = vec;
+    a.nchunk = nchunk;
+    a.nblocks = nrows * nchunk;
+    if (args_only) {
+        *args_only = a;
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(coli_prep_frag, dim3((unsigned)a.nblocks), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

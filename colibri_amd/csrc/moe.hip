@@ -319,14 +319,23 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
                                                              ColiProb *__restrict__ pdual, ColiProb *__restrict__ pdown,
                                                              int *__restrict__ uniq, int *__restrict__ xrows,
                                                              int *__restrict__ slotrow, int *__restrict__ mt,
-                                                             int *__restrict__ state) {
+                                                             int *__restrict__ state, ColiPrepArgs prep) {
     extern __shared__ int sm[];
     __shared__ int s_last;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // MW: workgroups past the S selecting ones build the rows' activation
+    // fragments for the gate/up GEMV (independent of the selection)
+    if constexpr (MW) {
+        if ((int)blockIdx.x >= S) {
+            prep_frag_block(prep, (int)blockIdx.x - S);
+            return;
+        }
+    }
+    const int nsel = MW ? S : (int)gridDim.x;   // selecting workgroups
     // LDS: slots [S K] | keff [S] | selection weights [4 E] floats, then the union's (7 E + 5) ints
     int *sidx = sm, *skeff = sm + S * K, *work = skeff + S;
     // decode: the descriptor templates go to LDS while the selection runs
-    const bool small = S * K <= 64 && gridDim.x == 1;
+    const bool small = S * K <= 64 && nsel == 1;
     ColiProb *stab = (ColiProb *)(((uintptr_t)(work + moe_work_ints(E)) + 15) & ~(uintptr_t)15);
     if (small)
         for (int i = threadIdx.x; i < 2 * (E + 1); i += blockDim.x) stab[i] = tab[i];
@@ -343,13 +352,13 @@ __global__ __launch_bounds__(256) void coli_moe_select_union(const float *__rest
         select_row<JM, true, false>(part, nch, bias, S, E, K, mode, topp, norm_topk, routed_scale, idx, wsel, keff,
                                     (float *)work + (size_t)wave * E, blockIdx.x * 4 + wave, lane, sidx, skeff);
     }
-    if (gridDim.x > 1) {
+    if (nsel > 1) {
         // publish, count; only the last workgroup goes on
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0) {
             const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = old == (int)gridDim.x - 1;
+            s_last = old == nsel - 1;
             if (s_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
@@ -1096,7 +1105,13 @@ static int launch_route(ColiHipMoe *m, const float *x_dev, int S, hipStream_t st
     return hip_check(hipGetLastError(), "moe routing");
 }
 
-static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
+// prep: a fragment build run by extra workgroups of the four-wave selection
+// launch (nblocks 0: none; only passed when that launch is taken)
+static bool select_union_mw(const ColiHipMoeConfig &c) {
+    return c.route_mode != 0 && c.E > 64 && c.E <= 256 && c.K <= 16;
+}
+
+static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st, const ColiPrepArgs &prep) {
     const ColiHipMoeConfig &c = m->cfg;
     const size_t work = (size_t)moe_work_ints(c.E) * sizeof(int) + 16 + (size_t)2 * (c.E + 1) * sizeof(ColiProb);
     const size_t shm = (size_t)(S * c.K + S) * sizeof(int) + work;
@@ -1105,14 +1120,15 @@ static int launch_select_union(ColiHipMoe *m, int nch, int S, hipStream_t st) {
 #define COLI_SU(JM)                                                                                             \
     hipLaunchKernelGGL((coli_moe_select_union<JM>), grid, block, shm, st, m->logits, nch, m->rb, S, c.E, c.K,     \
                        c.route_mode, c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, m->route_cnt, \
-                       c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state)
-    if (c.route_mode != 0 && c.E > 64 && c.E <= 256 && c.K <= 16) {
+                       c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state,  \
+                       prep)
+    if (select_union_mw(c)) {
         // one row per workgroup, selected by its four waves (DSV3's 256
-        // experts: S = 1 selection 8.0 -> 6.5 us)
-        hipLaunchKernelGGL((coli_moe_select_union<4, true>), dim3((unsigned)S), block, shm, st, m->logits, nch, m->rb, S,
-                           c.E, c.K,
-                           c.route_mode, c.topp, c.norm_topk, c.routed_scale, m->idx, m->wsel, m->keff, m->route_cnt,
-                           c.has_shared, m->tab, m->pdual, m->pdown, m->uniq, m->xrows, m->slotrow, m->mt, m->state);
+        // experts: S = 1 selection 8.0 -> 6.5 us), and the fragment build
+        hipLaunchKernelGGL((coli_moe_select_union<4, true>), dim3((unsigned)(S + prep.nblocks)), block, shm, st,
+                           m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp, c.norm_topk, c.routed_scale,
+                           m->idx, m->wsel, m->keff, m->route_cnt, c.has_shared, m->tab, m->pdual, m->pdown, m->uniq,
+                           m->xrows, m->slotrow, m->mt, m->state, prep);
         return hip_check(hipGetLastError(), "moe selection + union");
     }
     switch (jm) {
@@ -1153,6 +1169,13 @@ static bool launch_dual1(ColiHipMoe *m, hipStream_t st, const float *x, int nrt,
 #undef COLI_D1_KIND
 #undef COLI_D1
     return false;
+}
+
+// COLI_HIP_PREP_BESIDE=0: the rows' activation fragments keep their own
+// launch instead of running beside the four-wave selection.
+static bool prep_beside_enabled() {
+    const char *e = std::getenv("COLI_HIP_PREP_BESIDE");
+    return !(e && e[0] == '0');
 }
 
 // COLI_HIP_SHARED_OVERLAP=0: the shared expert's gate/up stays in the gate/up
@@ -1300,9 +1323,14 @@ static int moe_forward_impl(ColiHipMoe *m, DevCtx *ctx, const float *x_dev, floa
             !hip_check(hipGetLastError(), "moe selection + union + shared gate/up"))
             return 0;
     } else if (S <= 64 && !fused_route_disabled()) {
-        // 2. router partials, 3-4. selection and union in one launch
+        // 2. router partials, 3-4. selection and union in one launch (with
+        // the four-wave selection, the rows' fragments built beside it)
         const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
-        if (!nch || !launch_select_union(m, nch, S, st)) return 0;
+        ColiPrepArgs prep;
+        prep.nblocks = 0;
+        if (S > 1 && !mx && select_union_mw(c) && prep_beside_enabled() && !flush_frags_args(ctx, fx, &prep))
+            return 0;
+        if (!nch || !launch_select_union(m, nch, S, st, prep)) return 0;
     } else {
         const int nch = router_logits(ctx, x_dev, S, m->rw, c.D, c.E, m->logits);
         if (!nch || !hip_check(coli_launch_router_select(m->logits, nch, m->rb, S, c.E, c.K, c.route_mode, c.topp,
