@@ -275,6 +275,93 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
     }
 }
 
+// Two row blocks of one problem in one wave's loop (CH = 2): iterations
+// 0 .. nit-1 stream block 0's quads (result in acc0), nit .. 2 nit-1 block
+// 1's (result in acc1, zero on entry), through the same ring, so block 1's first weights are requested while
+// block 0's last quads are computed (one descriptor read, one ring fill and
+// one pipeline drain for both). The activations of the two blocks are the
+// same quads.
+template <int KIND, int R>
+__device__ __forceinline__ void load_weights2(Stage<KIND, R, true> &sg, bool valid, bool second, int q,
+                                              const TileRows<KIND, R> &rows0, const TileRows<KIND, R> &rows1,
+                                              const void *zero, int lane) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint8_t *wb = second ? rows1.w[r] : rows0.w[r];
+        const uint8_t *sb = second ? rows1.s[r] : rows0.s[r];
+        const int qs = second ? rows1.qstep[r] : rows0.qstep[r];
+        const int qq = valid ? q * qs : 0;
+        const uint8_t *w = valid ? wb : (const uint8_t *)zero;
+        const uint8_t *sp = valid ? sb : (const uint8_t *)zero;
+        sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + (size_t)qq * COLI_TILE_BYTES) + lane);
+        sg.sc[r].load(sp, (size_t)qq, lane & 15);
+    }
+}
+
+template <int KIND, int R, int NB4, int W, bool LO>
+__device__ __forceinline__ void gemv_quads2(floatx4 (&acc0)[R], floatx4 (&acc1)[R],
+                                            Stage<KIND, R, true> (&st)[COLI_PD], int q_first, int Q1,
+                                            const TileRows<KIND, R> &rows0, const TileRows<KIND, R> &rows1,
+                                            const uint8_t *xh, const uint8_t *xl, uint32_t xoff, const void *zero,
+                                            int lane) {
+    constexpr int PD = COLI_PD;
+    if (q_first >= Q1) return;
+    const int nit = (Q1 - q_first + W - 1) / W, NIT = 2 * nit;
+    const int q_last = q_first + (nit - 1) * W;
+    auto load_x = [&](Stage<KIND, R, true> &sg, int q) {
+        const uint8_t *qh = xh + (size_t)q * 256, *ql = xl + (size_t)q * 256;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            sg.xh[j] = *GPTR(half8v, qh + xoff + j * 64);
+            if constexpr (LO) sg.xl[j] = *GPTR(half8v, ql + xoff + j * 64);
+        }
+    };
+    auto load = [&](Stage<KIND, R, true> &sg, int it) {
+        const bool valid = it < NIT, second = it >= nit;
+        const int q = q_first + (second ? it - nit : it) * W;
+        load_weights2<KIND, R>(sg, valid, second, q, rows0, rows1, zero, lane);
+        load_x(sg, valid ? q : q_last);
+    };
+    auto compute = [&](const Stage<KIND, R, true> &sg, floatx4 (&acc)[R]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                half8v bw = unpack_b<KIND>(sg.w[r][j]);
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg.xh[j], bw, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if constexpr (LO) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(sg.xl[j], bw, d, 0, 0, 0);
+                const float scl = sg.sc[r].get(j);
+#pragma unroll
+                for (int i = 0; i < NB4; i++) acc[r][i] = fmaf(d[i], scl, acc[r][i]);
+            }
+        }
+    };
+    if constexpr (LO) {
+        const uint8_t *ql = xl + (size_t)q_first * 256;
+#pragma unroll
+        for (int j = 0; j < 4; j++) st[0].xl[j] = *GPTR(half8v, ql + xoff + j * 64);
+    }
+#pragma unroll
+    for (int p = 1; p < PD - 1; p++) load(st[p], p);
+    // one accumulator set in the loop: block 0's is moved out when its last
+    // quad is done
+    for (int it0 = 0; it0 < NIT; it0 += PD) {
+#pragma unroll
+        for (int u = 0; u < PD; u++) {
+            load(st[(u + PD - 1) % PD], it0 + u + PD - 1);
+            const int it = it0 + u;
+            if (it < NIT) compute(st[u], acc1);
+            if (it == nit - 1) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    acc0[r] = acc1[r];
+                    acc1[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    }
+}
+
 // One workgroup (W waves) = one work item: (problem, batch tile, row block,
 // K split). The W waves interleave over the item's quads (wave w takes quads
 // Q0+w, Q0+w+W, ...) so the group streams contiguous tile memory together,
@@ -297,8 +384,11 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
 // B16 460 -> 444 us, 21-row verification 603 -> 564 us, four waves). The
 // plain (down) matrices keep two waves without spills (DSV3 B8 282 -> 274 us,
 // B16 454 -> 440 us against three); int4 spills more and keeps two.
-template <int KIND, int R, bool DUAL, int NB4, int W, bool INL>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W <= 4 && !INL && DUAL ? 3 : 1, 8))) void coli_gemv_tiles(ColiGemvArgs a) {
+// CH = 2 (device descriptors, plain matrices, no K split): each workgroup
+// runs two consecutive row blocks of its problem back to back in one loop.
+template <int KIND, int R, bool DUAL, int NB4, int W, bool INL, int CH = 1>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W <= 4 && !INL && DUAL ? 3 : (CH == 2 ? 2 : 1), 8))) void coli_gemv_tiles(ColiGemvArgs a) {
+    static_assert(CH == 1 || (CH == 2 && !INL && !DUAL), "chained row blocks: device descriptors, plain matrices");
     constexpr int RT = DUAL ? R / 2 : R;
     __shared__ float red[W][R * NB4][64];
     __shared__ int split_last;
@@ -315,7 +405,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         bt = blockIdx.z;
     } else {
         const int item = blockIdx.x;
-        const int items_per_bt = a.rb_per_prob * a.splits;
+        const int items_per_bt = CH == 2 ? (a.rb_per_prob + 1) / 2 : a.rb_per_prob * a.splits;
         const int items_per_p = a.n_bt * items_per_bt;
         p = item / items_per_p;
         if (p >= a.nprob) return;
@@ -326,8 +416,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         int rem = item - p * items_per_p;
         bt = rem / items_per_bt;
         rem -= bt * items_per_bt;
-        rb = rem / a.splits;
-        s = rem - rb * a.splits;
+        if constexpr (CH == 2) {
+            rb = 2 * rem;
+            s = 0;
+        } else {
+            rb = rem / a.splits;
+            s = rem - rb * a.splits;
+        }
     }
     const ColiProb pr = uniform_prob(INL ? a.prob0 : pdesc);
     const int nb = min(16, pr.nrows - 16 * bt);
@@ -355,6 +450,21 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         rows.w[r] = live[r] ? wl : (const uint8_t *)a.zero;
         rows.s[r] = live[r] ? sl : (const uint8_t *)a.zero;
         rows.qstep[r] = live[r] ? 1 : 0;
+    }
+    // CH = 2: the second row block (rb + 1; dead past the matrix)
+    int rt1[R];
+    bool live1[R];
+    TileRows<KIND, R> rows1;
+    if constexpr (CH == 2) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            rt1[r] = (rb + 1) * R + r;
+            live1[r] = rt1[r] < a.nrt;
+            const size_t t0 = (size_t)(uint32_t)min(rt1[r], a.nrt - 1) * (uint32_t)a.nq;
+            rows1.w[r] = live1[r] ? pr.w0 + t0 * COLI_TILE_BYTES : (const uint8_t *)a.zero;
+            rows1.s[r] = live1[r] ? (const uint8_t *)pr.s0 + t0 * ScaleRegs<KIND>::kTileBytes : (const uint8_t *)a.zero;
+            rows1.qstep[r] = live1[r] ? 1 : 0;
+        }
     }
     // the first weight stage goes out before anything else is resolved
     Stage<KIND, R, true> st[COLI_PD];
@@ -399,6 +509,29 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
     for (int r = 0; r < R; r++) acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
     // the peeled loop fits two waves per SIMD only in these variants
     constexpr bool PEEL = INL && W == 8 && KIND == COLI_KIND_I4_H && R >= 2;
+    // reduction in fixed wave order and the epilogue of one row block (the
+    // chained form, CH = 2: no K split)
+    auto finish_block = [&](const floatx4 (&ac)[R], const int (&rtb)[R], const bool (&liveb)[R]) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < NB4; i++) red[wave][r * NB4 + i][lane] = ac[r][i];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int ii = wave + k * W;
+            if (ii >= NB4) break;
+            float vv[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float t = red[0][r * NB4 + ii][lane];
+#pragma unroll
+                for (int w = 1; w < W; w++) t += red[w][r * NB4 + ii][lane];
+                vv[r] = t;
+            }
+            gemv_epilogue<R, DUAL>(a, pr, bt, rtb, liveb, vv, ks * 4 + ii, lane, E_out[k]);
+        }
+    };
     if constexpr (INL && !DUAL) {
         if (gx) {
             // emitted fragments are f32 rows: their lo parts are always taken
@@ -409,6 +542,18 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         } else {
             gemv_quads<KIND, R, NB4, W, false, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
         }
+    } else if constexpr (CH == 2) {
+        floatx4 acc1[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc1[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        if (use_lo)
+            gemv_quads2<KIND, R, NB4, W, true>(acc, acc1, st, q_first, Q1, rows, rows1, xh, xl, xoff, a.zero, lane);
+        else
+            gemv_quads2<KIND, R, NB4, W, false>(acc, acc1, st, q_first, Q1, rows, rows1, xh, xl, xoff, a.zero, lane);
+        finish_block(acc, rt, live);
+        __syncthreads();   // the reduction buffer is reused
+        finish_block(acc1, rt1, live1);
+        return;
     } else {
         if (use_lo) gemv_quads<KIND, R, NB4, W, true, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
         else gemv_quads<KIND, R, NB4, W, false, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
@@ -640,6 +785,15 @@ struct ColiGemvPlan {
     int R, dual, nb4;
 };
 
+// Plain matrices on device descriptors with two-wave groups (the MoE down
+// projections) run two row blocks per workgroup (DSV3 B16 layer 430.7 ->
+// 424.8 us, 21-row step 550.6 -> 538.4 us MXFP4, 655.7 -> 635.9 us int4);
+// COLI_HIP_CHAIN=0: one.
+static bool chain_enabled() {
+    const char *e = std::getenv("COLI_HIP_CHAIN");
+    return !(e && e[0] == '0');
+}
+
 // 16-wave groups only for R <= 2: at R = 4 the 128-VGPR budget of a
 // 1024-thread group would spill.
 template <int KIND, int R, bool DUAL, int NB4>
@@ -656,6 +810,15 @@ static hipError_t launch_w(const ColiGemvArgs &a, int W, int blocks, hipStream_t
     // two waves: on device descriptors and without a K split only (the
     // split protocol has each wave finish one result register)
     if (W == 2 && !inl && a.splits == 1) {
+        if constexpr (!DUAL && R == 4) {
+            if (chain_enabled()) {
+                // two row blocks a workgroup
+                const long pairs = (long)a.nprob * a.n_bt * ((a.rb_per_prob + 1) / 2);
+                hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 2, false, 2>), dim3((unsigned)pairs),
+                                   dim3(128), 0, st, a);
+                return hipGetLastError();
+            }
+        }
         hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 2, false>), grid, dim3(128), 0, st, a);
         return hipGetLastError();
     }

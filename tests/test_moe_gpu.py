@@ -371,6 +371,42 @@ def test_moe_layer_deepseek_v4(session, fmt, S, shared, limit):
     assert rel_err(out, ref, mag).max() <= TOL
 
 
+# The down projections on two-wave groups run two row blocks per workgroup in
+# one loop (the second block's first weights requested while the first
+# block's last quads are computed): bitwise equal to one row block per
+# workgroup (COLI_HIP_CHAIN=0), and to the oracle's tolerance. Plan pinned to
+# two waves (the planner's choice at full size), a shared expert, int4 and
+# MXFP4, hidden sizes whose row blocks pair up and one that leaves the last
+# block alone (D = 320: five blocks of 64 rows; its pair reads the zero tile).
+@pytest.mark.parametrize("fmt,S,D", [(7, 16, 512), (4, 21, 512), (4, 5, 320), (7, 3, 640)])
+def test_moe_chained_row_blocks_bitwise(session, monkeypatch, fmt, S, D):
+    monkeypatch.setenv("COLI_HIP_PLAN", "4,2,1")
+    rng = np.random.default_rng(900 + fmt + S + D)
+    I, E, K, mode = 256, 32, 4, 2
+    layer = Layer(rng, fmt, D, I, E, shared=True)
+    x, W, b = make_router_inputs(rng, S, D, E, K, mode, bias=True)
+    m, hs = make_moe(session, layer, W, b, K, mode)
+    outs = []
+    try:
+        for chain in ("1", "0", "1"):
+            monkeypatch.setenv("COLI_HIP_CHAIN", chain)
+            out = np.zeros((S, D), np.float32)
+            idx = np.zeros((S, K), np.int32)
+            w = np.zeros((S, K), np.float32)
+            keff = np.zeros(S, np.int32)
+            assert session.b.hip_moe_forward(m, f32p(x), f32p(out), S, i32p(idx), f32p(w), i32p(keff))
+            outs.append(out)
+    finally:
+        session.b.hip_moe_free(m)
+        for h in hs:
+            for t in h:
+                session.free(t)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+    _, _, _, ref, mag = moe_reference(layer, x, W, b, K, mode)
+    assert rel_err(outs[0], ref, mag).max() <= TOL
+
+
 # Decode routing in one launch (router partials, selection and union; the
 # last workgroup to arrive selects) against the three separate launches:
 # bitwise equal outputs, slots and weights, over several calls in a row (the
