@@ -275,38 +275,23 @@ __device__ __forceinline__ void gemv_quads(floatx4 (&acc)[R], Stage<KIND, R, tru
     }
 }
 
-// Two row blocks of one problem in one wave's loop (CH = 2): iterations
-// 0 .. nit-1 stream block 0's quads (result in acc0), nit .. 2 nit-1 block
-// 1's (result in acc1, zero on entry), through the same ring, so block 1's first weights are requested while
-// block 0's last quads are computed (one descriptor read, one ring fill and
-// one pipeline drain for both). The activations of the two blocks are the
-// same quads.
-template <int KIND, int R>
-__device__ __forceinline__ void load_weights2(Stage<KIND, R, true> &sg, bool valid, bool second, int q,
-                                              const TileRows<KIND, R> &rows0, const TileRows<KIND, R> &rows1,
-                                              const void *zero, int lane) {
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint8_t *wb = second ? rows1.w[r] : rows0.w[r];
-        const uint8_t *sb = second ? rows1.s[r] : rows0.s[r];
-        const int qs = second ? rows1.qstep[r] : rows0.qstep[r];
-        const int qq = valid ? q * qs : 0;
-        const uint8_t *w = valid ? wb : (const uint8_t *)zero;
-        const uint8_t *sp = valid ? sb : (const uint8_t *)zero;
-        sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + (size_t)qq * COLI_TILE_BYTES) + lane);
-        sg.sc[r].load(sp, (size_t)qq, lane & 15);
-    }
-}
-
-template <int KIND, int R, int NB4, int W, bool LO>
-__device__ __forceinline__ void gemv_quads2(floatx4 (&acc0)[R], floatx4 (&acc1)[R],
-                                            Stage<KIND, R, true> (&st)[COLI_PD], int q_first, int Q1,
-                                            const TileRows<KIND, R> &rows0, const TileRows<KIND, R> &rows1,
-                                            const uint8_t *xh, const uint8_t *xl, uint32_t xoff, const void *zero,
-                                            int lane) {
+// CH consecutive row blocks of one problem in one wave's loop (CH = 2, 4):
+// iterations b nit .. (b + 1) nit - 1 stream block b's quads through the same
+// ring, so each block's first weights are requested while the previous
+// block's last quads are computed (one descriptor read, one ring fill and one
+// pipeline drain for all of them). Block b's row tiles are (rb + b) R + r,
+// their addresses formed per load (dead past the matrix: the zero tile). The
+// activations of the blocks are the same quads. One accumulator set runs in
+// the loop; each finished block's is shifted into `done` (blocks 0 .. CH-2 in
+// order), the last block's stays in acc.
+template <int KIND, int R, int NB4, int W, bool LO, int CH>
+__device__ __forceinline__ void gemv_quads_ch(floatx4 (&acc)[R], floatx4 (&done)[CH - 1][R],
+                                             Stage<KIND, R, true> (&st)[COLI_PD], int q_first, int Q1,
+                                             const ColiProb &pr, int rb, int nrt, int nq, const uint8_t *xh,
+                                             const uint8_t *xl, uint32_t xoff, const void *zero, int lane) {
     constexpr int PD = COLI_PD;
     if (q_first >= Q1) return;
-    const int nit = (Q1 - q_first + W - 1) / W, NIT = 2 * nit;
+    const int nit = (Q1 - q_first + W - 1) / W, NIT = CH * nit;
     const int q_last = q_first + (nit - 1) * W;
     auto load_x = [&](Stage<KIND, R, true> &sg, int q) {
         const uint8_t *qh = xh + (size_t)q * 256, *ql = xl + (size_t)q * 256;
@@ -317,12 +302,24 @@ __device__ __forceinline__ void gemv_quads2(floatx4 (&acc0)[R], floatx4 (&acc1)[
         }
     };
     auto load = [&](Stage<KIND, R, true> &sg, int it) {
-        const bool valid = it < NIT, second = it >= nit;
-        const int q = q_first + (second ? it - nit : it) * W;
-        load_weights2<KIND, R>(sg, valid, second, q, rows0, rows1, zero, lane);
+        int blk = 0;
+#pragma unroll
+        for (int k = 1; k < CH; k++) blk += it >= k * nit ? 1 : 0;
+        const bool valid = it < NIT;
+        const int q = q_first + (it - blk * nit) * W;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int rt = (rb + blk) * R + r;
+            const bool live = valid && rt < nrt;
+            const size_t tq = live ? (size_t)(uint32_t)rt * (uint32_t)nq + q : 0;
+            const uint8_t *w = live ? pr.w0 : (const uint8_t *)zero;
+            const uint8_t *sp = live ? (const uint8_t *)pr.s0 : (const uint8_t *)zero;
+            sg.w[r] = __builtin_nontemporal_load(GPTR(u32x4, w + tq * COLI_TILE_BYTES) + lane);
+            sg.sc[r].load(sp, tq, lane & 15);
+        }
         load_x(sg, valid ? q : q_last);
     };
-    auto compute = [&](const Stage<KIND, R, true> &sg, floatx4 (&acc)[R]) {
+    auto compute = [&](const Stage<KIND, R, true> &sg) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
 #pragma unroll
@@ -343,19 +340,21 @@ __device__ __forceinline__ void gemv_quads2(floatx4 (&acc0)[R], floatx4 (&acc1)[
     }
 #pragma unroll
     for (int p = 1; p < PD - 1; p++) load(st[p], p);
-    // one accumulator set in the loop: block 0's is moved out when its last
-    // quad is done
     for (int it0 = 0; it0 < NIT; it0 += PD) {
 #pragma unroll
         for (int u = 0; u < PD; u++) {
             load(st[(u + PD - 1) % PD], it0 + u + PD - 1);
             const int it = it0 + u;
-            if (it < NIT) compute(st[u], acc1);
-            if (it == nit - 1) {
+            if (it < NIT) compute(st[u]);
+            if (it + 1 < NIT && (it + 1) % nit == 0) {
+#pragma unroll
+                for (int b = 0; b + 1 < CH - 1; b++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) done[b][r] = done[b + 1][r];
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    acc0[r] = acc1[r];
-                    acc1[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+                    done[CH - 2][r] = acc[r];
+                    acc[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
                 }
             }
         }
@@ -384,11 +383,11 @@ __device__ __forceinline__ void gemv_quads2(floatx4 (&acc0)[R], floatx4 (&acc1)[
 // B16 460 -> 444 us, 21-row verification 603 -> 564 us, four waves). The
 // plain (down) matrices keep two waves without spills (DSV3 B8 282 -> 274 us,
 // B16 454 -> 440 us against three); int4 spills more and keeps two.
-// CH = 2 (device descriptors, plain matrices, no K split): each workgroup
-// runs two consecutive row blocks of its problem back to back in one loop.
+// CH > 1 (device descriptors, plain matrices, no K split): each workgroup
+// runs CH consecutive row blocks of its problem back to back in one loop.
 template <int KIND, int R, bool DUAL, int NB4, int W, bool INL, int CH = 1>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W <= 4 && !INL && DUAL ? 3 : (CH == 2 ? 2 : 1), 8))) void coli_gemv_tiles(ColiGemvArgs a) {
-    static_assert(CH == 1 || (CH == 2 && !INL && !DUAL), "chained row blocks: device descriptors, plain matrices");
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == COLI_KIND_FP4 && W <= 4 && !INL && DUAL ? 3 : (CH > 1 ? 2 : 1), 8))) void coli_gemv_tiles(ColiGemvArgs a) {
+    static_assert(CH == 1 || (!INL && !DUAL), "chained row blocks: device descriptors, plain matrices");
     constexpr int RT = DUAL ? R / 2 : R;
     __shared__ float red[W][R * NB4][64];
     __shared__ int split_last;
@@ -405,7 +404,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         bt = blockIdx.z;
     } else {
         const int item = blockIdx.x;
-        const int items_per_bt = CH == 2 ? (a.rb_per_prob + 1) / 2 : a.rb_per_prob * a.splits;
+        const int items_per_bt = CH > 1 ? (a.rb_per_prob + CH - 1) / CH : a.rb_per_prob * a.splits;
         const int items_per_p = a.n_bt * items_per_bt;
         p = item / items_per_p;
         if (p >= a.nprob) return;
@@ -416,8 +415,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         int rem = item - p * items_per_p;
         bt = rem / items_per_bt;
         rem -= bt * items_per_bt;
-        if constexpr (CH == 2) {
-            rb = 2 * rem;
+        if constexpr (CH > 1) {
+            rb = CH * rem;
             s = 0;
         } else {
             rb = rem / a.splits;
@@ -450,21 +449,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         rows.w[r] = live[r] ? wl : (const uint8_t *)a.zero;
         rows.s[r] = live[r] ? sl : (const uint8_t *)a.zero;
         rows.qstep[r] = live[r] ? 1 : 0;
-    }
-    // CH = 2: the second row block (rb + 1; dead past the matrix)
-    int rt1[R];
-    bool live1[R];
-    TileRows<KIND, R> rows1;
-    if constexpr (CH == 2) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            rt1[r] = (rb + 1) * R + r;
-            live1[r] = rt1[r] < a.nrt;
-            const size_t t0 = (size_t)(uint32_t)min(rt1[r], a.nrt - 1) * (uint32_t)a.nq;
-            rows1.w[r] = live1[r] ? pr.w0 + t0 * COLI_TILE_BYTES : (const uint8_t *)a.zero;
-            rows1.s[r] = live1[r] ? (const uint8_t *)pr.s0 + t0 * ScaleRegs<KIND>::kTileBytes : (const uint8_t *)a.zero;
-            rows1.qstep[r] = live1[r] ? 1 : 0;
-        }
     }
     // the first weight stage goes out before anything else is resolved
     Stage<KIND, R, true> st[COLI_PD];
@@ -510,7 +494,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
     // the peeled loop fits two waves per SIMD only in these variants
     constexpr bool PEEL = INL && W == 8 && KIND == COLI_KIND_I4_H && R >= 2;
     // reduction in fixed wave order and the epilogue of one row block (the
-    // chained form, CH = 2: no K split)
+    // chained form, CH > 1: no K split)
     auto finish_block = [&](const floatx4 (&ac)[R], const int (&rtb)[R], const bool (&liveb)[R]) {
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -542,17 +526,31 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(KIND == 
         } else {
             gemv_quads<KIND, R, NB4, W, false, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
         }
-    } else if constexpr (CH == 2) {
-        floatx4 acc1[R];
+    } else if constexpr (CH > 1) {
+        floatx4 done[CH - 1][R];
 #pragma unroll
-        for (int r = 0; r < R; r++) acc1[r] = (floatx4){0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < CH - 1; b++)
+#pragma unroll
+            for (int r = 0; r < R; r++) done[b][r] = (floatx4){0.f, 0.f, 0.f, 0.f};
         if (use_lo)
-            gemv_quads2<KIND, R, NB4, W, true>(acc, acc1, st, q_first, Q1, rows, rows1, xh, xl, xoff, a.zero, lane);
+            gemv_quads_ch<KIND, R, NB4, W, true, CH>(acc, done, st, q_first, Q1, pr, rb, a.nrt, a.nq, xh, xl, xoff,
+                                                     a.zero, lane);
         else
-            gemv_quads2<KIND, R, NB4, W, false>(acc, acc1, st, q_first, Q1, rows, rows1, xh, xl, xoff, a.zero, lane);
-        finish_block(acc, rt, live);
-        __syncthreads();   // the reduction buffer is reused
-        finish_block(acc1, rt1, live1);
+            gemv_quads_ch<KIND, R, NB4, W, false, CH>(acc, done, st, q_first, Q1, pr, rb, a.nrt, a.nq, xh, xl, xoff,
+                                                      a.zero, lane);
+#pragma unroll
+        for (int b = 0; b < CH; b++) {
+            int rtb[R];
+            bool liveb[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                rtb[r] = (rb + b) * R + r;
+                liveb[r] = rtb[r] < a.nrt;
+            }
+            if (b > 0) __syncthreads();   // the reduction buffer is reused
+            if (b < CH - 1) finish_block(done[b], rtb, liveb);
+            else finish_block(acc, rtb, liveb);
+        }
         return;
     } else {
         if (use_lo) gemv_quads<KIND, R, NB4, W, true, PEEL>(acc, st, q_first, Q1, rows, xh, xl, xoff, a.zero, lane);
@@ -787,11 +785,12 @@ struct ColiGemvPlan {
 
 // Plain matrices on device descriptors with two-wave groups (the MoE down
 // projections) run two row blocks per workgroup (DSV3 B16 layer 430.7 ->
-// 424.8 us, 21-row step 550.6 -> 538.4 us MXFP4, 655.7 -> 635.9 us int4);
+// 424.8 us, 21-row step 550.6 -> 538.4 us MXFP4, 655.7 -> 635.9 us int4;
+// four blocks spilled registers and were slower: B16 464 us);
 // COLI_HIP_CHAIN=0: one.
-static bool chain_enabled() {
+static int chain_blocks() {
     const char *e = std::getenv("COLI_HIP_CHAIN");
-    return !(e && e[0] == '0');
+    return e && e[0] == '0' ? 1 : 2;
 }
 
 // 16-wave groups only for R <= 2: at R = 4 the 128-VGPR budget of a
@@ -811,10 +810,10 @@ static hipError_t launch_w(const ColiGemvArgs &a, int W, int blocks, hipStream_t
     // split protocol has each wave finish one result register)
     if (W == 2 && !inl && a.splits == 1) {
         if constexpr (!DUAL && R == 4) {
-            if (chain_enabled()) {
-                // two row blocks a workgroup
-                const long pairs = (long)a.nprob * a.n_bt * ((a.rb_per_prob + 1) / 2);
-                hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 2, false, 2>), dim3((unsigned)pairs),
+            const int ch = chain_blocks();
+            if (ch > 1) {
+                const long groups = (long)a.nprob * a.n_bt * ((a.rb_per_prob + ch - 1) / ch);
+                hipLaunchKernelGGL((coli_gemv_tiles<KIND, R, DUAL, NB4, 2, false, 2>), dim3((unsigned)groups),
                                    dim3(128), 0, st, a);
                 return hipGetLastError();
             }

@@ -371,10 +371,10 @@ def test_moe_layer_deepseek_v4(session, fmt, S, shared, limit):
     assert rel_err(out, ref, mag).max() <= TOL
 
 
-# The down projections on two-wave groups run two row blocks per workgroup in
-# one loop (the second block's first weights requested while the first
-# block's last quads are computed): bitwise equal to one row block per
-# workgroup (COLI_HIP_CHAIN=0), and to the oracle's tolerance. Plan pinned to
+# The down projections on two-wave groups run two row blocks per
+# workgroup in one loop (each block's first weights requested while the
+# previous block's last quads are computed): bitwise equal to one row block
+# per workgroup (COLI_HIP_CHAIN=0), and to the oracle's tolerance. Plan pinned to
 # two waves (the planner's choice at full size), a shared expert, int4 and
 # MXFP4, hidden sizes whose row blocks pair up and one that leaves the last
 # block alone (D = 320: five blocks of 64 rows; its pair reads the zero tile).
