@@ -19,6 +19,34 @@
 //  * the selection kernel adds the chunks in chunk order while it reads them.
 // ---------------------------------------------------------------------------
 #define COLI_ROUTER_CHUNK 512
+// Sum of each of the SMAX per-row values over the 64 lanes, in the order of
+// the butterfly v += shfl_xor(v, 32), then 16, 8, 4, 2, 1 (so bitwise that
+// butterfly's result), as a reduce-scatter: at each of the first log2(SMAX)
+// steps a lane keeps half of its rows and adds its partner's copy of them, so
+// the steps exchange SMAX/2 + SMAX/4 + ... + 1 values instead of SMAX each.
+// Row (lane >> (6 - log2 SMAX)) ends in the lanes of its group; store(row, v)
+// runs on the group's first lane.
+template <int SMAX, typename F>
+__device__ __forceinline__ void reduce_rows64(float (&v)[SMAX], int lane, F &&store) {
+    constexpr int LG = SMAX >= 32 ? 5 : SMAX >= 16 ? 4 : SMAX >= 8 ? 3 : SMAX >= 4 ? 2 : SMAX >= 2 ? 1 : 0;
+    static_assert((1 << LG) == SMAX && SMAX <= 32, "a power of two up to 32 rows");
+#pragma unroll
+    for (int k = 0; k < LG; k++) {
+        const int o = 32 >> k, n = SMAX >> k, h = n / 2;
+        const bool up = (lane & o) != 0;
+#pragma unroll
+        for (int i = 0; i < h; i++) {
+            const float send = up ? v[i] : v[i + h];
+            const float keep = up ? v[i + h] : v[i];
+            v[i] = keep + __shfl_xor(send, o);
+        }
+    }
+    float t = v[0];
+#pragma unroll
+    for (int o = 32 >> LG; o; o >>= 1) t += __shfl_xor(t, o);
+    if ((lane & ((64 >> LG) - 1)) == 0) store(lane >> (6 - LG), t);
+}
+
 // One wave's partial logits of expert e over column chunk ch, rows 0..S-1
 // (S <= SMAX). ATOMIC: stored as agent-scope atomics, for a reader on
 // another XCD inside the same launch.
@@ -56,19 +84,13 @@ __device__ __forceinline__ void router_partial_wave(const float *__restrict__ x,
             }
         }
     }
-#pragma unroll
-    for (int s = 0; s < SMAX; s++) {
+    reduce_rows64<SMAX>(acc, lane, [&](int s, float v) {
         if (s < S) {
-            float v = acc[s];
-#pragma unroll
-            for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0) {
-                float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
-                if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else *dst = v;
-            }
+            float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
+            if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else *dst = v;
         }
-    }
+    });
 }
 
 
@@ -219,19 +241,13 @@ __device__ __forceinline__ void router_partial_block(const float *__restrict__ x
             acc[s] += fmaf(xv[3], wv[step][3], a);
         }
     }
-#pragma unroll
-    for (int s = 0; s < SMAX; s++) {
+    reduce_rows64<SMAX>(acc, lane, [&](int s, float v) {
         if (s < S) {
-            float v = acc[s];
-#pragma unroll
-            for (int off = 32; off; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0) {
-                float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
-                if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else *dst = v;
-            }
+            float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
+            if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else *dst = v;
         }
-    }
+    });
 }
 
 // The end of one row's selection, once lane kk < want holds the expert of
