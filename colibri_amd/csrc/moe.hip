@@ -553,10 +553,13 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1(con
         const float *hr = h + (size_t)pr.xrow_off * (NQ * 128) + 8 * ks + 2 * (r16 & 3) + 32 * (r16 >> 2);
         const size_t t0 = (size_t)rb * NQ;
         const uint8_t *wt = pr.w0 + t0 * COLI_TILE_BYTES;
-        // h first, then every weight quad of the tile: all in flight at once.
-        // (Two scalar loads, which the compiler pairs: the elements of one
-        // vector load broadcast by DPP were folded into one broadcast by this
-        // toolchain, a wrong result.)
+        // h first, then the weight quads of the tile (the compiler spreads
+        // the later quads' requests over the first quads' products, which
+        // keeps the wave at ~66 VGPRs: every workgroup of the launch is
+        // resident at once; a barrier forcing all requests first measured
+        // the same). (Two scalar loads for h, which the compiler pairs: the
+        // elements of one vector load broadcast by DPP were folded into one
+        // broadcast by this toolchain, a wrong result.)
         float xq[NQ][2];
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
