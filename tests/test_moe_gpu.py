@@ -412,11 +412,12 @@ def test_moe_chained_row_blocks_bitwise(session, monkeypatch, fmt, S, D):
 # bitwise equal outputs, slots and weights, over several calls in a row (the
 # arrival counter resets itself) and several column chunks. Above 64 experts
 # the selection + union launch selects each row with four waves (64 experts
-# each, merged by wave 0), the separate selection with one; the TOPP cases
-# cut rows below K slots (checked).
+# each, merged by wave 0), the separate selection with one, and from two rows
+# on the rows' fragment build runs beside it (40 and 64 rows: the grouped
+# GEMM reads them); the TOPP cases cut rows below K slots (checked).
 @pytest.mark.parametrize("mode,S,E,topp", [(0, 1, 64, 0.0), (1, 4, 32, 0.0), (2, 7, 256, 0.0), (3, 16, 128, 0.0),
                                          (2, 16, 256, 0.0), (1, 1, 256, 0.0), (2, 1, 256, 0.0), (3, 1, 200, 0.0),
-                                         (1, 3, 256, 0.5), (2, 5, 200, 0.6)])
+                                         (1, 3, 256, 0.5), (2, 5, 200, 0.6), (2, 40, 256, 0.0), (3, 64, 128, 0.0)])
 def test_moe_fused_routing_bitwise(session, monkeypatch, mode, S, E, topp):
     rng = np.random.default_rng(500 + mode * 7 + S + E)
     D, I, K = 1536, 256, 8 if E >= 64 else 4
