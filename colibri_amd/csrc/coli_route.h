@@ -197,18 +197,23 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 // (every wave reading them from L2 cost four times the traffic). The router
 // weights are requested before the staging. D % 4 == 0. All 256 threads of
 // the workgroup call it (it synchronizes).
-template <int SMAX, bool ATOMIC>
+template <int SMAX, bool ATOMIC, int EPW = 1>
 __device__ __forceinline__ void router_partial_block(const float *__restrict__ x, int S, const float *__restrict__ W,
                                                      int D, int E, float *__restrict__ part, size_t chstride,
-                                                     int e, int ch, int lane, floatx4 (*xs)[COLI_ROUTER_CHUNK / 4]) {
+                                                     int e0, int ch, int lane, floatx4 (*xs)[COLI_ROUTER_CHUNK / 4]) {
+    // EPW experts per wave (e0, e0 + 1, ...): each activation read from LDS
+    // feeds EPW products; the arithmetic of each expert is unchanged
     constexpr int NV = COLI_ROUTER_CHUNK / 4;   // float4 per row chunk
     const int d0 = ch * COLI_ROUTER_CHUNK;
-    floatx4 wv[COLI_ROUTER_CHUNK / 256];
+    floatx4 wv[EPW][COLI_ROUTER_CHUNK / 256];
 #pragma unroll
-    for (int step = 0; step < COLI_ROUTER_CHUNK / 256; step++) {
-        const int d = d0 + step * 256 + lane * 4;
-        wv[step] = (e < E && d < D) ? *(const floatx4 *)(W + (size_t)e * D + d) : (floatx4){0.f, 0.f, 0.f, 0.f};
-    }
+    for (int x_ = 0; x_ < EPW; x_++)
+#pragma unroll
+        for (int step = 0; step < COLI_ROUTER_CHUNK / 256; step++) {
+            const int d = d0 + step * 256 + lane * 4, e = e0 + x_;
+            wv[x_][step] = (e < E && d < D) ? *(const floatx4 *)(W + (size_t)e * D + d)
+                                             : (floatx4){0.f, 0.f, 0.f, 0.f};
+        }
     // the rows' chunk (SMAX x NV float4) staged by the 256 threads: every load
     // issued before any is waited for (one memory round trip)
     constexpr int PER = (SMAX * NV + 255) / 256;
@@ -226,28 +231,38 @@ __device__ __forceinline__ void router_partial_block(const float *__restrict__ x
         if (v < SMAX * NV) xs[v / NV][v % NV] = xv[u];
     }
     __syncthreads();
-    if (e >= E) return;
-    float acc[SMAX];
+    if (e0 >= E) return;
+    float acc[EPW][SMAX];
 #pragma unroll
-    for (int s = 0; s < SMAX; s++) acc[s] = 0.0f;
+    for (int x_ = 0; x_ < EPW; x_++)
+#pragma unroll
+        for (int s = 0; s < SMAX; s++) acc[x_][s] = 0.0f;
 #pragma unroll
     for (int step = 0; step < COLI_ROUTER_CHUNK / 256; step++) {
 #pragma unroll
         for (int s = 0; s < SMAX; s++) {
             const floatx4 xv = xs[s][step * 64 + lane];
-            float a = xv[0] * wv[step][0];
-            a = fmaf(xv[1], wv[step][1], a);
-            a = fmaf(xv[2], wv[step][2], a);
-            acc[s] += fmaf(xv[3], wv[step][3], a);
+#pragma unroll
+            for (int x_ = 0; x_ < EPW; x_++) {
+                float a = xv[0] * wv[x_][step][0];
+                a = fmaf(xv[1], wv[x_][step][1], a);
+                a = fmaf(xv[2], wv[x_][step][2], a);
+                acc[x_][s] += fmaf(xv[3], wv[x_][step][3], a);
+            }
         }
     }
-    reduce_rows64<SMAX>(acc, lane, [&](int s, float v) {
-        if (s < S) {
-            float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
-            if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else *dst = v;
-        }
-    });
+#pragma unroll
+    for (int x_ = 0; x_ < EPW; x_++) {
+        const int e = e0 + x_;
+        if (e >= E) break;
+        reduce_rows64<SMAX>(acc[x_], lane, [&](int s, float v) {
+            if (s < S) {
+                float *dst = part + (size_t)ch * chstride + (size_t)s * E + e;
+                if constexpr (ATOMIC) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else *dst = v;
+            }
+        });
+    }
 }
 
 // The end of one row's selection, once lane kk < want holds the expert of

@@ -62,6 +62,16 @@ __global__ void coli_sum_slots(float *dst, const float *slots, int n, int D) {
 
 #include "coli_route.h"
 
+// Experts per wave of the staged router partials at 5-16 rows: two, so each
+// activation read from LDS feeds two products and a workgroup stages the rows'
+// chunk for eight experts (DSV3 B16 layer 416.8 -> 413.7 us, 21-row step
+// 535.5 -> 528.1 us; four: 415.2 / 530.8 us). COLI_ROUTER_EPW16 overrides it
+// at build time (tuning).
+#ifndef COLI_ROUTER_EPW16
+#define COLI_ROUTER_EPW16 2
+#endif
+#define COLI_ROUTER_EPW(SMAX) ((SMAX) >= 16 ? COLI_ROUTER_EPW16 : 1)
+
 template <int SMAX>
 __global__ __launch_bounds__(256) void coli_router_partial(const float *__restrict__ x, int S,
                                                            const float *__restrict__ W, int D, int E,
@@ -72,8 +82,9 @@ __global__ __launch_bounds__(256) void coli_router_partial(const float *__restri
     if constexpr (SMAX > 1) {
         if ((D & 3) == 0) {
             __shared__ floatx4 xs[SMAX][COLI_ROUTER_CHUNK / 4];
-            router_partial_block<SMAX, false>(x, S, W, D, E, part, chstride, blockIdx.x * 4 + wave, blockIdx.y, lane,
-                                              xs);
+            constexpr int EPW = COLI_ROUTER_EPW(SMAX);
+            router_partial_block<SMAX, false, EPW>(x, S, W, D, E, part, chstride, (blockIdx.x * 4 + wave) * EPW,
+                                                   blockIdx.y, lane, xs);
             return;
         }
     }
@@ -189,11 +200,13 @@ extern "C" hipError_t coli_launch_router_logits(const float *x, int S, const flo
                                                 float *part, hipStream_t st) {
     const int nch = coli_router_chunks(D);
     const size_t chstride = (size_t)S * E;
-    const dim3 grid((E + 3) / 4, nch);
+    const bool vec = (D & 3) == 0;   // the staged form (several experts a wave) needs aligned rows
     for (int s0 = 0; s0 < S; s0 += 16) {   // 16 rows of accumulators per pass
         const int n = S - s0 < 16 ? S - s0 : 16;
         const float *xs = x + (size_t)s0 * D;
         float *ps = part + (size_t)s0 * E;
+        const int epw = n == 1 || !vec ? 1 : (n <= 4 ? COLI_ROUTER_EPW(4) : COLI_ROUTER_EPW(16));
+        const dim3 grid((E + 4 * epw - 1) / (4 * epw), nch);
         if (n == 1)
             hipLaunchKernelGGL((coli_router_partial<1>), grid, dim3(256), 0, st, xs, n, W, D, E, ps, chstride);
         else if (n <= 4)
