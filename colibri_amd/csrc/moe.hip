@@ -508,6 +508,32 @@ __device__ __forceinline__ float row_bcast(float v) {
 }
 template <int KIND, int J>
 __device__ __forceinline__ float dc_group_dpp(uint32_t wd, const ScaleRegs<KIND> &sc, const float (&xr)[2]) {
+    if constexpr (KIND == COLI_KIND_FP4) {
+        // the broadcast folded into the products: one v_fmac_f32 with a DPP
+        // source per product, in the order of dc_group (p = x_i * w_i + p,
+        // bitwise fmaf(w_i, x_i, p)); the leading s_nop keeps the DPP read
+        // of xr two wait states after any VALU write to it
+        typedef float float2v __attribute__((ext_vector_type(2)));
+        const float s = sc.get(J);
+        const float2v w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 0);
+        const float2v w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 1);
+        const float2v w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 2);
+        const float2v w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(wd, s, 3);
+        float p = 0.0f;
+        asm("s_nop 1\n\t"
+            "v_fmac_f32_dpp %0, %1, %3 row_newbcast:%11 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+            "v_fmac_f32_dpp %0, %2, %4 row_newbcast:%11 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+            "v_fmac_f32_dpp %0, %1, %5 row_newbcast:%12 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+            "v_fmac_f32_dpp %0, %2, %6 row_newbcast:%12 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+            "v_fmac_f32_dpp %0, %1, %7 row_newbcast:%13 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+            "v_fmac_f32_dpp %0, %2, %8 row_newbcast:%13 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+            "v_fmac_f32_dpp %0, %1, %9 row_newbcast:%14 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+            "v_fmac_f32_dpp %0, %2, %10 row_newbcast:%14 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+            : "+v"(p)
+            : "v"(xr[0]), "v"(xr[1]), "v"(w0[0]), "v"(w0[1]), "v"(w1[0]), "v"(w1[1]), "v"(w2[0]), "v"(w2[1]),
+              "v"(w3[0]), "v"(w3[1]), "n"(4 * J), "n"(4 * J + 1), "n"(4 * J + 2), "n"(4 * J + 3));
+        return p;
+    }
     float x[8];
     x[0] = row_bcast<4 * J + 0>(xr[0]);
     x[1] = row_bcast<4 * J + 0>(xr[1]);
