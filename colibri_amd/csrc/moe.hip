@@ -27,6 +27,7 @@
 #include "coli_hip_ext.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -774,24 +775,40 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1m(co
 // and wave 0 applies SwiGLU and writes the tile's 16 values of h.
 // ---------------------------------------------------------------------------
 // The token's row of x: each wave loads its share (quads w, w + W, ...) into
-// registers first, before anything else is requested.
-template <int W, int NQW>
-__device__ __forceinline__ void dual1_load_x(const float *__restrict__ x, floatx4 (&xv)[NQW / 2 + 1], int wave,
-                                             int lane) {
-    constexpr int XF4 = W * NQW * 32;   // float4s in the row
+// registers first, before anything else is requested. MXFP4 keeps them there
+// (two activations a lane and quad, taken by the products through DPP row
+// broadcasts); int4 stages the row in LDS.
+template <int KIND, int NQW>
+struct Dual1X {
+    floatx4 v[NQW / 2 + 1];   // LDS form: the wave's share of the row
+    float q[NQW][2];          // register form: lane (ks, r)'s two activations of each quad
+};
+template <int KIND, int W, int NQW>
+__device__ __forceinline__ void dual1_load_x(const float *__restrict__ x, Dual1X<KIND, NQW> &xv, int wave, int lane) {
+    if constexpr (KIND == COLI_KIND_FP4) {
 #pragma unroll
-    for (int k = 0; k < NQW / 2 + 1; k++) {
-        const int i = (wave + W * k) * 64 + lane;
-        xv[k] = i < XF4 ? *GPTR(floatx4, x + (size_t)i * 4) : (floatx4){0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < NQW; i++) {
+            const float *p = x + (size_t)(wave + W * i) * 128 + 32 * ((lane & 15) >> 2) + 8 * (lane >> 4) +
+                             2 * (lane & 3);
+            xv.q[i][0] = p[0];
+            xv.q[i][1] = p[1];
+        }
+    } else {
+        constexpr int XF4 = W * NQW * 32;   // float4s in the row
+#pragma unroll
+        for (int k = 0; k < NQW / 2 + 1; k++) {
+            const int i = (wave + W * k) * 64 + lane;
+            xv.v[k] = i < XF4 ? *GPTR(floatx4, x + (size_t)i * 4) : (floatx4){0.f, 0.f, 0.f, 0.f};
+        }
     }
 }
 
 // Gate/up of row tile rt of problem pr for the row whose share each wave
-// holds in xv: every weight quad of the wave's share requested at once, x
-// moved into LDS (a bare barrier: the weight loads in flight are not
+// holds in xv: every weight quad of the wave's share requested at once, (int4)
+// x moved into LDS (a bare barrier: the weight loads in flight are not
 // drained), f32 dots, the waves' sums in fixed order, SwiGLU by wave 0.
 template <int KIND, int W, int NQW>
-__device__ __forceinline__ void dual1_tile(const ColiProb &pr, int rt, const floatx4 (&xv)[NQW / 2 + 1],
+__device__ __forceinline__ void dual1_tile(const ColiProb &pr, int rt, const Dual1X<KIND, NQW> &xv,
                                            float *__restrict__ xs, float (&red)[W][2][16], float *__restrict__ h,
                                            int I, float swiglu_limit, int wave, int lane) {
     constexpr int NQ = W * NQW;   // the row's 128-column quads (D = NQ x 128)
@@ -808,24 +825,39 @@ __device__ __forceinline__ void dual1_tile(const ColiProb &pr, int rt, const flo
         sg[i].load(pr.s0, t0 + q, r16);
         su[i].load(pr.s1, t0 + q, r16);
     }
-#pragma unroll
-    for (int k = 0; k < NQW / 2 + 1; k++) {
-        const int i = (wave + W * k) * 64 + lane;
-        if (i < XF4) *(floatx4 *)(xs + (size_t)i * 4) = xv[k];
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
     float ag = 0.0f, au = 0.0f;
+    if constexpr (KIND == COLI_KIND_FP4) {
+        auto group = [&](auto jt, int i) {
+            constexpr int J = decltype(jt)::value;
+            ag += dc_group_dpp<KIND, J>(wg[i][J], sg[i], xv.q[i]);
+            au += dc_group_dpp<KIND, J>(wu[i][J], su[i], xv.q[i]);
+        };
 #pragma unroll
-    for (int i = 0; i < NQW; i++) {
+        for (int i = 0; i < NQW; i++) {
+            group(std::integral_constant<int, 0>{}, i);
+            group(std::integral_constant<int, 1>{}, i);
+            group(std::integral_constant<int, 2>{}, i);
+            group(std::integral_constant<int, 3>{}, i);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NQW / 2 + 1; k++) {
+            const int i = (wave + W * k) * 64 + lane;
+            if (i < XF4) *(floatx4 *)(xs + (size_t)i * 4) = xv.v[k];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        const int q = wave + W * i;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float *xp = xs + 32 * (4 * q + j) + 8 * ks;
-            ag += dc_group<KIND>(wg[i][j], sg[i], j, xp);
-            au += dc_group<KIND>(wu[i][j], su[i], j, xp);
+        for (int i = 0; i < NQW; i++) {
+            asm volatile("" ::: "memory");
+            const int q = wave + W * i;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float *xp = xs + 32 * (4 * q + j) + 8 * ks;
+                ag += dc_group<KIND>(wg[i][j], sg[i], j, xp);
+                au += dc_group<KIND>(wu[i][j], su[i], j, xp);
+            }
         }
     }
     ag += __shfl_xor(ag, 16);
@@ -865,8 +897,8 @@ __global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restr
     const ColiProb pd = pdual[p];
     if (p >= np) return;
     const ColiProb pr = uniform_prob(pd);
-    floatx4 xv[NQW / 2 + 1];
-    dual1_load_x<W, NQW>(x, xv, wave, lane);
+    Dual1X<KIND, NQW> xv;
+    dual1_load_x<KIND, W, NQW>(x, xv, wave, lane);
     dual1_tile<KIND, W, NQW>(pr, rt, xv, xs, red, h, I, swiglu_limit, wave, lane);
 }
 
@@ -891,8 +923,8 @@ __global__ __launch_bounds__(64 * W) void coli_moe_select_union_sh(
     if (blockIdx.x > 0) {
         __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
         __shared__ float red[W][2][16];
-        floatx4 xv[NQW / 2 + 1];
-        dual1_load_x<W, NQW>(x, xv, wave, lane);
+        Dual1X<KIND, NQW> xv;
+        dual1_load_x<KIND, W, NQW>(x, xv, wave, lane);
         ColiProb pr = uniform_prob(tab[2 * E]);
         pr.nrows = 1;
         pr.xrow_off = 0;
@@ -943,8 +975,8 @@ __global__ __launch_bounds__(64 * W) void coli_moe_route_dual1(
     ColiProb *stab = (ColiProb *)(dsm + (((size_t)E * sizeof(float) + 15) & ~(size_t)15));
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
-    floatx4 xv[NQW / 2 + 1];
-    dual1_load_x<W, NQW>(x, xv, wave, lane);
+    Dual1X<KIND, NQW> xv;
+    dual1_load_x<KIND, W, NQW>(x, xv, wave, lane);
     for (int i = threadIdx.x; i < 2 * (E + 1); i += 64 * W) stab[i] = tab[i];
     const bool first = blockIdx.x == 0;
     if (wave == 0)
