@@ -777,11 +777,14 @@ __global__ __launch_bounds__(64 * COLI_DC_WAVES) void coli_moe_down_combine1m(co
 // The token's row of x: each wave loads its share (quads w, w + W, ...) into
 // registers first, before anything else is requested. MXFP4 keeps them there
 // (two activations a lane and quad, taken by the products through DPP row
-// broadcasts); int4 stages the row in LDS.
+// broadcasts: f32 VALU dots); int4 converts them into fp16 hi / lo fragments
+// for the matrix cores.
+// 8-column chunks of a wave's share per lane (int4 matrix-core form)
+#define COLI_D1_NCL(NQW) (((NQW) * 16 + 63) / 64)
 template <int KIND, int NQW>
 struct Dual1X {
-    floatx4 v[NQW / 2 + 1];   // LDS form: the wave's share of the row
-    float q[NQW][2];          // register form: lane (ks, r)'s two activations of each quad
+    float q[NQW][2];                       // MXFP4: lane (ks, r)'s two activations of each quad
+    floatx4 m[2 * COLI_D1_NCL(NQW)];       // int4: chunks lane + 64 c of the wave's quads
 };
 template <int KIND, int W, int NQW>
 __device__ __forceinline__ void dual1_load_x(const float *__restrict__ x, Dual1X<KIND, NQW> &xv, int wave, int lane) {
@@ -794,25 +797,27 @@ __device__ __forceinline__ void dual1_load_x(const float *__restrict__ x, Dual1X
             xv.q[i][1] = p[1];
         }
     } else {
-        constexpr int XF4 = W * NQW * 32;   // float4s in the row
 #pragma unroll
-        for (int k = 0; k < NQW / 2 + 1; k++) {
-            const int i = (wave + W * k) * 64 + lane;
-            xv.v[k] = i < XF4 ? *GPTR(floatx4, x + (size_t)i * 4) : (floatx4){0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < COLI_D1_NCL(NQW); c++) {
+            const int ch = c * 64 + lane, i = ch >> 4;
+            const float *p = x + (size_t)(wave + W * i) * 128 + (ch & 15) * 8;
+            xv.m[2 * c] = ch < NQW * 16 ? *GPTR(floatx4, p) : (floatx4){0.f, 0.f, 0.f, 0.f};
+            xv.m[2 * c + 1] = ch < NQW * 16 ? *GPTR(floatx4, p + 4) : (floatx4){0.f, 0.f, 0.f, 0.f};
         }
     }
 }
+// LDS floats of the row staging of a dual1 workgroup
+#define COLI_D1_XS(W, NQW) ((W) * COLI_D1_NCL(NQW) * 512)
 
 // Gate/up of row tile rt of problem pr for the row whose share each wave
-// holds in xv: every weight quad of the wave's share requested at once, (int4)
-// x moved into LDS (a bare barrier: the weight loads in flight are not
-// drained), f32 dots, the waves' sums in fixed order, SwiGLU by wave 0.
+// holds in xv: every weight quad of the wave's share requested at once, the
+// dots (MXFP4: f32 VALU with DPP sources; int4: on the matrix cores),
+// the waves' sums in fixed order, SwiGLU by wave 0.
 template <int KIND, int W, int NQW>
 __device__ __forceinline__ void dual1_tile(const ColiProb &pr, int rt, const Dual1X<KIND, NQW> &xv,
                                            float *__restrict__ xs, float (&red)[W][2][16], float *__restrict__ h,
                                            int I, float swiglu_limit, int wave, int lane) {
     constexpr int NQ = W * NQW;   // the row's 128-column quads (D = NQ x 128)
-    constexpr int XF4 = NQ * 32;
     const int ks = lane >> 4, r16 = lane & 15;
     const size_t t0 = (size_t)rt * NQ;
     u32x4 wg[NQW], wu[NQW];
@@ -840,33 +845,48 @@ __device__ __forceinline__ void dual1_tile(const ColiProb &pr, int rt, const Dua
             group(std::integral_constant<int, 3>{}, i);
         }
     } else {
-#pragma unroll
-        for (int k = 0; k < NQW / 2 + 1; k++) {
-            const int i = (wave + W * k) * 64 + lane;
-            if (i < XF4) *(floatx4 *)(xs + (size_t)i * 4) = xv.v[k];
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
+        // int4 on the matrix cores: the wave's quads of x as fp16 hi / lo
+        // fragments with one exponent for the wave (its LDS region, read back
+        // by the wave only), the token's row in every row of the A operand;
+        // lane l ends with output row l % 16 of each group's product, scaled
+        // by the group scale and summed per group position
+        constexpr int NCL = COLI_D1_NCL(NQW), NC = NCL * 512;
+        _Float16 *hs = (_Float16 *)xs + (size_t)wave * (2 * NC);
+        int E;
+        const bool lo = row_to_frags<true, NCL>(xv.m, hs, NC, lane, &E);
+        float g4[4] = {0.f, 0.f, 0.f, 0.f}, u4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < NQW; i++) {
-            asm volatile("" ::: "memory");
-            const int q = wave + W * i;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float *xp = xs + 32 * (4 * q + j) + 8 * ks;
-                ag += dc_group<KIND>(wg[i][j], sg[i], j, xp);
-                au += dc_group<KIND>(wu[i][j], su[i], j, xp);
+                const int col = 128 * i + 32 * j + 8 * ks;
+                const half8v xh = *(const half8v *)(hs + col);
+                const half8v bg = unpack_b<KIND>(wg[i][j]), bu = unpack_b<KIND>(wu[i][j]);
+                floatx4 dg = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bg, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                floatx4 du = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bu, (floatx4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                if (lo) {
+                    const half8v xl = *(const half8v *)(hs + NC + col);
+                    dg = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bg, dg, 0, 0, 0);
+                    du = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bu, du, 0, 0, 0);
+                }
+                g4[j] = fmaf(dg[0], sg[i].get(j), g4[j]);
+                u4[j] = fmaf(du[0], su[i].get(j), u4[j]);
             }
         }
+        if (lane < 16) {
+            red[wave][0][lane] = ldexpf((g4[0] + g4[1]) + (g4[2] + g4[3]), E);
+            red[wave][1][lane] = ldexpf((u4[0] + u4[1]) + (u4[2] + u4[3]), E);
+        }
     }
-    ag += __shfl_xor(ag, 16);
-    ag += __shfl_xor(ag, 32);
-    au += __shfl_xor(au, 16);
-    au += __shfl_xor(au, 32);
-    if (lane < 16) {
-        red[wave][0][lane] = ag;
-        red[wave][1][lane] = au;
+    if constexpr (KIND == COLI_KIND_FP4) {
+        ag += __shfl_xor(ag, 16);
+        ag += __shfl_xor(ag, 32);
+        au += __shfl_xor(au, 16);
+        au += __shfl_xor(au, 32);
+        if (lane < 16) {
+            red[wave][0][lane] = ag;
+            red[wave][1][lane] = au;
+        }
     }
     __syncthreads();
     if (wave == 0 && lane < 16) {
@@ -886,7 +906,7 @@ __global__ __launch_bounds__(64 * W) void coli_moe_dual1(const ColiProb *__restr
                                                          const int *__restrict__ state, const float *__restrict__ x,
                                                          int D, int nrt, float *__restrict__ h, int I,
                                                          float swiglu_limit, int routed_only) {
-    __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
+    __shared__ __attribute__((aligned(16))) float xs[COLI_D1_XS(W, NQW)];
     __shared__ float red[W][2][16];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = blockIdx.x / nrt, rt = blockIdx.x - p * nrt;
@@ -921,7 +941,7 @@ __global__ __launch_bounds__(64 * W) void coli_moe_select_union_sh(
     int *__restrict__ state, const float *__restrict__ x, float *__restrict__ h, int I, float swiglu_limit) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (blockIdx.x > 0) {
-        __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
+        __shared__ __attribute__((aligned(16))) float xs[COLI_D1_XS(W, NQW)];
         __shared__ float red[W][2][16];
         Dual1X<KIND, NQW> xv;
         dual1_load_x<KIND, W, NQW>(x, xv, wave, lane);
@@ -967,7 +987,7 @@ __global__ __launch_bounds__(64 * W) void coli_moe_route_dual1(
     int *__restrict__ uniq, int *__restrict__ xrows, int *__restrict__ slotrow, int *__restrict__ mt,
     int *__restrict__ state, const float *__restrict__ x, int nrt, float *__restrict__ h, int I, float swiglu_limit) {
     extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
-    __shared__ __attribute__((aligned(16))) float xs[W * NQW * 128];
+    __shared__ __attribute__((aligned(16))) float xs[COLI_D1_XS(W, NQW)];
     __shared__ float red[W][2][16];
     __shared__ int sidx[64], skeff[1];
     // dynamic LDS: the selection's E floats, then the 2 (E + 1) descriptor templates
