@@ -62,9 +62,9 @@ def fp16_scales(rng, O, ng):
 
 
 def cpu_baseline(secs):
-    """The reference's CPU path on this host (OpenMP over
-    the physical cores, OMP_PROC_BIND=close, set in main() before any OpenMP
-    library loads): the dense int4 step of configs[1] (`value`), plus an
+    """The reference's CPU path on this host (as the reference publishes its
+    CPU numbers: OpenMP over the physical cores, OMP_PROC_BIND=close, set in
+    main() before any OpenMP library loads): the dense int4 step of configs[1] (`value`), plus an
     MXFP4 expert GEMV leg (configs[2] shapes) and an OLMoE-shaped MoE layer
     leg (configs[0], the reference's kernels composed in the order of
     c/olmoe.c:645-697). It runs in a child process of its own that never
@@ -640,8 +640,8 @@ CPU_INFO = {}
 
 
 def main():
-    # The CPU baseline's OpenMP runs on the physical cores, bound close
-    # set before any OpenMP library is loaded. An
+    # The CPU baseline's OpenMP runs on the physical cores, bound close (the
+    # reference's published CPU setup): set before any OpenMP library is loaded. An
     # OMP_NUM_THREADS already in the environment (the host's CPU share) caps it.
     model, phys, logical = cpu_topology()
     threads = min(phys, int(os.environ.get("OMP_NUM_THREADS", phys)))
@@ -673,7 +673,7 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the expert path has no collectives; "
-                                   "run with --gpus 1 (see DESIGN.md for how it would shard)"}))
+                                   "run with --gpus 1 (expert parallelism across GPUs is not built here)"}))
         sys.exit(2)
     # the CPU baseline first, in a child process, before this process loads
     # the GPU runtime (and so before any GPU work that host load could disturb)
